@@ -1,0 +1,170 @@
+"""fronk_amd: MI355X-native expert neuron-slice backend for Fronk.
+
+Python is test and benchmark plumbing over the C ABI of libfronk_hip.so
+(include/fronk_hip.h); the compute path is HIP. Importing works without a GPU;
+every call that needs the library raises if libfronk_hip.so was not built.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import build as _build
+
+OK, INVALID, STATE, NUMERIC, IO, UNSUPPORTED = 0, -1, -2, -3, -4, -5
+FMT_LEGACY, FMT_NATIVE, FMT_Q4KT, FMT_Q8, FMT_MXFP4 = 0, 1, 2, 3, 4
+MODE_F32, MODE_F64, MODE_Q8 = 0, 1, 2
+Q4_0, Q8_0, Q4_K, MXFP4 = 2, 8, 12, 39
+MAX_BURST, MAX_HIDDEN, BLOCKS = 8, 4096, 20
+
+LIB_PATH = _build.HIP_LIB
+
+
+class Request(C.Structure):
+    _fields_ = [("layer", C.c_uint), ("burst", C.c_uint), ("hidden", C.c_uint), ("mode", C.c_uint),
+                ("expert", C.POINTER(C.c_uint16)), ("gate", C.POINTER(C.c_float)),
+                ("x", C.POINTER(C.c_float))]
+
+
+class Sample(C.Structure):
+    _fields_ = [("runs", C.c_uint64), ("weight_bytes", C.c_uint64), ("hot_allocations", C.c_uint64),
+                ("blocks", C.c_uint), ("unique_experts", C.c_uint), ("pairs", C.c_uint), ("grid", C.c_uint),
+                ("last_kernel_ns", C.c_double)]
+
+
+# Every symbol include/fronk_hip.h declares, with its ctypes signature.
+SIGNATURES = {
+    "fr_hip_open": (C.c_int, [C.c_int]),
+    "fr_hip_close": (C.c_int, []),
+    "fr_hip_probe": (C.c_int, [C.c_int, C.c_char_p, C.c_size_t]),
+    "fr_hip_upload": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint64, C.c_uint, C.c_uint]),
+    "fr_hip_reserve": (C.c_int, [C.c_uint, C.c_uint, C.c_uint]),
+    "fr_hip_refresh": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.c_uint]),
+    "fr_hip_release": (C.c_int, [C.c_uint]),
+    "fr_hip_unit_bytes": (C.c_uint64, [C.c_uint, C.c_uint]),
+    "fr_hip_run": (C.c_int, [C.POINTER(Request), C.POINTER(C.c_float)]),
+    "fr_hip_plan_bytes": (C.c_size_t, [C.c_uint, C.c_uint]),
+    "fr_hip_plan": (C.c_int, [C.POINTER(Request), C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t),
+                              C.POINTER(C.c_uint)]),
+    "fr_hip_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "fr_hip_last_output": (C.c_int, [C.c_void_p, C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_uint)]),
+    "fr_hip_sample_get": (C.c_int, [C.POINTER(Sample)]),
+    "fr_hip_debug_dequant": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
+    "fr_hip_debug_dequant_down": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
+    "fr_hip_debug_quantize": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.POINTER(C.c_float)]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded libfronk_hip.so. Raises if it was not built: there is no
+    fallback path."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() (hipcc, gfx950)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def fptr(a):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def check(rc, what):
+    if rc != OK:
+        raise RuntimeError(f"{what} failed with {rc}")
+
+
+def unit_bytes(hidden, fmt):
+    return lib().fr_hip_unit_bytes(hidden, fmt)
+
+
+def make_request(layer, experts, gates, x, mode=MODE_F32):
+    """Build a Request over numpy arrays; returns (request, keepalive)."""
+    experts = np.ascontiguousarray(experts, np.uint16).reshape(-1, 10)
+    gates = np.ascontiguousarray(gates, np.float32).reshape(-1, 11)
+    x = np.ascontiguousarray(x, np.float32)
+    burst, hidden = x.shape
+    req = Request(layer, burst, hidden, mode, experts.ctypes.data_as(C.POINTER(C.c_uint16)),
+                  fptr(gates), fptr(x))
+    return req, (experts, gates, x)
+
+
+class Engine:
+    """Thin owner of the process-wide device engine (one GPU)."""
+
+    def __init__(self, device=0):
+        self.device = device
+        check(lib().fr_hip_open(device), "fr_hip_open")
+
+    def close(self):
+        return lib().fr_hip_close()
+
+    def upload(self, block, unit, hidden, fmt):
+        unit = np.asarray(unit)
+        return lib().fr_hip_upload(block, unit.ctypes.data, unit.nbytes, hidden, fmt)
+
+    def reserve(self, block, hidden, fmt):
+        return lib().fr_hip_reserve(block, hidden, fmt)
+
+    def load_sparse(self, block, unit, hidden, fmt, slices):
+        """Reserve a zeroed device unit and copy only the (layer, expert) slices
+        listed: equivalent to a full upload of a sparse unit."""
+        rc = self.reserve(block, hidden, fmt)
+        if rc != OK:
+            return rc
+        for layer, expert in slices:
+            rc = self.refresh(block, unit, layer, expert)
+            if rc != OK:
+                return rc
+        return OK
+
+    def refresh(self, block, unit, layer, expert):
+        return lib().fr_hip_refresh(block, np.asarray(unit).ctypes.data, layer, expert)
+
+    def release(self, block):
+        return lib().fr_hip_release(block)
+
+    def run(self, layer, experts, gates, x, mode=MODE_F32):
+        req, keep = make_request(layer, experts, gates, x, mode)
+        y = np.zeros((req.burst, req.hidden), np.float32)
+        rc = lib().fr_hip_run(C.byref(req), fptr(y))
+        return rc, y
+
+    def plan(self, layer, experts, gates, x, mode=MODE_F32):
+        req, keep = make_request(layer, experts, gates, x, mode)
+        cap = lib().fr_hip_plan_bytes(req.burst, req.hidden)
+        buf = np.zeros(cap, np.uint8)
+        used, grid = C.c_size_t(), C.c_uint()
+        rc = lib().fr_hip_plan(C.byref(req), buf.ctypes.data, cap, C.byref(used), C.byref(grid))
+        check(rc, "fr_hip_plan")
+        return buf[:used.value].copy(), grid.value
+
+    def sample(self):
+        s = Sample()
+        lib().fr_hip_sample_get(C.byref(s))
+        return s
+
+    def dequant(self, typ, row, n):
+        out = np.zeros(n, np.float32)
+        rc = lib().fr_hip_debug_dequant(typ, np.ascontiguousarray(row, np.uint8).ctypes.data, n, fptr(out))
+        return rc, out
+
+    def dequant_down(self, fmt, down, hidden):
+        out = np.zeros((hidden, 32), np.float32)
+        rc = lib().fr_hip_debug_dequant_down(fmt, np.ascontiguousarray(down, np.uint8).ctypes.data, hidden,
+                                             fptr(out))
+        return rc, out
+
+    def quantize(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        rc = lib().fr_hip_debug_quantize(fptr(x), x.size, fptr(out))
+        return rc, out

@@ -1,0 +1,1633 @@
+// fronk_hip.hip - MI355X (gfx950) expert neuron-slice engine behind a C ABI.
+//
+// One run() of the reference backend contract (src/backend.h:63) is ONE
+// kernel launch covering every (expert, owned 32-neuron slice) pair of a
+// layer request. The launch is a list of workgroup tasks, dispatched in
+// block-index order:
+//
+//   phase A  (pair, 8 neurons): the pair's gate and up rows are streamed
+//            once from HBM, dequantized in registers and dotted with the
+//            activation staged in LDS, one wavefront per row; a DPP/shuffle
+//            tree reduces each row; h = SiLU(a)*u goes to a small device
+//            buffer and a per-pair counter is released.
+//   phase B  (group of pairs, 256 output dims): waits (bounded) until every
+//            pair of its group has all 32 h values, then streams the down
+//            weights of the group and accumulates gate*W_down*h for its 256
+//            output dims in fp64; the group partial goes to scratch.
+//   reduce   the last phase-B task of each 256-dim range (atomic ticket)
+//            sums the group partials in a fixed order and writes y.
+//
+// No fp32 atomics touch y: the result is bit-reproducible run to run and a
+// token's bits do not depend on which other tokens share the burst beyond
+// fp64 summation order. Reference semantics: backends/ref.c:57-98.
+#include <hip/hip_runtime.h>
+
+#include <float.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "fronk_hip.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kNeurons = 32;
+constexpr int kMaxBurst = 8;
+constexpr int kBlocks = 20;
+constexpr int kLayers = 48;
+constexpr int kRouted = 512;
+constexpr int kShared = 512;
+constexpr int kMaxUnique = kMaxBurst * 10 + 1;
+constexpr int kMaxPairs = kMaxUnique * kBlocks;
+constexpr int kCols = 256;            // output dims per phase-B task
+constexpr int kMaxHidden = 4096;
+constexpr int kMaxRanges = kMaxHidden / kCols;
+constexpr int kLdsLimit = 64 * 1024;
+constexpr uint32_t kSpinLimit = 1u << 21;
+
+// Status bits of the output word.
+constexpr uint32_t kErrScale = 1;     // referenced non-finite scale
+constexpr uint32_t kErrRange = 2;     // a, u, h or y outside fp32
+constexpr uint32_t kErrTimeout = 4;   // dependency wait exceeded its bound
+
+enum : uint8_t { TQ4_0 = 2, TQ8_0 = 8, TQ4_K = 12, TMXFP4 = 39, TQ4_KT = 140 };
+enum { MODE_F32 = 0, MODE_F64 = 1, MODE_Q8 = 2 };
+
+struct PairDesc {            // one (expert, block) slice of the request
+  uint64_t slice;            // device address of the re-tiled slice
+  uint32_t proj;             // bytes of the 32 gate rows (= up offset)
+  uint8_t gu, dn, tmask, pad;
+  float gate[kMaxBurst];     // per-token expert weight (0 when not routed)
+};
+static_assert(sizeof(PairDesc) == 48, "pair layout");
+
+struct GroupDesc {
+  uint16_t first, count;
+  uint8_t dn, pad[3];
+};
+static_assert(sizeof(GroupDesc) == 8, "group layout");
+
+struct PlanHeader {
+  uint32_t hidden, burst, mode, npairs;
+  uint32_t ngroups, nranges, ntA, ntB;
+  uint32_t nn, tchunk, pairs_off, groups_off;
+  uint32_t x_off, total, gmax, lds;
+};
+static_assert(sizeof(PlanHeader) == 64, "header layout");
+
+struct Scratch {
+  uint32_t* done;            // [2][kMaxPairs] phase-A completions per pair
+  uint32_t* fin;             // [2][kMaxRanges] phase-B completions per range
+  float* hbuf;               // [kMaxPairs][8][32]
+  double* partial;           // [groups][burst][hidden]
+  uint32_t* out;             // [2][out_words]: status, pad x3, y
+  uint32_t out_words;
+  uint32_t parity;
+};
+
+// ------------------------------------------------------------ scalars
+
+__device__ __forceinline__ float half_to_float(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+__device__ __forceinline__ bool half_bad(uint32_t bits) { return (bits & 0x7c00u) == 0x7c00u; }
+
+// 2^(e-127) for an E8M0 exponent 0..254; e = 0 is the subnormal 2^-127.
+__device__ __forceinline__ float e8m0(uint32_t e) {
+  return __uint_as_float(e ? e << 23 : 0x00400000u);
+}
+// OCP E2M1 code -> float {0,.5,1,1.5,2,3,4,6} with sign; code 8 is +0 as in
+// the reference table (src/native.c:9).
+__device__ __forceinline__ float e2m1(uint32_t c) {
+  uint32_t e = (c >> 1) & 3u, m = c & 1u;
+  uint32_t mag = e ? ((e + 126u) << 23) | (m << 22) : (m ? 126u << 23 : 0u);
+  return __uint_as_float(mag ? mag | ((c & 8u) << 28) : 0u);
+}
+
+// Q4_K 6-bit scale/min of group g from the 12 packed bytes s0|s1|s2
+// (src/native.c:14-19).
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t g,
+                                              uint32_t& sc, uint32_t& mi) {
+  if (g < 4) {
+    sc = (s0 >> (8 * g)) & 63u;
+    mi = (s1 >> (8 * g)) & 63u;
+  } else {
+    uint32_t k = 8 * (g - 4);
+    sc = ((s2 >> k) & 15u) | (((s0 >> k) >> 6 & 3u) << 4);
+    mi = ((s2 >> k) >> 4 & 15u) | (((s1 >> k) >> 6 & 3u) << 4);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ void flag(uint32_t* status, uint32_t bit) {
+  __hip_atomic_fetch_or(status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// fr_q8_activation on n <= 64 values held one per lane... here: a whole
+// group in registers of one thread (src/q4.c:37-61).
+__device__ void q8_group(float* v, int n) {
+  float max = 0.f;
+  for (int j = 0; j < n; ++j) max = fmaxf(max, fabsf(v[j]));
+  float scale = max / 127.0f;
+  if (scale == 0.f) {
+    for (int j = 0; j < n; ++j) v[j] = 0.f;
+    return;
+  }
+  float inv = 127.0f / max;
+  bool finite_inv = isfinite(inv);
+  for (int j = 0; j < n; ++j) {
+    float q = finite_inv ? v[j] * inv : (v[j] / max) * 127.0f;
+    q = rintf(q);
+    q = fminf(fmaxf(q, -127.f), 127.f);
+    double back = (double)q * (double)scale;
+    back = fmin(fmax(back, -(double)FLT_MAX), (double)FLT_MAX);
+    v[j] = (float)back;
+  }
+}
+
+// ------------------------------------------------- re-tiled row layouts
+//
+// Gate/up rows (n = hidden columns, nch = n/64 lane chunks of 64 columns):
+//  Q4_K : [2 parts][nch][16 B] quants (bytes 0-15 / 16-31 of each 32-byte
+//         chunk of a super-block), then [n/256][16 B] super-block headers.
+//  Q8_0 : [4 parts][nch][16 B] int8, then [nch][2 x fp16] scales.
+//  MXFP4: [2 parts][nch][16 B] codes, then [nch][2 B] exponents.
+//  Q4_0 : [2 parts][nch][16 B] nibbles, then [nch][2 x fp16] scales.
+// Lane c reads its 64 columns with 16-byte loads; 64 lanes read contiguous
+// 1 KB runs. Same byte count as the native row (the permutation is lossless).
+
+// Decode the lane's 64 columns of a gate/up row exactly as the reference
+// decodes each weight (src/native.c:13-31, src/q4.c:29-31). Used by the
+// fp64 modes and by the debug decoder; returns false on a non-finite scale.
+template <int type>
+__device__ __forceinline__ bool decode_lane_t(const uint8_t* row, int nch, int c, float* w) {
+  bool ok = true;
+  if (type == TQ4_K) {
+    uint4 h = ld16(row + 32 * nch + 16 * (c >> 2));
+    uint4 qa = ld16(row + 16 * c), qb = ld16(row + 16 * nch + 16 * c);
+    ok = !half_bad(h.x) && !half_bad(h.x >> 16);
+    float d = half_to_float(h.x & 0xffff), dm = half_to_float(h.x >> 16);
+    uint32_t g0 = 2 * (c & 3), sc0, mi0, sc1, mi1;
+    q4k_scale_min(h.y, h.z, h.w, g0, sc0, mi0);
+    q4k_scale_min(h.y, h.z, h.w, g0 + 1, sc1, mi1);
+    float D0 = d * (float)sc0, M0 = dm * (float)mi0, D1 = d * (float)sc1, M1 = dm * (float)mi1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t v = word(i < 4 ? qa : qb, i & 3);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        uint32_t byte = v >> (8 * b);
+        w[4 * i + b] = fmaf(D0, (float)(byte & 15u), -M0);
+        w[32 + 4 * i + b] = fmaf(D1, (float)((byte >> 4) & 15u), -M1);
+      }
+    }
+  } else if (type == TQ8_0) {
+    uint32_t s = *reinterpret_cast<const uint32_t*>(row + 64 * nch + 4 * c);
+    ok = !half_bad(s) && !half_bad(s >> 16);
+    float d0 = half_to_float(s & 0xffff), d1 = half_to_float(s >> 16);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      uint4 q = ld16(row + 16 * nch * p + 16 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t v = word(q, i);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          w[16 * p + 4 * i + b] = (p < 2 ? d0 : d1) * (float)(int8_t)(v >> (8 * b));
+      }
+    }
+  } else if (type == TMXFP4) {
+    uint32_t e = *reinterpret_cast<const uint16_t*>(row + 32 * nch + 2 * c);
+    ok = (e & 0xff) != 255 && (e >> 8) != 255;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      float sc = e8m0((e >> (8 * p)) & 0xff);
+      uint4 q = ld16(row + 16 * nch * p + 16 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t v = word(q, i);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          uint32_t byte = v >> (8 * b);
+          w[32 * p + 4 * i + b] = sc * e2m1(byte & 15u);
+          w[32 * p + 16 + 4 * i + b] = sc * e2m1((byte >> 4) & 15u);
+        }
+      }
+    }
+  } else {  // Q4_0
+    uint32_t s = *reinterpret_cast<const uint32_t*>(row + 32 * nch + 4 * c);
+    ok = !half_bad(s) && !half_bad(s >> 16);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      float d = half_to_float(p ? s >> 16 : s & 0xffff);
+      uint4 q = ld16(row + 16 * nch * p + 16 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t v = word(q, i);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          uint32_t byte = v >> (8 * b);
+          w[32 * p + 4 * i + b] = (float)((int)(byte & 15u) - 8) * d;
+          w[32 * p + 16 + 4 * i + b] = (float)((int)((byte >> 4) & 15u) - 8) * d;
+        }
+      }
+    }
+  }
+  return ok;
+}
+
+__device__ bool decode_lane(uint8_t type, const uint8_t* row, int nch, int c, float* w) {
+  switch (type) {
+    case TQ4_K: return decode_lane_t<TQ4_K>(row, nch, c, w);
+    case TQ8_0: return decode_lane_t<TQ8_0>(row, nch, c, w);
+    case TMXFP4: return decode_lane_t<TMXFP4>(row, nch, c, w);
+    default: return decode_lane_t<TQ4_0>(row, nch, c, w);
+  }
+}
+
+// Per-lane raw row data for the fp32 path: loaded once, reused per token.
+struct LaneRow {
+  uint4 q[4];
+  float s[4];    // per-64-column-half scale factors
+  float m[2];    // Q4_K mins (per group)
+  bool ok;
+};
+
+template <int type>
+__device__ __forceinline__ void load_lane(const uint8_t* row, int nch, int c, LaneRow& r) {
+  if (type == TQ4_K) {
+    uint4 h = ld16(row + 32 * nch + 16 * (c >> 2));
+    r.q[0] = ld16(row + 16 * c);
+    r.q[1] = ld16(row + 16 * nch + 16 * c);
+    r.ok = !half_bad(h.x) && !half_bad(h.x >> 16);
+    float d = half_to_float(h.x & 0xffff), dm = half_to_float(h.x >> 16);
+    uint32_t g0 = 2 * (c & 3), sc0, mi0, sc1, mi1;
+    q4k_scale_min(h.y, h.z, h.w, g0, sc0, mi0);
+    q4k_scale_min(h.y, h.z, h.w, g0 + 1, sc1, mi1);
+    r.s[0] = d * (float)sc0;
+    r.s[1] = d * (float)sc1;
+    r.m[0] = dm * (float)mi0;
+    r.m[1] = dm * (float)mi1;
+  } else if (type == TQ8_0) {
+    uint32_t s = *reinterpret_cast<const uint32_t*>(row + 64 * nch + 4 * c);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) r.q[p] = ld16(row + 16 * nch * p + 16 * c);
+    r.ok = !half_bad(s) && !half_bad(s >> 16);
+    r.s[0] = half_to_float(s & 0xffff);
+    r.s[1] = half_to_float(s >> 16);
+  } else if (type == TMXFP4) {
+    uint32_t e = *reinterpret_cast<const uint16_t*>(row + 32 * nch + 2 * c);
+    r.q[0] = ld16(row + 16 * c);
+    r.q[1] = ld16(row + 16 * nch + 16 * c);
+    r.ok = (e & 0xff) != 255 && (e >> 8) != 255;
+    r.s[0] = e8m0(e & 0xff);
+    r.s[1] = e8m0(e >> 8);
+  } else {  // Q4_0
+    uint32_t s = *reinterpret_cast<const uint32_t*>(row + 32 * nch + 4 * c);
+    r.q[0] = ld16(row + 16 * c);
+    r.q[1] = ld16(row + 16 * nch + 16 * c);
+    r.ok = !half_bad(s) && !half_bad(s >> 16);
+    r.s[0] = half_to_float(s & 0xffff);
+    r.s[1] = half_to_float(s >> 16);
+  }
+}
+
+// fp32 partial of one lane for one token. x points at the lane's 64
+// activations; X0/X1 are the sums of x[0..31] and x[32..63]. The Q4_K and
+// Q4_0 forms factor the scale and min out of the 32-column groups:
+// sum_j (D*q_j - M)*x_j = D*sum_j q_j*x_j - M*sum_j x_j.
+template <int type>
+__device__ __forceinline__ float lane_dot_f32(const LaneRow& r, const float* xp, float X0, float X1) {
+  const float4* x = reinterpret_cast<const float4*>(xp);
+  float s0 = 0.f, s1 = 0.f;
+  if (type == TQ4_K) {
+    // Byte i of the 32-byte chunk: column i (low nibble), 32+i (high).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t v = word(r.q[i >> 2], i & 3);
+      const float4 a = x[i], b = x[8 + i];
+      s0 = fmaf((float)(v & 15u), a.x, s0);
+      s0 = fmaf((float)((v >> 8) & 15u), a.y, s0);
+      s0 = fmaf((float)((v >> 16) & 15u), a.z, s0);
+      s0 = fmaf((float)((v >> 24) & 15u), a.w, s0);
+      s1 = fmaf((float)((v >> 4) & 15u), b.x, s1);
+      s1 = fmaf((float)((v >> 12) & 15u), b.y, s1);
+      s1 = fmaf((float)((v >> 20) & 15u), b.z, s1);
+      s1 = fmaf((float)(v >> 28), b.w, s1);
+    }
+    return (r.s[0] * s0 - r.m[0] * X0) + (r.s[1] * s1 - r.m[1] * X1);
+  }
+  if (type == TQ4_0) {
+    // Per 32-column block p, byte i: column i (low nibble), 16+i (high).
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t v = word(r.q[p], i);
+        const float4 a = x[8 * p + i], b = x[8 * p + 4 + i];
+        s = fmaf((float)(v & 15u), a.x, s);
+        s = fmaf((float)((v >> 8) & 15u), a.y, s);
+        s = fmaf((float)((v >> 16) & 15u), a.z, s);
+        s = fmaf((float)((v >> 24) & 15u), a.w, s);
+        s = fmaf((float)((v >> 4) & 15u), b.x, s);
+        s = fmaf((float)((v >> 12) & 15u), b.y, s);
+        s = fmaf((float)((v >> 20) & 15u), b.z, s);
+        s = fmaf((float)(v >> 28), b.w, s);
+      }
+      if (p) s1 = s; else s0 = s;
+    }
+    return r.s[0] * (s0 - 8.f * X0) + r.s[1] * (s1 - 8.f * X1);
+  }
+  if (type == TQ8_0) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t v = word(r.q[p], i);
+        const float4 a = x[4 * p + i];
+        s = fmaf((float)(int8_t)v, a.x, s);
+        s = fmaf((float)(int8_t)(v >> 8), a.y, s);
+        s = fmaf((float)(int8_t)(v >> 16), a.z, s);
+        s = fmaf((float)(int8_t)(v >> 24), a.w, s);
+      }
+      if (p < 2) s0 += s; else s1 += s;
+    }
+    return r.s[0] * s0 + r.s[1] * s1;
+  }
+  // MXFP4: per 32-column block p, byte i holds element i (low) and 16+i.
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v = word(r.q[p], i);
+      const float4 a = x[8 * p + i], b = x[8 * p + 4 + i];
+      s = fmaf(e2m1(v & 15u), a.x, s);
+      s = fmaf(e2m1((v >> 8) & 15u), a.y, s);
+      s = fmaf(e2m1((v >> 16) & 15u), a.z, s);
+      s = fmaf(e2m1((v >> 24) & 15u), a.w, s);
+      s = fmaf(e2m1((v >> 4) & 15u), b.x, s);
+      s = fmaf(e2m1((v >> 12) & 15u), b.y, s);
+      s = fmaf(e2m1((v >> 20) & 15u), b.z, s);
+      s = fmaf(e2m1(v >> 28), b.w, s);
+    }
+    if (p) s1 = s; else s0 = s;
+  }
+  return r.s[0] * s0 + r.s[1] * s1;
+}
+
+// ------------------------------------------------------------ phase A
+//
+// Task (pair p, neuron group ng): 4 wavefronts, each owning nn/4 neurons.
+// Lane c of a wave owns activation columns 64c..64c+63 of every row it
+// streams; a 64-lane butterfly reduces the row. Tokens are processed in
+// tiles of BT (compile time) so per-token values stay in registers.
+
+template <int MODE, int BT, int GU>
+__device__ __forceinline__ uint32_t phase_a_rows(const PlanHeader& H, const Scratch& S, unsigned p, unsigned ng,
+                                                 uint64_t slice, uint32_t proj, uint32_t tmask, unsigned t0,
+                                                 unsigned tc, const float* lds) {
+  const unsigned hidden = H.hidden, nch = hidden / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool active = lane < (int)nch;
+  const int c = active ? lane : 0;
+  const uint32_t row_bytes = proj / kNeurons;
+  const unsigned per_wave = H.nn / kWaves;
+  uint32_t bad = 0;
+  float X0[BT], X1[BT];
+#pragma unroll
+  for (int t = 0; t < BT; ++t) {
+    X0[t] = X1[t] = 0.f;
+    if (MODE == MODE_F32 && (GU == TQ4_K || GU == TQ4_0) && t < (int)tc) {
+      const float4* x = reinterpret_cast<const float4*>(lds + t * hidden + 64 * c);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float4 a = x[i], b = x[8 + i];
+        X0[t] += (a.x + a.y) + (a.z + a.w);
+        X1[t] += (b.x + b.y) + (b.z + b.w);
+      }
+    }
+  }
+  for (unsigned k = 0; k < per_wave; ++k) {
+    const unsigned n = ng * H.nn + wave * per_wave + k;
+    float av[BT], uv[BT];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint8_t* row = reinterpret_cast<const uint8_t*>(slice) + (r ? proj : 0) + (size_t)n * row_bytes;
+      if (MODE == MODE_F32) {
+        LaneRow lr;
+        load_lane<GU>(row, nch, c, lr);
+        if (active && !lr.ok) bad |= kErrScale;
+#pragma unroll
+        for (int t = 0; t < BT; ++t) {
+          float part = 0.f;
+          if (active && t < (int)tc) part = lane_dot_f32<GU>(lr, lds + t * hidden + 64 * c, X0[t], X1[t]);
+          float sum = wave_sum(part);
+          if (r) uv[t] = sum; else av[t] = sum;
+        }
+      } else {
+        float w[64];
+        bool ok = decode_lane_t<GU>(row, nch, c, w);
+        if (active && !ok) bad |= kErrScale;
+#pragma unroll
+        for (int t = 0; t < BT; ++t) {
+          double acc = 0.0;
+          if (active && t < (int)tc) {
+            const float* x = lds + t * hidden + 64 * c;
+#pragma unroll
+            for (int j = 0; j < 64; ++j) acc = fma((double)w[j], (double)x[j], acc);
+          }
+          double sum = wave_sum(acc);
+          float f = (!isfinite(sum) || fabs(sum) > (double)FLT_MAX) ? INFINITY : (float)sum;
+          if (r) uv[t] = f; else av[t] = f;
+        }
+      }
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int t = 0; t < BT; ++t) {
+        if (t >= (int)tc || !((tmask >> (t0 + t)) & 1u)) continue;
+        float a = av[t], u = uv[t], h = 0.f;
+        if (!isfinite(a) || !isfinite(u)) {
+          bad |= kErrRange;
+        } else {
+          // Stable sigmoid in double, as backends/ref.c:82-83.
+          double ad = a;
+          double sig = ad >= 0 ? 1.0 / (1.0 + exp(-ad)) : exp(ad) / (1.0 + exp(ad));
+          double hv = ad * sig * (double)u;
+          if (!isfinite(hv) || fabs(hv) > (double)FLT_MAX) bad |= kErrRange;
+          else h = (float)hv;
+        }
+        S.hbuf[((size_t)p * kMaxBurst + t0 + t) * kNeurons + n] = h;
+      }
+    }
+  }
+  return bad;
+}
+
+template <int MODE, int BT>
+__device__ void phase_a(const PlanHeader& H, const uint8_t* plan, const Scratch& S, uint32_t* status,
+                        unsigned task, float* lds) {
+  const unsigned per_pair = kNeurons / H.nn;
+  const unsigned p = task / per_pair, ng = task % per_pair;
+  const PairDesc* P = reinterpret_cast<const PairDesc*>(plan + H.pairs_off) + p;
+  const uint64_t slice = P->slice;
+  const uint32_t proj = P->proj;
+  const uint8_t gu = P->gu;
+  const uint32_t tmask = P->tmask;
+  const unsigned hidden = H.hidden, nch = hidden / 64, T = H.burst;
+  const float* xg = reinterpret_cast<const float*>(plan + H.x_off);
+  uint32_t bad = 0;
+
+  for (unsigned t0 = 0; t0 < T; t0 += BT) {
+    const unsigned tc = min((unsigned)BT, T - t0);
+    // Stage tc activation rows in LDS (Q8 mode: quantized per 64-group).
+    if (t0) __syncthreads();
+    {
+      const float4* src = reinterpret_cast<const float4*>(xg + (size_t)t0 * hidden);
+      float4* dst = reinterpret_cast<float4*>(lds);
+      for (unsigned i = threadIdx.x; i < tc * hidden / 4; i += kThreads) dst[i] = src[i];
+    }
+    __syncthreads();
+    if (MODE == MODE_Q8) {
+      // One thread per 64-value group: a lane chunk is one quantizer group.
+      for (unsigned g = threadIdx.x; g < tc * nch; g += kThreads) q8_group(lds + 64 * g, 64);
+      __syncthreads();
+    }
+    switch (gu) {
+      case TQ4_K: bad |= phase_a_rows<MODE, BT, TQ4_K>(H, S, p, ng, slice, proj, tmask, t0, tc, lds); break;
+      case TQ8_0: bad |= phase_a_rows<MODE, BT, TQ8_0>(H, S, p, ng, slice, proj, tmask, t0, tc, lds); break;
+      case TMXFP4: bad |= phase_a_rows<MODE, BT, TMXFP4>(H, S, p, ng, slice, proj, tmask, t0, tc, lds); break;
+      default: bad |= phase_a_rows<MODE, BT, TQ4_0>(H, S, p, ng, slice, proj, tmask, t0, tc, lds); break;
+    }
+  }
+  if (bad) flag(status, bad);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(S.done + (size_t)S.parity * kMaxPairs + p, 1u, __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ------------------------------------------------------------ phase B
+//
+// Down matrices, re-tiled:
+//  MXFP4 [H x 32]: [H][16 B] codes (byte i: neuron i low, 16+i high), [H] E8M0.
+//  Q8_0  [H x 32]: [2 parts][H][16 B] int8, then [H][fp16].
+//  Q4_0  [H x 32]: [H][16 B] nibbles (byte i: neuron i low, 16+i high), [H][fp16].
+//  Q4_K transposed [32 x H]: per 256-column super-block, [4][64 lanes][16 B]
+//         nibbles, lane l holding columns 4l..4l+3 of neurons 8k..8k+7 (dword
+//         w: neurons 8k+2w, 8k+2w+1; nibble j: neuron +j/4, column +j%4),
+//         then the 32 neurons' 16-byte super-block headers.
+
+__device__ __forceinline__ void hdr_dm(const uint4& h, uint32_t g, float& D, float& M, bool& ok) {
+  ok = !half_bad(h.x) && !half_bad(h.x >> 16);
+  uint32_t sc, mi;
+  q4k_scale_min(h.y, h.z, h.w, g, sc, mi);
+  D = half_to_float(h.x & 0xffff) * (float)sc;
+  M = half_to_float(h.x >> 16) * (float)mi;
+}
+
+// Decode one [H x 32] down row (neurons 0..31 of output d) exactly.
+__device__ bool decode_down_row(uint8_t dn, const uint8_t* down, unsigned hidden, unsigned d, float* w) {
+  bool ok = true;
+  if (dn == TMXFP4) {
+    uint4 q = ld16(down + 16 * (size_t)d);
+    uint32_t e = down[16 * (size_t)hidden + d];
+    ok = e != 255;
+    float sc = e8m0(e);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t v = word(q, i);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        uint32_t byte = v >> (8 * b);
+        w[4 * i + b] = sc * e2m1(byte & 15u);
+        w[16 + 4 * i + b] = sc * e2m1((byte >> 4) & 15u);
+      }
+    }
+  } else if (dn == TQ8_0) {
+    uint32_t s = reinterpret_cast<const uint16_t*>(down + 32 * (size_t)hidden)[d];
+    ok = !half_bad(s);
+    float sc = half_to_float(s);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      uint4 q = ld16(down + 16 * (size_t)hidden * p + 16 * (size_t)d);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t v = word(q, i);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) w[16 * p + 4 * i + b] = sc * (float)(int8_t)(v >> (8 * b));
+      }
+    }
+  } else {  // Q4_0
+    uint32_t s = reinterpret_cast<const uint16_t*>(down + 16 * (size_t)hidden)[d];
+    ok = !half_bad(s);
+    float sc = half_to_float(s);
+    uint4 q = ld16(down + 16 * (size_t)d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t v = word(q, i);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        uint32_t byte = v >> (8 * b);
+        w[4 * i + b] = (float)((int)(byte & 15u) - 8) * sc;
+        w[16 + 4 * i + b] = (float)((int)((byte >> 4) & 15u) - 8) * sc;
+      }
+    }
+  }
+  return ok;
+}
+
+// Decode the 4 columns x 32 neurons of lane l in super-block sb of a
+// transposed Q4_K down matrix: w[n*4 + c] (exact reference decode).
+__device__ bool decode_down_q4kt(const uint8_t* down, unsigned sb, int l, float* w) {
+  const uint8_t* base = down + 4608 * (size_t)sb;
+  bool ok = true;
+  const uint32_t g = (uint32_t)l >> 3;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint4 q = ld16(base + 1024 * k + 16 * l);
+#pragma unroll
+    for (int wd = 0; wd < 4; ++wd) {
+      uint32_t v = word(q, wd);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        int n = 8 * k + 2 * wd + s;
+        uint4 h = ld16(base + 4096 + 16 * n);
+        float D, M;
+        bool hok;
+        hdr_dm(h, g, D, M, hok);
+        ok &= hok;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) w[4 * n + cc] = fmaf(D, (float)((v >> (4 * (4 * s + cc))) & 15u), -M);
+      }
+    }
+  }
+  return ok;
+}
+
+template <int MODE, int TB>
+__device__ void phase_b(const PlanHeader& H, const uint8_t* plan, const Scratch& S, uint32_t* status,
+                        unsigned task, float* lds) {
+  const unsigned gi = task / H.nranges, cr = task % H.nranges;
+  const GroupDesc G = reinterpret_cast<const GroupDesc*>(plan + H.groups_off)[gi];
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + H.pairs_off);
+  const unsigned hidden = H.hidden, T = H.burst, count = G.count;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t bad = 0;
+
+  // LDS: hs[count][T][32] floats | per-wave tables | wave reduction.
+  float* hs = lds;
+  const unsigned wstride = 512 + T * 256 + T * 8;
+  float* wtab = hs + H.gmax * T * kNeurons;
+  double* red = reinterpret_cast<double*>(wtab + kWaves * wstride);
+
+  // Bounded wait for the 32 h values of every pair of the group: every
+  // phase-A task has a lower block index than any phase-B task.
+  if (tid == 0) {
+    const uint32_t need = kNeurons / H.nn;
+    for (unsigned j = 0; j < count; ++j) {
+      const uint32_t* ctr = S.done + (size_t)S.parity * kMaxPairs + G.first + j;
+      uint32_t spins = 0;
+      while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < need) {
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins > kSpinLimit) {
+          bad |= kErrTimeout;
+          break;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  for (unsigned i = tid; i < count * T * kNeurons; i += kThreads) {
+    unsigned j = i / (T * kNeurons), r = i % (T * kNeurons);
+    hs[i] = S.hbuf[((size_t)(G.first + j) * kMaxBurst) * kNeurons + r];
+  }
+  __syncthreads();
+  if (MODE == MODE_Q8) {  // ref-q8 quantizes each slice's h (backends/ref.c:85)
+    for (unsigned i = tid; i < count * T; i += kThreads) q8_group(hs + i * kNeurons, kNeurons);
+    __syncthreads();
+  }
+
+  double y[TB][4];
+#pragma unroll
+  for (int t = 0; t < TB; ++t)
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) y[t][cc] = 0.0;
+
+  if (G.dn != TQ4_KT) {
+    // [H x 32]: thread = output row d; every wave walks every pair.
+    const unsigned d = cr * kCols + tid;
+    for (unsigned j = 0; j < count; ++j) {
+      const PairDesc* P = pairs + G.first + j;
+      const uint8_t* down = reinterpret_cast<const uint8_t*>(P->slice) + 2 * (size_t)P->proj;
+      const uint32_t tmask = P->tmask;
+      if (MODE == MODE_F32) {
+        // Raw codes once, one fp32 dot per token, fp64 accumulation.
+        uint4 q0, q1 = {0, 0, 0, 0};
+        float sc;
+        if (G.dn == TMXFP4) {
+          q0 = ld16(down + 16 * (size_t)d);
+          uint32_t e = down[16 * (size_t)hidden + d];
+          if (e == 255) bad |= kErrScale;
+          sc = e8m0(e);
+        } else if (G.dn == TQ8_0) {
+          q0 = ld16(down + 16 * (size_t)d);
+          q1 = ld16(down + 16 * (size_t)hidden + 16 * (size_t)d);
+          uint32_t sb = reinterpret_cast<const uint16_t*>(down + 32 * (size_t)hidden)[d];
+          if (half_bad(sb)) bad |= kErrScale;
+          sc = half_to_float(sb);
+        } else {
+          q0 = ld16(down + 16 * (size_t)d);
+          uint32_t sb = reinterpret_cast<const uint16_t*>(down + 16 * (size_t)hidden)[d];
+          if (half_bad(sb)) bad |= kErrScale;
+          sc = half_to_float(sb);
+        }
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+          if (t >= (int)T || !((tmask >> t) & 1u)) continue;
+          const float* h = hs + (j * T + t) * kNeurons;
+          float sum = 0.f;
+          if (G.dn == TQ8_0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              uint32_t v = word(i < 4 ? q0 : q1, i & 3);
+#pragma unroll
+              for (int b = 0; b < 4; ++b) sum = fmaf((float)(int8_t)(v >> (8 * b)), h[4 * i + b], sum);
+            }
+          } else if (G.dn == TMXFP4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              uint32_t v = word(q0, i);
+#pragma unroll
+              for (int b = 0; b < 4; ++b) {
+                uint32_t byte = v >> (8 * b);
+                sum = fmaf(e2m1(byte & 15u), h[4 * i + b], sum);
+                sum = fmaf(e2m1((byte >> 4) & 15u), h[16 + 4 * i + b], sum);
+              }
+            }
+          } else {
+            float hsum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              uint32_t v = word(q0, i);
+#pragma unroll
+              for (int b = 0; b < 4; ++b) {
+                uint32_t byte = v >> (8 * b);
+                sum = fmaf((float)(byte & 15u), h[4 * i + b], sum);
+                sum = fmaf((float)((byte >> 4) & 15u), h[16 + 4 * i + b], sum);
+                hsum += h[4 * i + b] + h[16 + 4 * i + b];
+              }
+            }
+            sum -= 8.f * hsum;
+          }
+          y[t][0] += (double)P->gate[t] * ((double)sc * (double)sum);
+        }
+      } else {
+        float w[32];
+        if (!decode_down_row(G.dn, down, hidden, d, w)) bad |= kErrScale;
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+          if (t >= (int)T || !((tmask >> t) & 1u)) continue;
+          const float* h = hs + (j * T + t) * kNeurons;
+          double sum = 0.0;
+#pragma unroll
+          for (int n = 0; n < 32; ++n) sum = fma((double)w[n], (double)h[n], sum);
+          y[t][0] += (double)P->gate[t] * sum;
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TB; ++t)
+      if (t < (int)T) S.partial[((size_t)gi * T + t) * hidden + d] = y[t][0];
+  } else {
+    // Transposed Q4_K: lane = 4 columns of super-block cr; wave w takes
+    // pairs j = w, w+4, ...; the 4 waves are summed in LDS in wave order.
+    float* tab = wtab + wave * wstride;     // D[8][32], M[8][32] | cD[T][8][32] | B[T][8]
+    float* cD = tab + 512;
+    float* Bt = cD + T * 256;
+    const uint32_t g = (uint32_t)lane >> 3;
+    for (unsigned j = wave; j < count; j += kWaves) {
+      const PairDesc* P = pairs + G.first + j;
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(P->slice) + 2 * (size_t)P->proj + 4608 * (size_t)cr;
+      const uint32_t tmask = P->tmask;
+      uint4 q[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) q[k] = ld16(base + 1024 * k + 16 * lane);
+      // Scale/min table: item lane + 64r -> neuron (lane>>3)+8r, group lane&7.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = (lane >> 3) + 8 * r, gg = lane & 7;
+        uint4 hd = ld16(base + 4096 + 16 * n);
+        float D, M;
+        bool ok;
+        hdr_dm(hd, gg, D, M, ok);
+        if (!ok) bad |= kErrScale;
+        tab[gg * 32 + n] = D;
+        tab[256 + gg * 32 + n] = M;
+        if (MODE == MODE_F32) {
+#pragma unroll
+          for (int t = 0; t < TB; ++t)
+            if (t < (int)T) cD[t * 256 + gg * 32 + n] = D * hs[(j * T + t) * kNeurons + n];
+        }
+      }
+      if (MODE == MODE_F32) {
+        // B[t][g] = sum_n M[g][n]*h[n] in a fixed order: 4 terms per lane,
+        // then a butterfly over the 8 lanes sharing g.
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+          if (t >= (int)T) continue;
+          float part = 0.f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = (lane >> 3) + 8 * r;
+            part += tab[256 + (lane & 7) * 32 + n] * hs[(j * T + t) * kNeurons + n];
+          }
+          part += __shfl_xor(part, 8, 64);
+          part += __shfl_xor(part, 16, 64);
+          part += __shfl_xor(part, 32, 64);
+          if (lane < 8) Bt[t * 8 + lane] = part;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int t = 0; t < TB; ++t) {
+        if (t >= (int)T || !((tmask >> t) & 1u)) continue;
+        const double gate = (double)P->gate[t];
+        if (MODE == MODE_F32) {
+          const float* cd = cD + t * 256 + g * 32;
+          float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int wd = 0; wd < 4; ++wd) {
+              uint32_t v = word(q[k], wd);
+#pragma unroll
+              for (int sN = 0; sN < 2; ++sN) {
+                float coef = cd[8 * k + 2 * wd + sN];
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc)
+                  s4[cc] = fmaf((float)((v >> (4 * (4 * sN + cc))) & 15u), coef, s4[cc]);
+              }
+            }
+          float B = Bt[t * 8 + g];
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) y[t][cc] += gate * (double)(s4[cc] - B);
+        } else {
+          const float* h = hs + (j * T + t) * kNeurons;
+          double s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int wd = 0; wd < 4; ++wd) {
+              uint32_t v = word(q[k], wd);
+#pragma unroll
+              for (int sN = 0; sN < 2; ++sN) {
+                const int n = 8 * k + 2 * wd + sN;
+                const float D = tab[g * 32 + n], M = tab[256 + g * 32 + n];
+                const double hn = (double)h[n];
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                  float w = fmaf(D, (float)((v >> (4 * (4 * sN + cc))) & 15u), -M);
+                  s4[cc] = fma((double)w, hn, s4[cc]);
+                }
+              }
+            }
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) y[t][cc] += gate * s4[cc];
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      if (t >= (int)T) continue;
+      __syncthreads();
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) red[wave * kCols + 4 * lane + cc] = y[t][cc];
+      __syncthreads();
+      double v = ((red[tid] + red[kCols + tid]) + red[2 * kCols + tid]) + red[3 * kCols + tid];
+      S.partial[((size_t)gi * T + t) * hidden + cr * kCols + tid] = v;
+    }
+  }
+  if (bad) flag(status, bad);
+
+  // The last-arriving group of this output range reduces it, in group order.
+  __shared__ uint32_t ticket;
+  __syncthreads();
+  if (tid == 0) {
+    ticket = __hip_atomic_fetch_add(S.fin + (size_t)S.parity * kMaxRanges + cr, 1u, __ATOMIC_ACQ_REL,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (ticket != H.ngroups - 1) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  float* yout = reinterpret_cast<float*>(status + 4);
+  const unsigned col = cr * kCols + tid;
+  for (unsigned t = 0; t < T; ++t) {
+    double v = 0.0;
+    for (unsigned g2 = 0; g2 < H.ngroups; ++g2) v += S.partial[((size_t)g2 * T + t) * hidden + col];
+    float f = 0.f;
+    if (!isfinite(v) || fabs(v) > (double)FLT_MAX) flag(status, kErrRange);
+    else f = (float)v;
+    yout[(size_t)t * hidden + col] = f;
+  }
+}
+
+// TILE = 1 for single-token requests, 8 for bursts (phase A in tiles of 4).
+template <int MODE, int TILE>
+__global__ __launch_bounds__(kThreads) void layer_kernel(const uint8_t* __restrict__ plan, Scratch S) {
+  extern __shared__ __align__(16) float lds[];
+  const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
+  uint32_t* status = S.out + (size_t)S.parity * S.out_words;
+  if (blockIdx.x == 0) {
+    // Clear the other parity's counters and status for the next launch.
+    const uint32_t other = S.parity ^ 1u;
+    for (unsigned i = threadIdx.x; i < kMaxPairs; i += kThreads) S.done[(size_t)other * kMaxPairs + i] = 0;
+    if (threadIdx.x < kMaxRanges) S.fin[(size_t)other * kMaxRanges + threadIdx.x] = 0;
+    if (threadIdx.x == 0) S.out[(size_t)other * S.out_words] = 0;
+  }
+  const unsigned b = blockIdx.x;
+  if (b < H.ntA) phase_a<MODE, TILE == 1 ? 1 : 4>(H, plan, S, status, b, lds);
+  else phase_b<MODE, TILE>(H, plan, S, status, b - H.ntA, lds);
+}
+
+// ------------------------------------------------------- load re-tiling
+//
+// dst[o] = src[source(o)] for every byte o of a slice; the permutations are
+// the layouts documented above. One workgroup per slice.
+
+struct SliceShape {
+  uint32_t hidden, gu, dn, proj, down, slice;
+};
+
+__device__ __forceinline__ uint32_t gu_source(uint8_t type, uint32_t nch, uint32_t o) {
+  // o is a byte offset inside one re-tiled gate/up row of 64*nch columns.
+  if (type == TQ4_K) {
+    if (o < 32 * nch) {
+      uint32_t p = o / (16 * nch), r = o % (16 * nch), c = r / 16, i = r % 16;
+      uint32_t sb = c / 4, k = c % 4;
+      return 144 * sb + 16 + 32 * k + 16 * p + i;
+    }
+    uint32_t r = o - 32 * nch;
+    return 144 * (r / 16) + r % 16;
+  }
+  if (type == TQ8_0) {
+    if (o < 64 * nch) {
+      uint32_t p = o / (16 * nch), r = o % (16 * nch), c = r / 16, i = r % 16;
+      return 34 * (2 * c + p / 2) + 2 + 16 * (p % 2) + i;
+    }
+    uint32_t r = o - 64 * nch, c = r / 4, k = r % 4;
+    return 34 * (2 * c + k / 2) + k % 2;
+  }
+  if (type == TMXFP4) {
+    if (o < 32 * nch) {
+      uint32_t p = o / (16 * nch), r = o % (16 * nch), c = r / 16, i = r % 16;
+      return 17 * (2 * c + p) + 1 + i;
+    }
+    uint32_t r = o - 32 * nch, c = r / 2, p = r % 2;
+    return 17 * (2 * c + p);
+  }
+  // Q4_0
+  if (o < 32 * nch) {
+    uint32_t p = o / (16 * nch), r = o % (16 * nch), c = r / 16, i = r % 16;
+    return 18 * (2 * c + p) + 2 + i;
+  }
+  uint32_t r = o - 32 * nch, c = r / 4, k = r % 4;
+  return 18 * (2 * c + k / 2) + k % 2;
+}
+
+// Byte o of a re-tiled [H x 32] down matrix.
+__device__ __forceinline__ uint32_t down_source(uint8_t dn, uint32_t hidden, uint32_t o) {
+  if (dn == TMXFP4) return o < 16 * hidden ? 17 * (o / 16) + 1 + o % 16 : 17 * (o - 16 * hidden);
+  if (dn == TQ8_0) {
+    if (o < 32 * hidden) {
+      uint32_t p = o / (16 * hidden), r = o % (16 * hidden);
+      return 34 * (r / 16) + 2 + 16 * p + r % 16;
+    }
+    uint32_t r = o - 32 * hidden;
+    return 34 * (r / 2) + r % 2;
+  }
+  // Q4_0
+  if (o < 16 * hidden) return 18 * (o / 16) + 2 + o % 16;
+  uint32_t r = o - 16 * hidden;
+  return 18 * (r / 2) + r % 2;
+}
+
+// Nibble (neuron n, column j) of a native transposed Q4_K down.
+__device__ __forceinline__ uint32_t q4kt_nibble(const uint8_t* src, uint32_t row_bytes, uint32_t n, uint32_t j) {
+  const uint8_t* b = src + (size_t)n * row_bytes + 144 * (j / 256);
+  uint32_t jj = j % 256, chunk = jj / 64, i = jj % 32, half = (jj % 64) / 32;
+  return (b[16 + 32 * chunk + i] >> (4 * half)) & 15u;
+}
+
+__device__ __forceinline__ uint8_t q4kt_byte(const uint8_t* src, uint32_t hidden, uint32_t o) {
+  const uint32_t row_bytes = 144 * (hidden / 256);
+  uint32_t sb = o / 4608, r = o % 4608;
+  if (r >= 4096) {
+    uint32_t n = (r - 4096) / 16, i = (r - 4096) % 16;
+    return src[(size_t)n * row_bytes + 144 * sb + i];
+  }
+  uint32_t k = r / 1024, l = (r % 1024) / 16, m = r % 16, wd = m / 4, bb = m % 4;
+  uint32_t n = 8 * k + 2 * wd + bb / 2;
+  uint32_t j = 256 * sb + 4 * l + 2 * (bb % 2);
+  return (uint8_t)(q4kt_nibble(src, row_bytes, n, j) | (q4kt_nibble(src, row_bytes, n, j + 1) << 4));
+}
+
+__device__ uint8_t retile_byte(const SliceShape& s, const uint8_t* src, uint32_t o) {
+  const uint32_t nch = s.hidden / 64;
+  if (o < 2 * s.proj) {
+    uint32_t row_bytes = s.proj / kNeurons, rbase = (o / row_bytes) * row_bytes;
+    return src[rbase + gu_source((uint8_t)s.gu, nch, o - rbase)];
+  }
+  uint32_t od = o - 2 * s.proj;
+  const uint8_t* dsrc = src + 2 * s.proj;
+  if (s.dn == TQ4_KT) return q4kt_byte(dsrc, s.hidden, od);
+  return dsrc[down_source((uint8_t)s.dn, s.hidden, od)];
+}
+
+// Slices [first, first+count) of consecutive layout: routed slices of one
+// shape; `shared_every` marks the shared slice position (513th of a layer).
+__global__ void retile_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, SliceShape routed,
+                              SliceShape shared, uint64_t layer_bytes, uint32_t first_slice, uint32_t nslices) {
+  uint32_t sidx = first_slice + blockIdx.x;
+  if (blockIdx.x >= nslices) return;
+  uint32_t layer = sidx / 513, e = sidx % 513;
+  uint64_t off = layer * layer_bytes + (uint64_t)e * routed.slice;
+  const SliceShape& s = e == kShared ? shared : routed;
+  const uint8_t* in = src + off;
+  uint8_t* out = dst + off;
+  for (uint32_t o = threadIdx.x; o < s.slice; o += blockDim.x) out[o] = retile_byte(s, in, o);
+}
+
+// Debug: decode re-tiled gate/up row(s) with the hot path's decoder.
+__global__ void debug_decode_rows(uint8_t type, const uint8_t* row, uint32_t n, float* out, uint32_t* status) {
+  int c = threadIdx.x;
+  uint32_t nch = n / 64;
+  if (c >= (int)nch) return;
+  float w[64];
+  if (!decode_lane(type, row, nch, c, w)) atomicOr(status, kErrScale);
+  for (int j = 0; j < 64; ++j) {
+    // lane chunk column -> row column
+    uint32_t col;
+    if (type == TQ4_K) col = 64 * c + j;                 // chunk columns in order
+    else col = 64 * c + j;                               // two 32-blocks in order
+    out[col] = w[j];
+  }
+}
+
+__global__ void debug_decode_down(uint8_t dn, const uint8_t* down, uint32_t hidden, float* out, uint32_t* status) {
+  uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (dn == TQ4_KT) {
+    // thread = (super-block, lane)
+    uint32_t sb = i / 64, l = i % 64;
+    if (sb >= hidden / 256) return;
+    float w[128];
+    if (!decode_down_q4kt(down, sb, (int)l, w)) atomicOr(status, kErrScale);
+    for (int n = 0; n < 32; ++n)
+      for (int cc = 0; cc < 4; ++cc) out[(size_t)(256 * sb + 4 * l + cc) * 32 + n] = w[4 * n + cc];
+    return;
+  }
+  if (i >= hidden) return;
+  float w[32];
+  if (!decode_down_row(dn, down, hidden, i, w)) atomicOr(status, kErrScale);
+  for (int n = 0; n < 32; ++n) out[(size_t)i * 32 + n] = w[n];
+}
+
+__global__ void debug_retile_row(SliceShape s, const uint8_t* in, uint8_t* outb, uint32_t bytes) {
+  for (uint32_t o = threadIdx.x; o < bytes; o += blockDim.x) outb[o] = in[gu_source((uint8_t)s.gu, s.hidden / 64, o)];
+}
+
+__global__ void debug_retile_down(uint8_t dn, uint32_t hidden, const uint8_t* in, uint8_t* outb, uint32_t bytes) {
+  for (uint32_t o = threadIdx.x; o < bytes; o += blockDim.x)
+    outb[o] = dn == TQ4_KT ? q4kt_byte(in, hidden, o) : in[down_source(dn, hidden, o)];
+}
+
+__global__ void debug_quantize(float* x, uint32_t groups) {
+  uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g < groups) q8_group(x + 64 * g, 64);
+}
+
+__global__ void debug_quantize32(float* x, uint32_t groups) {
+  uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g < groups) q8_group(x + 32 * g, 32);
+}
+
+// ================================================================ host
+
+struct Layout {
+  uint32_t hidden, format, gu, dn, shared_gu, shared_dn;
+  uint64_t proj, down, slice, shared_proj, shared_slice, layer, block;
+};
+
+uint64_t row_bytes(uint32_t type, uint32_t n) {
+  switch (type) {
+    case TQ4_K: return (uint64_t)n / 256 * 144;
+    case TMXFP4: return (uint64_t)n / 32 * 17;
+    case TQ8_0: return (uint64_t)n / 32 * 34;
+    case TQ4_0: return (uint64_t)n / 32 * 18;
+    default: return 0;
+  }
+}
+
+bool layout_of(uint32_t hidden, uint32_t format, Layout& l) {
+  if (!hidden || hidden > (uint32_t)kMaxHidden || hidden % kCols) return false;
+  memset(&l, 0, sizeof(l));
+  l.hidden = hidden;
+  l.format = format;
+  switch (format) {
+    case FR_HIP_FMT_LEGACY: l.gu = TQ4_0; l.dn = TQ4_0; break;
+    case FR_HIP_FMT_NATIVE: l.gu = TQ4_K; l.dn = TMXFP4; break;
+    case FR_HIP_FMT_Q4KT: l.gu = TQ4_K; l.dn = TQ4_KT; break;
+    case FR_HIP_FMT_Q8: l.gu = TQ8_0; l.dn = TQ8_0; break;
+    case FR_HIP_FMT_MXFP4: l.gu = TMXFP4; l.dn = TMXFP4; break;
+    default: return false;
+  }
+  l.proj = kNeurons * row_bytes(l.gu, hidden);
+  l.down = l.dn == TQ4_KT ? kNeurons * row_bytes(TQ4_K, hidden) : (uint64_t)hidden * row_bytes(l.dn, kNeurons);
+  l.slice = 2 * l.proj + l.down;
+  if (format == FR_HIP_FMT_LEGACY) {
+    l.shared_gu = l.shared_dn = TQ4_0;
+    l.shared_proj = l.proj;
+    l.shared_slice = l.slice;
+  } else {
+    l.shared_gu = l.shared_dn = TQ8_0;
+    l.shared_proj = kNeurons * row_bytes(TQ8_0, hidden);
+    l.shared_slice = 3 * l.shared_proj;
+  }
+  l.layer = (uint64_t)kRouted * l.slice + l.shared_slice;
+  l.block = (uint64_t)kLayers * l.layer;
+  return true;
+}
+
+SliceShape shape_of(const Layout& l, bool shared) {
+  SliceShape s;
+  s.hidden = l.hidden;
+  s.gu = shared ? l.shared_gu : l.gu;
+  s.dn = shared ? l.shared_dn : l.dn;
+  s.proj = (uint32_t)(shared ? l.shared_proj : l.proj);
+  s.down = (uint32_t)(shared ? l.shared_proj : l.down);
+  s.slice = (uint32_t)(shared ? l.shared_slice : l.slice);
+  return s;
+}
+
+struct Engine {
+  int device = -1;
+  hipStream_t stream = nullptr;
+  uint8_t* block[kBlocks] = {};
+  Layout lay[kBlocks];
+  uint32_t* done = nullptr;
+  uint32_t* fin = nullptr;
+  float* hbuf = nullptr;
+  double* partial = nullptr;
+  size_t partial_bytes = 0;
+  uint32_t* out = nullptr;
+  uint32_t out_words = 0;
+  uint8_t* plan_dev = nullptr;
+  uint8_t* plan_host = nullptr;   // pinned
+  size_t plan_cap = 0;
+  uint32_t* out_host = nullptr;   // pinned
+  uint8_t* staging = nullptr;     // device staging for uploads
+  size_t staging_bytes = 0;
+  uint32_t parity = 0;
+  uint32_t last_parity = 0;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  fr_hip_sample sample = {};
+};
+Engine E;
+bool g_open = false;
+
+size_t plan_capacity(uint32_t burst, uint32_t hidden) {
+  return sizeof(PlanHeader) + (size_t)kMaxPairs * sizeof(PairDesc) + (size_t)kMaxPairs * sizeof(GroupDesc) + 256 +
+         (size_t)burst * hidden * sizeof(float);
+}
+
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+
+// Pairs per down-phase group: about 48 KB of down weights per task.
+uint32_t group_pairs(uint8_t dn) {
+  uint32_t per = dn == TQ4_KT ? 4608u : kCols * (uint32_t)row_bytes(dn, kNeurons);
+  int over = env_int("FRONK_HIP_GROUP_BYTES", 49152);
+  uint32_t g = (uint32_t)over / per;
+  return g < 1 ? 1 : g > 64 ? 64 : g;
+}
+
+int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, unsigned* grid) {
+  if (!r || !out || !used || !grid || !r->expert || !r->gate || !r->x) return FR_HIP_INVALID;
+  if (r->burst < 1 || r->burst > (unsigned)kMaxBurst || r->layer >= (unsigned)kLayers || r->mode > 2)
+    return FR_HIP_INVALID;
+  const uint32_t T = r->burst, hidden = r->hidden;
+  int nloaded = 0;
+  for (int b = 0; b < kBlocks; ++b) {
+    if (!E.block[b]) continue;
+    if (E.lay[b].hidden != hidden) return FR_HIP_INVALID;
+    ++nloaded;
+  }
+  if (!nloaded) return FR_HIP_STATE;
+  if (cap < plan_capacity(T, hidden)) return FR_HIP_INVALID;
+  // Unique experts, token-major first appearance (backends/avx2.c:661-672).
+  uint16_t ids[kMaxUnique];
+  uint8_t masks[kMaxUnique] = {};
+  float gates[kMaxUnique][kMaxBurst] = {};
+  int nu = 0;
+  for (uint32_t t = 0; t < T; ++t)
+    for (int e = 0; e < 11; ++e) {
+      float g = r->gate[t * 11 + e];
+      if (e == 10 && g == 0.f) continue;
+      uint16_t id = e == 10 ? (uint16_t)kShared : r->expert[t * 10 + e];
+      if (id > kShared) return FR_HIP_INVALID;
+      int s = 0;
+      while (s < nu && ids[s] != id) ++s;
+      if (s == nu) ids[nu++] = id;
+      masks[s] |= (uint8_t)(1u << t);
+      gates[s][t] = g;
+    }
+  // Pairs, partitioned by down format so each group is homogeneous.
+  PlanHeader* H = reinterpret_cast<PlanHeader*>(out);
+  memset(H, 0, sizeof(*H));
+  PairDesc* pairs = reinterpret_cast<PairDesc*>(out + sizeof(PlanHeader));
+  uint32_t np = 0;
+  uint8_t classes[4] = {TQ4_KT, TMXFP4, TQ4_0, TQ8_0};
+  GroupDesc groups[kMaxPairs];
+  uint32_t ng = 0, gmax = 1;
+  uint64_t wbytes = 0;
+  for (uint8_t cls : classes) {
+    uint32_t start = np;
+    for (int s = 0; s < nu; ++s)
+      for (int b = 0; b < kBlocks; ++b) {
+        if (!E.block[b]) continue;
+        const Layout& l = E.lay[b];
+        bool shared = ids[s] == kShared;
+        uint8_t dn = (uint8_t)(shared ? l.shared_dn : l.dn);
+        if (dn != cls) continue;
+        PairDesc& P = pairs[np++];
+        memset(&P, 0, sizeof(P));
+        P.slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer + (uint64_t)ids[s] * l.slice);
+        P.proj = (uint32_t)(shared ? l.shared_proj : l.proj);
+        P.gu = (uint8_t)(shared ? l.shared_gu : l.gu);
+        P.dn = dn;
+        P.tmask = masks[s];
+        for (uint32_t t = 0; t < T; ++t) P.gate[t] = gates[s][t];
+        wbytes += shared ? l.shared_slice : l.slice;
+      }
+    uint32_t gp = group_pairs(cls);
+    for (uint32_t f = start; f < np; f += gp) {
+      GroupDesc& G = groups[ng++];
+      memset(&G, 0, sizeof(G));
+      G.first = (uint16_t)f;
+      G.count = (uint16_t)(np - f < gp ? np - f : gp);
+      G.dn = cls;
+      if (G.count > gmax) gmax = G.count;
+    }
+  }
+  const uint32_t nn = (uint32_t)env_int("FRONK_HIP_NEURONS_PER_TASK", 8);
+  if (nn < 4 || nn > 32 || kNeurons % nn || nn % kWaves) return FR_HIP_INVALID;
+  H->hidden = hidden;
+  H->burst = T;
+  H->mode = r->mode;
+  H->npairs = np;
+  H->ngroups = ng;
+  H->nranges = hidden / kCols;
+  H->nn = nn;
+  H->ntA = np * (kNeurons / nn);
+  H->ntB = ng * H->nranges;
+  // Phase A stages activations in tiles of 1 (single token) or 4 tokens.
+  const uint32_t tchunk = T == 1 ? 1 : (T < 4 ? T : 4);
+  H->tchunk = tchunk;
+  H->gmax = gmax;
+  H->pairs_off = sizeof(PlanHeader);
+  H->groups_off = H->pairs_off + np * sizeof(PairDesc);
+  memcpy(out + H->groups_off, groups, ng * sizeof(GroupDesc));
+  H->x_off = (uint32_t)((H->groups_off + ng * sizeof(GroupDesc) + 255) & ~255u);
+  memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
+  H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
+  size_t ldsA = (size_t)tchunk * hidden * sizeof(float);
+  size_t wstride = 512 + T * 256 + T * 8;
+  size_t ldsB = (size_t)gmax * T * kNeurons * sizeof(float) + kWaves * wstride * sizeof(float) + 8 +
+                kWaves * kCols * sizeof(double);
+  H->lds = (uint32_t)(ldsA > ldsB ? ldsA : ldsB);
+  if (H->lds > (uint32_t)kLdsLimit) return FR_HIP_UNSUPPORTED;
+  *used = H->total;
+  *grid = H->ntA + H->ntB;
+  E.sample.unique_experts = (unsigned)nu;
+  E.sample.pairs = np;
+  E.sample.grid = *grid;
+  E.sample.blocks = (unsigned)nloaded;
+  E.sample.weight_bytes = wbytes;
+  return FR_HIP_OK;
+}
+
+int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream) {
+  Scratch S;
+  S.done = E.done;
+  S.fin = E.fin;
+  S.hbuf = E.hbuf;
+  S.partial = E.partial;
+  S.out = E.out;
+  S.out_words = E.out_words;
+  S.parity = E.parity;
+  if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
+  const dim3 g(grid), blk(kThreads);
+  const bool one = H.burst == 1;
+  switch (H.mode) {
+    case MODE_F32:
+      if (one) hipLaunchKernelGGL((layer_kernel<MODE_F32, 1>), g, blk, H.lds, stream, dev_plan, S);
+      else hipLaunchKernelGGL((layer_kernel<MODE_F32, 8>), g, blk, H.lds, stream, dev_plan, S);
+      break;
+    case MODE_F64:
+      if (one) hipLaunchKernelGGL((layer_kernel<MODE_F64, 1>), g, blk, H.lds, stream, dev_plan, S);
+      else hipLaunchKernelGGL((layer_kernel<MODE_F64, 8>), g, blk, H.lds, stream, dev_plan, S);
+      break;
+    default:
+      if (one) hipLaunchKernelGGL((layer_kernel<MODE_Q8, 1>), g, blk, H.lds, stream, dev_plan, S);
+      else hipLaunchKernelGGL((layer_kernel<MODE_Q8, 8>), g, blk, H.lds, stream, dev_plan, S);
+      break;
+  }
+  if (hipGetLastError() != hipSuccess) return FR_HIP_IO;
+  E.last_parity = E.parity;
+  E.parity ^= 1u;
+  return FR_HIP_OK;
+}
+
+#define CK(x) do { if ((x) != hipSuccess) return FR_HIP_IO; } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int fr_hip_probe(int device, char* arch, size_t cap) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return FR_HIP_UNSUPPORTED;
+  hipDeviceProp_t p;
+  if (hipGetDeviceProperties(&p, device) != hipSuccess) return FR_HIP_UNSUPPORTED;
+  if (arch && cap) snprintf(arch, cap, "%s", p.gcnArchName);
+  return strncmp(p.gcnArchName, "gfx950", 6) ? FR_HIP_UNSUPPORTED : FR_HIP_OK;
+}
+
+uint64_t fr_hip_unit_bytes(unsigned hidden, unsigned format) {
+  Layout l;
+  return layout_of(hidden, format, l) ? l.block : 0;
+}
+
+int fr_hip_open(int device) {
+  if (g_open) return E.device == device ? FR_HIP_OK : FR_HIP_STATE;
+  int rc = fr_hip_probe(device, nullptr, 0);
+  if (rc) return rc;
+  CK(hipSetDevice(device));
+  E = Engine();
+  E.device = device;
+  CK(hipStreamCreateWithFlags(&E.stream, hipStreamNonBlocking));
+  CK(hipMalloc(&E.done, 2 * kMaxPairs * sizeof(uint32_t)));
+  CK(hipMalloc(&E.fin, 2 * kMaxRanges * sizeof(uint32_t)));
+  CK(hipMalloc(&E.hbuf, (size_t)kMaxPairs * kMaxBurst * kNeurons * sizeof(float)));
+  // Worst case groups: every pair its own group.
+  E.partial_bytes = (size_t)kMaxPairs * kMaxBurst * kMaxHidden * sizeof(double) / 4;
+  CK(hipMalloc(&E.partial, E.partial_bytes));
+  E.out_words = 4 + kMaxBurst * kMaxHidden;
+  CK(hipMalloc(&E.out, 2 * (size_t)E.out_words * sizeof(uint32_t)));
+  CK(hipMemset(E.done, 0, 2 * kMaxPairs * sizeof(uint32_t)));
+  CK(hipMemset(E.fin, 0, 2 * kMaxRanges * sizeof(uint32_t)));
+  CK(hipMemset(E.out, 0, 2 * (size_t)E.out_words * sizeof(uint32_t)));
+  E.plan_cap = plan_capacity(kMaxBurst, kMaxHidden);
+  CK(hipMalloc(&E.plan_dev, E.plan_cap));
+  CK(hipHostMalloc(reinterpret_cast<void**>(&E.plan_host), E.plan_cap, hipHostMallocDefault));
+  CK(hipHostMalloc(reinterpret_cast<void**>(&E.out_host), (size_t)E.out_words * sizeof(uint32_t), hipHostMallocDefault));
+  CK(hipEventCreate(&E.ev0));
+  CK(hipEventCreate(&E.ev1));
+  CK(hipDeviceSynchronize());
+  g_open = true;
+  return FR_HIP_OK;
+}
+
+int fr_hip_close(void) {
+  if (!g_open) return FR_HIP_OK;
+  for (int b = 0; b < kBlocks; ++b)
+    if (E.block[b]) return FR_HIP_STATE;
+  (void)hipSetDevice(E.device);
+  (void)hipStreamSynchronize(E.stream);
+  (void)hipFree(E.done);
+  (void)hipFree(E.fin);
+  (void)hipFree(E.hbuf);
+  (void)hipFree(E.partial);
+  (void)hipFree(E.out);
+  (void)hipFree(E.plan_dev);
+  (void)hipFree(E.staging);
+  (void)hipHostFree(E.plan_host);
+  (void)hipHostFree(E.out_host);
+  (void)hipEventDestroy(E.ev0);
+  (void)hipEventDestroy(E.ev1);
+  (void)hipStreamDestroy(E.stream);
+  E = Engine();
+  g_open = false;
+  return FR_HIP_OK;
+}
+
+static int ensure_staging(size_t bytes) {
+  if (E.staging_bytes >= bytes) return FR_HIP_OK;
+  if (E.staging) (void)hipFree(E.staging);
+  E.staging = nullptr;
+  E.staging_bytes = 0;
+  CK(hipMalloc(&E.staging, bytes));
+  E.staging_bytes = bytes;
+  return FR_HIP_OK;
+}
+
+// Copy slices [first, first+n) of a unit (native bytes at `unit`) into
+// block `b`, re-tiled. Slices are consecutive in the unit layout.
+static int upload_slices(int b, const uint8_t* unit, uint32_t first, uint32_t n) {
+  const Layout& l = E.lay[b];
+  uint32_t layer0 = first / 513;
+  uint64_t off0 = (uint64_t)layer0 * l.layer + (uint64_t)(first % 513) * l.slice;
+  uint32_t last = first + n - 1;
+  uint64_t off1 = (uint64_t)(last / 513) * l.layer + (uint64_t)(last % 513) * l.slice +
+                  ((last % 513) == (uint32_t)kShared ? l.shared_slice : l.slice);
+  uint64_t bytes = off1 - off0;
+  int rc = ensure_staging(bytes);
+  if (rc) return rc;
+  CK(hipMemcpyAsync(E.staging, unit + off0, bytes, hipMemcpyHostToDevice, E.stream));
+  // retile_kernel addresses slices relative to layer 0 of `src`/`dst`.
+  hipLaunchKernelGGL(retile_kernel, dim3(n), dim3(256), 0, E.stream, E.staging - off0, E.block[b],
+                     shape_of(l, false), shape_of(l, true), l.layer, first, n);
+  CK(hipGetLastError());
+  CK(hipStreamSynchronize(E.stream));
+  return FR_HIP_OK;
+}
+
+int fr_hip_upload(unsigned block, const void* unit, uint64_t len, unsigned hidden, unsigned format) {
+  if (!g_open) return FR_HIP_STATE;
+  if (block >= (unsigned)kBlocks || !unit) return FR_HIP_INVALID;
+  Layout l;
+  if (!layout_of(hidden, format, l) || len != l.block) return FR_HIP_INVALID;
+  if (E.block[block]) return FR_HIP_STATE;
+  CK(hipSetDevice(E.device));
+  uint8_t* dev = nullptr;
+  if (hipMalloc(&dev, l.block) != hipSuccess) return FR_HIP_IO;
+  E.block[block] = dev;
+  E.lay[block] = l;
+  const uint8_t* src = static_cast<const uint8_t*>(unit);
+  // Two layers per step bound the staging buffer.
+  for (uint32_t layer = 0; layer < (uint32_t)kLayers; layer += 2) {
+    uint32_t nl = layer + 2 <= (uint32_t)kLayers ? 2 : 1;
+    int rc = upload_slices((int)block, src, layer * 513, nl * 513);
+    if (rc) {
+      (void)hipFree(dev);
+      E.block[block] = nullptr;
+      return rc;
+    }
+  }
+  return FR_HIP_OK;
+}
+
+int fr_hip_reserve(unsigned block, unsigned hidden, unsigned format) {
+  if (!g_open) return FR_HIP_STATE;
+  if (block >= (unsigned)kBlocks) return FR_HIP_INVALID;
+  Layout l;
+  if (!layout_of(hidden, format, l)) return FR_HIP_INVALID;
+  if (E.block[block]) return FR_HIP_STATE;
+  CK(hipSetDevice(E.device));
+  uint8_t* dev = nullptr;
+  if (hipMalloc(&dev, l.block) != hipSuccess) return FR_HIP_IO;
+  if (hipMemsetAsync(dev, 0, l.block, E.stream) != hipSuccess || hipStreamSynchronize(E.stream) != hipSuccess) {
+    (void)hipFree(dev);
+    return FR_HIP_IO;
+  }
+  E.block[block] = dev;
+  E.lay[block] = l;
+  return FR_HIP_OK;
+}
+
+int fr_hip_refresh(unsigned block, const void* unit, unsigned layer, unsigned expert) {
+  if (!g_open) return FR_HIP_STATE;
+  if (block >= (unsigned)kBlocks || !unit || layer >= (unsigned)kLayers || expert > (unsigned)kShared)
+    return FR_HIP_INVALID;
+  if (!E.block[block]) return FR_HIP_STATE;
+  CK(hipSetDevice(E.device));
+  return upload_slices((int)block, static_cast<const uint8_t*>(unit), layer * 513 + expert, 1);
+}
+
+int fr_hip_release(unsigned block) {
+  if (block >= (unsigned)kBlocks) return FR_HIP_INVALID;
+  if (!g_open || !E.block[block]) return FR_HIP_STATE;
+  (void)hipSetDevice(E.device);
+  (void)hipStreamSynchronize(E.stream);
+  (void)hipFree(E.block[block]);
+  E.block[block] = nullptr;
+  return FR_HIP_OK;
+}
+
+size_t fr_hip_plan_bytes(unsigned burst, unsigned hidden) { return plan_capacity(burst, hidden); }
+
+int fr_hip_plan(const fr_hip_request* req, void* plan, size_t cap, size_t* used, unsigned* grid) {
+  if (!g_open) return FR_HIP_STATE;
+  return build_plan(req, static_cast<uint8_t*>(plan), cap, used, grid);
+}
+
+int fr_hip_launch(const void* host_plan, const void* device_plan, void* stream) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!host_plan || !device_plan) return FR_HIP_INVALID;
+  const PlanHeader& H = *static_cast<const PlanHeader*>(host_plan);
+  if (!H.burst || H.burst > (unsigned)kMaxBurst || !H.ntA || !H.ntB) return FR_HIP_INVALID;
+  return launch(static_cast<const uint8_t*>(device_plan), H, H.ntA + H.ntB,
+                stream ? static_cast<hipStream_t>(stream) : E.stream);
+}
+
+int fr_hip_last_output(void* stream, float* y, size_t count, unsigned* status) {
+  if (!g_open) return FR_HIP_STATE;
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : E.stream;
+  if (count > (size_t)kMaxBurst * kMaxHidden) return FR_HIP_INVALID;
+  CK(hipStreamSynchronize(s));
+  const uint32_t* src = E.out + (size_t)E.last_parity * E.out_words;
+  CK(hipMemcpy(E.out_host, src, (4 + count) * sizeof(uint32_t), hipMemcpyDeviceToHost));
+  if (status) *status = E.out_host[0];
+  if (y) memcpy(y, E.out_host + 4, count * sizeof(float));
+  return FR_HIP_OK;
+}
+
+int fr_hip_run(const fr_hip_request* req, float* y) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!req || !y) return FR_HIP_INVALID;
+  CK(hipSetDevice(E.device));
+  size_t used = 0;
+  unsigned grid = 0;
+  int rc = build_plan(req, E.plan_host, E.plan_cap, &used, &grid);
+  if (rc) return rc;
+  const PlanHeader& H = *reinterpret_cast<const PlanHeader*>(E.plan_host);
+  CK(hipMemcpyAsync(E.plan_dev, E.plan_host, used, hipMemcpyHostToDevice, E.stream));
+  CK(hipEventRecord(E.ev0, E.stream));
+  rc = launch(E.plan_dev, H, grid, E.stream);
+  if (rc) return rc;
+  CK(hipEventRecord(E.ev1, E.stream));
+  const size_t count = (size_t)H.burst * H.hidden;
+  const uint32_t* src = E.out + (size_t)E.last_parity * E.out_words;
+  CK(hipMemcpyAsync(E.out_host, src, (4 + count) * sizeof(uint32_t), hipMemcpyDeviceToHost, E.stream));
+  CK(hipStreamSynchronize(E.stream));
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, E.ev0, E.ev1) == hipSuccess) E.sample.last_kernel_ns = ms * 1e6;
+  ++E.sample.runs;
+  uint32_t status = E.out_host[0];
+  if (status & kErrTimeout) return FR_HIP_IO;
+  if (status) return FR_HIP_NUMERIC;
+  memcpy(y, E.out_host + 4, count * sizeof(float));
+  return FR_HIP_OK;
+}
+
+int fr_hip_sample_get(fr_hip_sample* out) {
+  if (!out) return FR_HIP_INVALID;
+  *out = E.sample;
+  return FR_HIP_OK;
+}
+
+static int debug_upload(const void* bytes, size_t n, uint8_t** dev) {
+  CK(hipMalloc(dev, n ? n : 1));
+  CK(hipMemcpy(*dev, bytes, n, hipMemcpyHostToDevice));
+  return FR_HIP_OK;
+}
+
+int fr_hip_debug_dequant(unsigned type, const void* row, unsigned n, float* out) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!row || !out || !n || n % 64 || n > (unsigned)kMaxHidden) return FR_HIP_INVALID;
+  if (type != TQ4_K && type != TQ8_0 && type != TMXFP4 && type != TQ4_0) return FR_HIP_INVALID;
+  if (type == TQ4_K && n % 256) return FR_HIP_INVALID;
+  CK(hipSetDevice(E.device));
+  // Re-tile the row as row 0 of a gate block of a one-slice layout.
+  size_t rb = row_bytes(type, n);
+  uint8_t *src = nullptr, *dst = nullptr;
+  float* dout = nullptr;
+  uint32_t* st = nullptr;
+  int rc = debug_upload(row, rb, &src);
+  if (rc) return rc;
+  CK(hipMalloc(&dst, rb));
+  CK(hipMalloc(&dout, n * sizeof(float)));
+  CK(hipMalloc(&st, sizeof(uint32_t)));
+  CK(hipMemset(st, 0, sizeof(uint32_t)));
+  SliceShape s = {n, type, TQ8_0, (uint32_t)rb * kNeurons, 0, (uint32_t)rb};
+  // Gather through the same re-tile mapping, one row only.
+  hipLaunchKernelGGL(debug_retile_row, dim3(1), dim3(256), 0, E.stream, s, src, dst, (uint32_t)rb);
+  hipLaunchKernelGGL(debug_decode_rows, dim3(1), dim3(64), 0, E.stream, (uint8_t)type, dst, n, dout, st);
+  CK(hipGetLastError());
+  CK(hipStreamSynchronize(E.stream));
+  uint32_t status = 0;
+  CK(hipMemcpy(out, dout, n * sizeof(float), hipMemcpyDeviceToHost));
+  CK(hipMemcpy(&status, st, sizeof(status), hipMemcpyDeviceToHost));
+  (void)hipFree(src);
+  (void)hipFree(dst);
+  (void)hipFree(dout);
+  (void)hipFree(st);
+  return status ? FR_HIP_NUMERIC : FR_HIP_OK;
+}
+
+int fr_hip_debug_dequant_down(unsigned format, const void* down, unsigned hidden, float* out) {
+  if (!g_open) return FR_HIP_STATE;
+  Layout l;
+  if (!down || !out || !layout_of(hidden, format, l)) return FR_HIP_INVALID;
+  CK(hipSetDevice(E.device));
+  uint8_t *src = nullptr, *dst = nullptr;
+  float* dout = nullptr;
+  uint32_t* st = nullptr;
+  int rc = debug_upload(down, l.down, &src);
+  if (rc) return rc;
+  CK(hipMalloc(&dst, l.down));
+  CK(hipMalloc(&dout, (size_t)hidden * 32 * sizeof(float)));
+  CK(hipMalloc(&st, sizeof(uint32_t)));
+  CK(hipMemset(st, 0, sizeof(uint32_t)));
+  hipLaunchKernelGGL(debug_retile_down, dim3(1), dim3(256), 0, E.stream, (uint8_t)l.dn, hidden, src, dst, (uint32_t)l.down);
+  unsigned threads = l.dn == TQ4_KT ? hidden / 256 * 64 : hidden;
+  hipLaunchKernelGGL(debug_decode_down, dim3((threads + 255) / 256), dim3(256), 0, E.stream, (uint8_t)l.dn, dst,
+                     hidden, dout, st);
+  CK(hipGetLastError());
+  CK(hipStreamSynchronize(E.stream));
+  uint32_t status = 0;
+  CK(hipMemcpy(out, dout, (size_t)hidden * 32 * sizeof(float), hipMemcpyDeviceToHost));
+  CK(hipMemcpy(&status, st, sizeof(status), hipMemcpyDeviceToHost));
+  (void)hipFree(src);
+  (void)hipFree(dst);
+  (void)hipFree(dout);
+  (void)hipFree(st);
+  return status ? FR_HIP_NUMERIC : FR_HIP_OK;
+}
+
+int fr_hip_debug_quantize(const float* x, unsigned n, float* out) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!x || !out || !n || (n % 64 && n != 32)) return FR_HIP_INVALID;
+  CK(hipSetDevice(E.device));
+  float* d = nullptr;
+  CK(hipMalloc(&d, n * sizeof(float)));
+  CK(hipMemcpy(d, x, n * sizeof(float), hipMemcpyHostToDevice));
+  if (n == 32) hipLaunchKernelGGL(debug_quantize32, dim3(1), dim3(64), 0, E.stream, d, 1u);
+  else hipLaunchKernelGGL(debug_quantize, dim3((n / 64 + 63) / 64), dim3(64), 0, E.stream, d, n / 64);
+  CK(hipGetLastError());
+  CK(hipStreamSynchronize(E.stream));
+  CK(hipMemcpy(out, d, n * sizeof(float), hipMemcpyDeviceToHost));
+  (void)hipFree(d);
+  return FR_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,117 @@
+/* fronk_hip.h - C ABI of libfronk_hip.so, the MI355X (gfx950) expert-slice engine.
+ *
+ * The reference's backend plugin API is the fr_backend vtable
+ * (src/backend.h:52-67). Its hot path, run() for expert neuron slices, is
+ * implemented here as HIP kernels; fronk_amd/host/hip.c is the drop-in vtable
+ * ("hip", next to ref/avx2/neon/metal) that calls these entry points. Only C
+ * types cross this boundary: plain pointers, sizes and int return codes that
+ * use the reference's FR_* values (src/backend.h:17-18).
+ *
+ * All calls are synchronous with respect to the host unless noted, and are
+ * externally serialized per process like the vtable (src/backend.h:2).
+ */
+#ifndef FRONK_HIP_H
+#define FRONK_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes: the reference's values (src/backend.h:17-18). */
+enum { FR_HIP_OK = 0, FR_HIP_INVALID = -1, FR_HIP_STATE = -2, FR_HIP_NUMERIC = -3,
+       FR_HIP_IO = -4, FR_HIP_UNSUPPORTED = -5 };
+
+/* Unit formats. LEGACY is the Q4_0 ownership block (src/backend.h:37-50) and
+ * NATIVE the lossless GGUF unit (src/native.h:1-15: routed Q4_K gate/up, MXFP4
+ * down [H x 32], shared Q8_0). Q4KT, Q8 and MXFP4 are the same unit with every
+ * routed projection Q4_K (down stored transposed [32 x H]), Q8_0 or MXFP4. */
+enum { FR_HIP_FMT_LEGACY = 0, FR_HIP_FMT_NATIVE = 1, FR_HIP_FMT_Q4KT = 2,
+       FR_HIP_FMT_Q8 = 3, FR_HIP_FMT_MXFP4 = 4 };
+
+/* Arithmetic modes of run().
+ * F32: fp32 activations, fp32 dot products, fp64 accumulation over experts
+ *      and blocks; parity with `ref` (backends/ref.c:124) at 1e-5 rel. L2.
+ * F64: fp32 activations, exactly decoded weights, fp64 dot products: the
+ *      arithmetic of `ref` (backends/ref.c:57-98) up to summation order.
+ * Q8:  `ref-q8` (backends/ref.c:125): x and each slice's h quantized by the
+ *      reference quantizer (src/q4.c:37-61), bit-exact, with fp64 dots. */
+enum { FR_HIP_MODE_F32 = 0, FR_HIP_MODE_F64 = 1, FR_HIP_MODE_Q8 = 2 };
+
+/* ggml type ids accepted by the debug decoders (src/native.h:8). */
+enum { FR_HIP_Q4_0 = 2, FR_HIP_Q8_0 = 8, FR_HIP_Q4_K = 12, FR_HIP_MXFP4 = 39 };
+
+/* One layer request of 1..8 tokens; the fields of fr_req
+ * (src/backend.h:20-25) with the hidden size as a parameter. */
+typedef struct {
+    unsigned layer, burst, hidden, mode;
+    const uint16_t *expert;  /* [burst][10] distinct routed ids < 512 */
+    const float *gate;       /* [burst][11], index 10 = shared expert 512 */
+    const float *x;          /* [burst][hidden] */
+} fr_hip_request;
+
+/* Counters in the spirit of fr_avx2_sample (src/avx2.h:11-15). */
+typedef struct {
+    uint64_t runs, weight_bytes, hot_allocations;
+    unsigned blocks, unique_experts, pairs, grid;
+    double last_kernel_ns;
+} fr_hip_sample;
+
+/* Device setup and teardown. Replaces the lazy pool setup of load
+ * (backends/avx2.c:561-607, backends/metal.m:370-373). Returns
+ * FR_HIP_UNSUPPORTED when `device` is not a gfx950 GPU. */
+int fr_hip_open(int device);
+int fr_hip_close(void);
+/* Name of the open device's architecture ("gfx950"), for probe(). */
+int fr_hip_probe(int device, char *arch, size_t cap);
+
+/* Copy a whole 48-layer unit to HBM and re-tile it for the kernels
+ * (load: src/backend.h:55-61; layout src/native.h:9-21). `len` must equal the
+ * unit size of (`hidden`, `format`). */
+int fr_hip_upload(unsigned block, const void *unit, uint64_t len, unsigned hidden, unsigned format);
+/* Allocate a zero-filled device unit without copying (the slices are then
+ * written with fr_hip_refresh). For sparse fixtures and device-side data. */
+int fr_hip_reserve(unsigned block, unsigned hidden, unsigned format);
+/* Re-read one (layer, expert) slice of a loaded block from `unit`, the
+ * borrowed host bytes, so that run() sees later host-side changes
+ * (src/native.c:118-130 mutates the unit after load). */
+int fr_hip_refresh(unsigned block, const void *unit, unsigned layer, unsigned expert);
+/* Free one block's device copy (unload: src/backend.h:62). */
+int fr_hip_release(unsigned block);
+/* Unit bytes of a (hidden, format) pair, 0 if unsupported. */
+uint64_t fr_hip_unit_bytes(unsigned hidden, unsigned format);
+
+/* The hot path (run: src/backend.h:63, backends/ref.c:57-98): H2D of x and
+ * the launch plan, ONE kernel launch over every (expert, owned slice) pair,
+ * D2H of y. y receives burst*hidden floats only on success. Request
+ * validation is the caller's (backends/ref.c:41-56); this checks shapes. */
+int fr_hip_run(const fr_hip_request *req, float *y);
+
+/* Resident-input path for timing: build the plan (and x) into host memory,
+ * copy it to device memory the caller owns, then enqueue launches on
+ * `stream` (a hipStream_t; NULL = the library stream). The host copy gives
+ * the launch shape; the device copy is what the kernel reads. `cap` must be
+ * at least fr_hip_plan_bytes(burst, hidden). */
+size_t fr_hip_plan_bytes(unsigned burst, unsigned hidden);
+int fr_hip_plan(const fr_hip_request *req, void *plan, size_t cap, size_t *used, unsigned *grid);
+int fr_hip_launch(const void *host_plan, const void *device_plan, void *stream);
+/* Wait for `stream` and copy the last launch's status word and y
+ * (burst*hidden floats) to the host. */
+int fr_hip_last_output(void *stream, float *y, size_t count, unsigned *status);
+
+int fr_hip_sample_get(fr_hip_sample *out);
+
+/* Parity hooks (no reference counterpart): the hot path's own device
+ * decoder and quantizer on caller data, for bit-exact checks against the
+ * reference's fr_native_dot decode (src/native.c:13-31) and fr_q8_activation
+ * (src/q4.c:37-61). `row` is one native row of n weights. */
+int fr_hip_debug_dequant(unsigned type, const void *row, unsigned n, float *out);
+/* Down matrix of one slice, native bytes, decoded to [hidden][32] floats
+ * (element (d, n) = weight of neuron n for output d) for every down format. */
+int fr_hip_debug_dequant_down(unsigned format, const void *down, unsigned hidden, float *out);
+int fr_hip_debug_quantize(const float *x, unsigned n, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

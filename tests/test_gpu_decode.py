@@ -1,0 +1,108 @@
+"""Bit-exact decode and quantization on the GPU.
+
+The device decoder that the fp64 and q8 paths use (and that the re-tiled
+layout feeds) must reproduce the reference's per-weight decode
+(src/native.c:13-31, src/q4.c:29-31) bit for bit, and the device activation
+quantizer must reproduce fr_q8_activation (src/q4.c:37-61) bit for bit.
+"""
+import numpy as np
+import pytest
+
+import fronk_amd as fa
+import oracle
+from fixtures import baseline_row
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def eng():
+    return fa.Engine(0)
+
+
+def special_row(rng, typ, n):
+    """Random row with the edge scales the reference tests: subnormal and zero
+    fp16 scales, negative scales, E8M0 0 (2^-127) and 254."""
+    per, size = {oracle.Q4_K: (256, 144), oracle.Q8_0: (32, 34), oracle.MXFP4: (32, 17), oracle.Q4_0: (32, 18)}[typ]
+    b = baseline_row(rng, typ, n).reshape(-1, size)
+    nb = b.shape[0]
+    if typ == oracle.MXFP4:
+        b[0, 0], b[1 % nb, 0] = 0, 254
+    else:
+        b[0, 0:2] = [0x01, 0x00]          # smallest subnormal
+        b[1 % nb, 0:2] = [0x00, 0x80]     # -0
+        b[2 % nb, 0:2] = [0xff, 0x83]     # negative subnormal
+        b[3 % nb, 0:2] = [0x00, 0x7b]     # large finite
+        if typ == oracle.Q4_K:
+            b[0, 2:4] = [0xff, 0x03]
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("typ", [oracle.Q4_K, oracle.Q8_0, oracle.MXFP4, oracle.Q4_0])
+@pytest.mark.parametrize("n", [2560, 4096])
+def test_dequant_rows_bit_exact(eng, typ, n):
+    rng = np.random.default_rng(typ * 100 + n)
+    for trial in range(3):
+        row = special_row(rng, typ, n) if trial else baseline_row(rng, typ, n)
+        rc, got = eng.dequant(typ, row, n)
+        assert rc == fa.OK
+        want = oracle.dequant(row, typ, n)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (typ, n, trial)
+
+
+@pytest.mark.parametrize("typ", [oracle.Q4_K, oracle.Q8_0, oracle.MXFP4, oracle.Q4_0])
+def test_dequant_rejects_nonfinite_scale(eng, typ):
+    rng = np.random.default_rng(5)
+    row = baseline_row(rng, typ, 4096)
+    if typ == oracle.MXFP4:
+        row[17 * 5] = 255
+    else:
+        row[1] = 0x7c
+    rc, _ = eng.dequant(typ, row, 4096)
+    assert rc == fa.NUMERIC
+
+
+@pytest.mark.parametrize("fmt,hidden", [(oracle.FMT_NATIVE, 2560), (oracle.FMT_NATIVE, 4096),
+                                        (oracle.FMT_Q4KT, 4096), (oracle.FMT_Q8, 4096),
+                                        (oracle.FMT_MXFP4, 4096), (oracle.FMT_LEGACY, 2560)])
+def test_dequant_down_bit_exact(eng, fmt, hidden):
+    lay = oracle.layout(hidden, fmt)
+    rng = np.random.default_rng(fmt * 7 + hidden)
+    if lay.down_transposed:
+        rows = [baseline_row(rng, lay.down_type, hidden) for _ in range(32)]
+        down = np.concatenate(rows)
+        rowb = len(rows[0])
+        want = np.stack([oracle.dequant(down[n * rowb:(n + 1) * rowb], lay.down_type, hidden) for n in range(32)]).T
+    else:
+        down = baseline_row(rng, lay.down_type, 32 * hidden)
+        rowb = down.size // hidden
+        want = np.stack([oracle.dequant(down[d * rowb:(d + 1) * rowb], lay.down_type, 32) for d in range(hidden)])
+    rc, got = eng.dequant_down(fmt, down, hidden)
+    assert rc == fa.OK
+    assert np.array_equal(np.ascontiguousarray(got).view(np.uint32), np.ascontiguousarray(want).view(np.uint32))
+
+
+def test_quantize_bit_exact(eng):
+    rng = np.random.default_rng(3)
+    cases = [rng.standard_normal(4096).astype(np.float32),
+             (rng.standard_normal(4096) * 1e-30).astype(np.float32),
+             (rng.standard_normal(4096) * 1e30).astype(np.float32),
+             np.zeros(4096, np.float32)]
+    ties = np.zeros(4096, np.float32)
+    ties[:7] = [127, .5, 1.5, 2.5, -.5, -1.5, -2.5]
+    ties[64:66] = [254, 3]
+    ties[128] = np.finfo(np.float32).max
+    ties[192] = 2.0 ** -149
+    ties[256] = 2.0 ** -125
+    cases.append(ties)
+    for x in cases:
+        rc, got = eng.quantize(x)
+        assert rc == fa.OK
+        rc, want = oracle.q8_activation(x)
+        assert rc == 0
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # The 32-value hidden-slice form.
+    for x in [rng.standard_normal(32).astype(np.float32) * 1e4, ties[:32].copy()]:
+        rc, got = eng.quantize(x)
+        assert rc == fa.OK
+        assert np.array_equal(got.view(np.uint32), oracle.q8_activation(x)[1].view(np.uint32))

@@ -1,0 +1,175 @@
+"""End-to-end parity of the single-launch layer kernel with the oracle.
+
+Every test runs the HIP path through the C ABI (fr_hip_run) and compares it
+with the restated reference run() (backends/ref.c:57-98) on the same bytes.
+Tolerances (per token, fr_compare metrics of src/backend.c:74-92):
+  F32 mode vs ref     relative L2 <= 1e-5 and normalized max <= 1e-3
+  F64 mode vs ref     relative L2 <= 1e-9 (fp64 arithmetic, other order)
+  Q8  mode vs ref-q8  relative L2 <= 1e-9 (bit-exact quantizers, fp64)
+"""
+import numpy as np
+import pytest
+
+import fronk_amd as fa
+import oracle
+from fixtures import (fill_experts, native_fixture, oracle_request, softmax_gates, sparse_unit, zipf_routes)
+
+pytestmark = pytest.mark.gpu
+
+TOL = {fa.MODE_F32: (1e-5, 1e-3), fa.MODE_F64: (1e-9, 1e-8), fa.MODE_Q8: (1e-9, 1e-8)}
+
+
+@pytest.fixture(scope="module")
+def eng():
+    e = fa.Engine(0)
+    yield e
+    for b in range(20):
+        e.release(b)
+
+
+def check_close(ref, got, mode, what=""):
+    l2, mx = TOL[mode]
+    for t in range(ref.shape[0]):
+        rc, err = oracle.compare(ref[t], got[t])
+        assert rc == 0, what
+        assert err[0] <= l2 and err[1] <= mx, (what, t, err)
+
+
+def run_both(eng, blocks, fmt, layer, experts, gates, x, mode):
+    rc, y = eng.run(layer, experts, gates, x, mode)
+    assert rc == fa.OK, (rc, mode)
+    req = oracle_request(layer, experts, gates, x)
+    rc, ref = oracle.ref_run(blocks, fmt, mode == fa.MODE_Q8, req)
+    assert rc == 0
+    return ref, y
+
+
+@pytest.fixture(scope="module")
+def native2560(eng):
+    """The reference native self-test fixture at H=2560 in block 19."""
+    lay = oracle.layout(2560, oracle.FMT_NATIVE)
+    data, gates, x = native_fixture(lay)
+    assert eng.upload(19, data, 2560, fa.FMT_NATIVE) == fa.OK
+    blocks = [None] * 20
+    blocks[19] = data
+    yield lay, data, gates, x, blocks
+    assert eng.release(19) == fa.OK
+
+
+@pytest.mark.parametrize("mode", [fa.MODE_F32, fa.MODE_F64, fa.MODE_Q8])
+def test_native_fixture_all_bursts(eng, native2560, mode):
+    """fr_native_self_test's request grid (src/native.c:77-93): distinct and
+    reused routing, bursts 1..8, shared expert at gate 0.5."""
+    lay, data, gates, x, blocks = native2560
+    for reuse in (0, 1):
+        for burst in range(1, 9):
+            experts = np.array([[e + (0 if reuse else t * 10) for e in range(10)] for t in range(burst)])
+            ref, y = run_both(eng, blocks, oracle.FMT_NATIVE, 47, experts, gates[:burst], x[:burst], mode)
+            check_close(ref, y, mode, (reuse, burst))
+
+
+def test_native_fixture_deterministic_and_burst_invariant(eng, native2560):
+    lay, data, gates, x, blocks = native2560
+    experts = np.array([[e + t * 3 for e in range(10)] for t in range(8)])
+    rc, y8 = eng.run(47, experts, gates, x, fa.MODE_F32)
+    assert rc == fa.OK
+    rc, again = eng.run(47, experts, gates, x, fa.MODE_F32)
+    assert np.array_equal(y8.view(np.uint32), again.view(np.uint32)), "run-to-run bits differ"
+    same = 0
+    for t in range(8):
+        rc, y1 = eng.run(47, experts[t:t + 1], gates[t:t + 1], x[t:t + 1], fa.MODE_F32)
+        assert rc == fa.OK
+        same += np.array_equal(y1[0].view(np.uint32), y8[t].view(np.uint32))
+        check_close(y1, y8[t:t + 1], fa.MODE_F32)
+    # fp64 accumulation over pairs: a burst differs from T=1 only in summation
+    # order, so nearly every token is bit-identical.
+    assert same >= 6
+
+
+def test_native_error_paths(eng, native2560):
+    lay, data, gates, x, blocks = native2560
+    experts = np.arange(10).reshape(1, 10)
+    rc, y = eng.run(47, experts, gates[:1], np.full((1, 2560), np.finfo(np.float32).max, np.float32))
+    assert rc == fa.NUMERIC
+    for off, val in [(oracle.slice_offset(lay, 47, 0) + 1, 0x7C),
+                     (oracle.slice_offset(lay, 47, 0) + 2 * lay.proj, 255),
+                     (oracle.slice_offset(lay, 47, 512) + 1, 0x7C)]:
+        saved = data[off]
+        data[off] = val
+        layer, expert = 47, (512 if off >= oracle.slice_offset(lay, 47, 512) else 0)
+        assert eng.refresh(19, data, layer, expert) == fa.OK
+        rc, _ = eng.run(47, experts, gates[:1], x[:1])
+        assert rc == fa.NUMERIC, off
+        data[off] = saved
+        assert eng.refresh(19, data, layer, expert) == fa.OK
+    rc, _ = eng.run(47, experts, gates[:1], x[:1])
+    assert rc == fa.OK
+
+
+@pytest.mark.parametrize("fmt", [fa.FMT_Q4KT, fa.FMT_Q8, fa.FMT_MXFP4, fa.FMT_NATIVE])
+def test_h4096_baseline_distributions(eng, fmt):
+    """Measurement-config weights at H=4096: 10 experts of 512, softmax gates,
+    x ~ N(0,1), two owned blocks, T=1 and a Zipf T=4 burst."""
+    lay = oracle.layout(4096, fmt)
+    rng = np.random.default_rng(100 + fmt)
+    layer = 5
+    experts1 = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+    experts4 = zipf_routes(rng, 4)
+    used = sorted(set(experts1.ravel()) | set(experts4.ravel()))
+    units = {}
+    for b in (3, 17):
+        u = sparse_unit(lay)
+        fill_experts(u, lay, layer, used, seed=b * 1000 + fmt)
+        assert eng.load_sparse(b, u, 4096, fmt, [(layer, e) for e in used]) == fa.OK
+        units[b] = u
+    blocks = [units.get(b) for b in range(20)]
+    try:
+        for experts in (experts1, experts4):
+            T = experts.shape[0]
+            gates = np.zeros((T, 11), np.float32)
+            gates[:, :10] = softmax_gates(rng, T)
+            x = rng.standard_normal((T, 4096)).astype(np.float32)
+            for mode in (fa.MODE_F32, fa.MODE_F64, fa.MODE_Q8):
+                ref, y = run_both(eng, blocks, fmt, layer, experts, gates, x, mode)
+                check_close(ref, y, mode, (fmt, T, mode))
+    finally:
+        for b in units:
+            assert eng.release(b) == fa.OK
+
+
+def test_legacy_golden_corpus(eng):
+    """The reference's committed golden partials (tests/vectors/*) through the
+    GPU legacy Q4_0 path: F64 within the reference reproducibility tolerance,
+    F32 within the measurement tolerance."""
+    import ctypes as C
+    import os
+    from test_oracle_golden import build_vector, golden_values, GOLDEN
+    for index in range(8):
+        req, mask, name, blocks, _ = build_vector(index)
+        loaded = []
+        used = sorted(set(int(e) for e in req.experts()[:req.burst].ravel()) | {512})
+        for b in range(20):
+            if blocks[b] is not None:
+                # Only the fixture's slices are materialized: copy just those.
+                assert eng.load_sparse(b, blocks[b], 2560, fa.FMT_LEGACY, [(req.layer, e) for e in used]) == fa.OK
+                loaded.append(b)
+        try:
+            _, gold = golden_values(os.path.join(GOLDEN, name + ".txt"), req.burst)
+            T = req.burst
+            experts = req.experts()[:T]
+            gates = req.gates()[:T]
+            x = req.xs()[:T, :2560]
+            for mode, limit in [(fa.MODE_F64, oracle.REFERENCE_TOLERANCE), (fa.MODE_F32, (1e-5, 1e-3, 0.9999))]:
+                rc, y = eng.run(req.layer, experts, gates, x, mode)
+                assert rc == fa.OK
+                for t in range(T):
+                    rc, err = oracle.compare(gold[t], y[t])
+                    assert rc == 0 and oracle.conforms(err, limit), (name, mode, t, err)
+        finally:
+            for b in loaded:
+                assert eng.release(b) == fa.OK
+
+
+def test_state_errors(eng):
+    rc, _ = eng.run(0, np.arange(10).reshape(1, 10), np.zeros((1, 11), np.float32), np.zeros((1, 4096), np.float32))
+    assert rc == fa.STATE
