@@ -29,6 +29,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <cmath>
+
 #include "fronk_hip.h"
 
 namespace {
@@ -47,7 +49,7 @@ constexpr int kCols = 256;            // output dims per phase-B task
 constexpr int kMaxHidden = 4096;
 constexpr int kMaxRanges = kMaxHidden / kCols;
 constexpr int kLdsLimit = 64 * 1024;
-constexpr uint32_t kSpinLimit = 1u << 21;
+constexpr uint32_t kSpinLimit = 1u << 16;   // about 0.1 s of polling
 
 // Status bits of the output word.
 constexpr uint32_t kErrScale = 1;     // referenced non-finite scale
@@ -80,7 +82,7 @@ struct PlanHeader {
 static_assert(sizeof(PlanHeader) == 64, "header layout");
 
 struct Scratch {
-  uint32_t* done;            // [2][kMaxPairs] phase-A completions per pair
+  uint32_t* done;            // [2][kMaxPairs] phase-A wave completions per pair
   uint32_t* fin;             // [2][kMaxRanges] phase-B completions per range
   float* hbuf;               // [kMaxPairs][8][32]
   double* partial;           // [groups][burst][hidden]
@@ -100,12 +102,18 @@ __device__ __forceinline__ bool half_bad(uint32_t bits) { return (bits & 0x7c00u
 __device__ __forceinline__ float e8m0(uint32_t e) {
   return __uint_as_float(e ? e << 23 : 0x00400000u);
 }
-// OCP E2M1 code -> float {0,.5,1,1.5,2,3,4,6} with sign; code 8 is +0 as in
-// the reference table (src/native.c:9).
-__device__ __forceinline__ float e2m1(uint32_t c) {
-  uint32_t e = (c >> 1) & 3u, m = c & 1u;
-  uint32_t mag = e ? ((e + 126u) << 23) | (m << 22) : (m ? 126u << 23 : 0u);
-  return __uint_as_float(mag ? mag | ((c & 8u) << 28) : 0u);
+// Two OCP E2M1 codes (byte b of v: low nibble first) -> floats times
+// `scale`, with the gfx950 conversion instruction. The products are exact
+// (E2M1 values have two significant bits, scales are powers of two, the
+// subnormal 2^-127 included); code 8 yields -0, the reference table +0
+// (src/native.c:9), which only the exact decoders normalize.
+__device__ __forceinline__ float2 fp4_pair(uint32_t v, float scale, int b) {
+  switch (b) {
+    case 0: { auto r = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v, scale, 0); return make_float2(r[0], r[1]); }
+    case 1: { auto r = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v, scale, 1); return make_float2(r[0], r[1]); }
+    case 2: { auto r = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v, scale, 2); return make_float2(r[0], r[1]); }
+    default: { auto r = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v, scale, 3); return make_float2(r[0], r[1]); }
+  }
 }
 
 // Q4_K 6-bit scale/min of group g from the 12 packed bytes s0|s1|s2
@@ -133,8 +141,95 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v;
 }
 
+// Full-wave sum with DPP: quad butterflies, two rotations inside each
+// 16-lane row, then the four row totals read as scalars. The result is
+// wave-uniform and the association order is fixed.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  uint64_t b = __builtin_bit_cast(uint64_t, v);
+  uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xf, 0xf, false);
+  uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowRor4 = 0x124, kRowRor8 = 0x128, kRowHalfMirror = 0x141;
+
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp_f<kQuadXor1>(v);
+  v += dpp_f<kQuadXor2>(v);
+  v += dpp_f<kRowRor4>(v);
+  v += dpp_f<kRowRor8>(v);
+  return v;
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wave_total(float v) {
+  v = row_sum(v);
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+  uint64_t b = __builtin_bit_cast(uint64_t, v);
+  uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+  uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_total(double v) {
+  v += dpp_d<kQuadXor1>(v);
+  v += dpp_d<kQuadXor2>(v);
+  v += dpp_d<kRowRor4>(v);
+  v += dpp_d<kRowRor8>(v);
+  return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+// Sum over each aligned group of 8 lanes (quad butterflies + half-row mirror).
+__device__ __forceinline__ float oct_sum(float v) {
+  v += dpp_f<kQuadXor1>(v);
+  v += dpp_f<kQuadXor2>(v);
+  v += dpp_f<kRowHalfMirror>(v);
+  return v;
+}
+
 __device__ __forceinline__ void flag(uint32_t* status, uint32_t bit) {
   __hip_atomic_fetch_or(status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Cross-workgroup publication without cache-maintenance fences. On gfx950
+// an agent-scope release writes back the whole L2 of the XCD and an acquire
+// invalidates it (measured: ~100 us per 44 MB call when every wave does it).
+// Shared values are instead stored with device-coherent (sc1) stores, the
+// writing wave drains its memory counter, and only then bumps a relaxed
+// counter (an atomic performed at the device coherence point). Readers poll
+// the counter relaxed and load the values with device-coherent loads; they
+// touch a value's line only after its counter says it is complete.
+__device__ __forceinline__ void drain_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+template <typename T>
+__device__ __forceinline__ void put(T* p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+template <typename T>
+__device__ __forceinline__ T get(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t bump(uint32_t* p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Byte k of v as a float: one v_cvt_f32_ubyte<k> when v holds four nibbles
+// already masked to their bytes.
+__device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xffu); }
+// The low and high nibbles of the four bytes of v, each in its own byte. The
+// AND is opaque to the optimizer, which would otherwise fold it into the byte
+// extraction and emit a bit-field extract per nibble.
+__device__ __forceinline__ uint32_t nib_lo(uint32_t v) {
+  uint32_t r;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+__device__ __forceinline__ uint32_t nib_hi(uint32_t v) {
+  uint32_t r;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(v >> 4));
+  return r;
 }
 
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
@@ -164,6 +259,25 @@ __device__ void q8_group(float* v, int n) {
   }
 }
 
+// fr_q8_activation of one 64-value group held in registers (src/q4.c:37-61).
+__device__ __forceinline__ void q8_regs64(float4* x4) {
+  float max = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    max = fmaxf(fmaxf(fmaxf(max, fabsf(x4[i].x)), fmaxf(fabsf(x4[i].y), fabsf(x4[i].z))), fabsf(x4[i].w));
+  const float scale = max / 127.0f;
+  const float inv = 127.0f / max;
+  const bool zero = scale == 0.f, finite_inv = isfinite(inv);
+  auto q = [&](float v) {
+    float r = finite_inv ? v * inv : (v / max) * 127.0f;
+    r = fminf(fmaxf(rintf(r), -127.f), 127.f);
+    double back = fmin(fmax((double)r * (double)scale, -(double)FLT_MAX), (double)FLT_MAX);
+    return zero ? 0.f : (float)back;
+  };
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x4[i] = make_float4(q(x4[i].x), q(x4[i].y), q(x4[i].z), q(x4[i].w));
+}
+
 // ------------------------------------------------- re-tiled row layouts
 //
 // Gate/up rows (n = hidden columns, nch = n/64 lane chunks of 64 columns):
@@ -178,136 +292,121 @@ __device__ void q8_group(float* v, int n) {
 // Decode the lane's 64 columns of a gate/up row exactly as the reference
 // decodes each weight (src/native.c:13-31, src/q4.c:29-31). Used by the
 // fp64 modes and by the debug decoder; returns false on a non-finite scale.
+// The lane's raw bytes of one gate/up row: quants and the scale words.
+struct LaneRaw {
+  uint4 q[4];
+  uint4 h;
+};
+
 template <int type>
-__device__ __forceinline__ bool decode_lane_t(const uint8_t* row, int nch, int c, float* w) {
-  bool ok = true;
+__device__ __forceinline__ void load_raw(const uint8_t* row, int nch, int c, LaneRaw& r) {
   if (type == TQ4_K) {
-    uint4 h = ld16(row + 32 * nch + 16 * (c >> 2));
-    uint4 qa = ld16(row + 16 * c), qb = ld16(row + 16 * nch + 16 * c);
-    ok = !half_bad(h.x) && !half_bad(h.x >> 16);
-    float d = half_to_float(h.x & 0xffff), dm = half_to_float(h.x >> 16);
+    r.q[0] = ld16(row + 16 * c);
+    r.q[1] = ld16(row + 16 * nch + 16 * c);
+    r.h = ld16(row + 32 * nch + 16 * (c >> 2));
+  } else if (type == TQ8_0) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) r.q[p] = ld16(row + 16 * nch * p + 16 * c);
+    r.h.x = *reinterpret_cast<const uint32_t*>(row + 64 * nch + 4 * c);
+  } else if (type == TMXFP4) {
+    r.q[0] = ld16(row + 16 * c);
+    r.q[1] = ld16(row + 16 * nch + 16 * c);
+    r.h.x = *reinterpret_cast<const uint16_t*>(row + 32 * nch + 2 * c);
+  } else {
+    r.q[0] = ld16(row + 16 * c);
+    r.q[1] = ld16(row + 16 * nch + 16 * c);
+    r.h.x = *reinterpret_cast<const uint32_t*>(row + 32 * nch + 4 * c);
+  }
+}
+
+// Scale factors of the raw row for the fp32 path; false on a bad scale.
+template <int type>
+__device__ __forceinline__ bool raw_scales(const LaneRaw& r, int c, float s[2], float m[2]) {
+  if (type == TQ4_K) {
+    float d = half_to_float(r.h.x & 0xffff), dm = half_to_float(r.h.x >> 16);
     uint32_t g0 = 2 * (c & 3), sc0, mi0, sc1, mi1;
-    q4k_scale_min(h.y, h.z, h.w, g0, sc0, mi0);
-    q4k_scale_min(h.y, h.z, h.w, g0 + 1, sc1, mi1);
-    float D0 = d * (float)sc0, M0 = dm * (float)mi0, D1 = d * (float)sc1, M1 = dm * (float)mi1;
+    q4k_scale_min(r.h.y, r.h.z, r.h.w, g0, sc0, mi0);
+    q4k_scale_min(r.h.y, r.h.z, r.h.w, g0 + 1, sc1, mi1);
+    s[0] = d * (float)sc0;
+    s[1] = d * (float)sc1;
+    m[0] = dm * (float)mi0;
+    m[1] = dm * (float)mi1;
+    return !half_bad(r.h.x) && !half_bad(r.h.x >> 16);
+  } else if (type == TMXFP4) {
+    s[0] = e8m0(r.h.x & 0xff);
+    s[1] = e8m0((r.h.x >> 8) & 0xff);
+    m[0] = m[1] = 0.f;
+    return (r.h.x & 0xff) != 255 && ((r.h.x >> 8) & 0xff) != 255;
+  } else {  // Q8_0, Q4_0: two fp16 scales
+    s[0] = half_to_float(r.h.x & 0xffff);
+    s[1] = half_to_float(r.h.x >> 16);
+    m[0] = m[1] = 0.f;
+    return !half_bad(r.h.x) && !half_bad(r.h.x >> 16);
+  }
+}
+
+// Exact reference decode of the raw row (src/native.c:13-31, src/q4.c:29-31).
+template <int type>
+__device__ __forceinline__ bool decode_raw(const LaneRaw& r, int c, float* w) {
+  float s[2], m[2];
+  bool ok = raw_scales<type>(r, c, s, m);
+  if (type == TQ4_K) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      uint32_t v = word(i < 4 ? qa : qb, i & 3);
+      uint32_t v = word(r.q[i >> 2], i & 3);
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         uint32_t byte = v >> (8 * b);
-        w[4 * i + b] = fmaf(D0, (float)(byte & 15u), -M0);
-        w[32 + 4 * i + b] = fmaf(D1, (float)((byte >> 4) & 15u), -M1);
+        w[4 * i + b] = fmaf(s[0], (float)(byte & 15u), -m[0]);
+        w[32 + 4 * i + b] = fmaf(s[1], (float)((byte >> 4) & 15u), -m[1]);
       }
     }
   } else if (type == TQ8_0) {
-    uint32_t s = *reinterpret_cast<const uint32_t*>(row + 64 * nch + 4 * c);
-    ok = !half_bad(s) && !half_bad(s >> 16);
-    float d0 = half_to_float(s & 0xffff), d1 = half_to_float(s >> 16);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      uint4 q = ld16(row + 16 * nch * p + 16 * c);
+    for (int p = 0; p < 4; ++p)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        uint32_t v = word(q, i);
+        uint32_t v = word(r.q[p], i);
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
-          w[16 * p + 4 * i + b] = (p < 2 ? d0 : d1) * (float)(int8_t)(v >> (8 * b));
+        for (int b = 0; b < 4; ++b) w[16 * p + 4 * i + b] = (p < 2 ? s[0] : s[1]) * (float)(int8_t)(v >> (8 * b));
       }
-    }
   } else if (type == TMXFP4) {
-    uint32_t e = *reinterpret_cast<const uint16_t*>(row + 32 * nch + 2 * c);
-    ok = (e & 0xff) != 255 && (e >> 8) != 255;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      float sc = e8m0((e >> (8 * p)) & 0xff);
-      uint4 q = ld16(row + 16 * nch * p + 16 * c);
+    for (int p = 0; p < 2; ++p)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        uint32_t v = word(q, i);
+        uint32_t v = word(r.q[p], i);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          float2 e = fp4_pair(v, s[p], b);
+          w[32 * p + 4 * i + b] = e.x + 0.0f;   // -0 -> +0 as the reference table
+          w[32 * p + 16 + 4 * i + b] = e.y + 0.0f;
+        }
+      }
+  } else {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t v = word(r.q[p], i);
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           uint32_t byte = v >> (8 * b);
-          w[32 * p + 4 * i + b] = sc * e2m1(byte & 15u);
-          w[32 * p + 16 + 4 * i + b] = sc * e2m1((byte >> 4) & 15u);
+          w[32 * p + 4 * i + b] = (float)((int)(byte & 15u) - 8) * s[p];
+          w[32 * p + 16 + 4 * i + b] = (float)((int)((byte >> 4) & 15u) - 8) * s[p];
         }
       }
-    }
-  } else {  // Q4_0
-    uint32_t s = *reinterpret_cast<const uint32_t*>(row + 32 * nch + 4 * c);
-    ok = !half_bad(s) && !half_bad(s >> 16);
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      float d = half_to_float(p ? s >> 16 : s & 0xffff);
-      uint4 q = ld16(row + 16 * nch * p + 16 * c);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t v = word(q, i);
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          uint32_t byte = v >> (8 * b);
-          w[32 * p + 4 * i + b] = (float)((int)(byte & 15u) - 8) * d;
-          w[32 * p + 16 + 4 * i + b] = (float)((int)((byte >> 4) & 15u) - 8) * d;
-        }
-      }
-    }
   }
   return ok;
 }
 
 __device__ bool decode_lane(uint8_t type, const uint8_t* row, int nch, int c, float* w) {
+  LaneRaw r;
   switch (type) {
-    case TQ4_K: return decode_lane_t<TQ4_K>(row, nch, c, w);
-    case TQ8_0: return decode_lane_t<TQ8_0>(row, nch, c, w);
-    case TMXFP4: return decode_lane_t<TMXFP4>(row, nch, c, w);
-    default: return decode_lane_t<TQ4_0>(row, nch, c, w);
-  }
-}
-
-// Per-lane raw row data for the fp32 path: loaded once, reused per token.
-struct LaneRow {
-  uint4 q[4];
-  float s[4];    // per-64-column-half scale factors
-  float m[2];    // Q4_K mins (per group)
-  bool ok;
-};
-
-template <int type>
-__device__ __forceinline__ void load_lane(const uint8_t* row, int nch, int c, LaneRow& r) {
-  if (type == TQ4_K) {
-    uint4 h = ld16(row + 32 * nch + 16 * (c >> 2));
-    r.q[0] = ld16(row + 16 * c);
-    r.q[1] = ld16(row + 16 * nch + 16 * c);
-    r.ok = !half_bad(h.x) && !half_bad(h.x >> 16);
-    float d = half_to_float(h.x & 0xffff), dm = half_to_float(h.x >> 16);
-    uint32_t g0 = 2 * (c & 3), sc0, mi0, sc1, mi1;
-    q4k_scale_min(h.y, h.z, h.w, g0, sc0, mi0);
-    q4k_scale_min(h.y, h.z, h.w, g0 + 1, sc1, mi1);
-    r.s[0] = d * (float)sc0;
-    r.s[1] = d * (float)sc1;
-    r.m[0] = dm * (float)mi0;
-    r.m[1] = dm * (float)mi1;
-  } else if (type == TQ8_0) {
-    uint32_t s = *reinterpret_cast<const uint32_t*>(row + 64 * nch + 4 * c);
-#pragma unroll
-    for (int p = 0; p < 4; ++p) r.q[p] = ld16(row + 16 * nch * p + 16 * c);
-    r.ok = !half_bad(s) && !half_bad(s >> 16);
-    r.s[0] = half_to_float(s & 0xffff);
-    r.s[1] = half_to_float(s >> 16);
-  } else if (type == TMXFP4) {
-    uint32_t e = *reinterpret_cast<const uint16_t*>(row + 32 * nch + 2 * c);
-    r.q[0] = ld16(row + 16 * c);
-    r.q[1] = ld16(row + 16 * nch + 16 * c);
-    r.ok = (e & 0xff) != 255 && (e >> 8) != 255;
-    r.s[0] = e8m0(e & 0xff);
-    r.s[1] = e8m0(e >> 8);
-  } else {  // Q4_0
-    uint32_t s = *reinterpret_cast<const uint32_t*>(row + 32 * nch + 4 * c);
-    r.q[0] = ld16(row + 16 * c);
-    r.q[1] = ld16(row + 16 * nch + 16 * c);
-    r.ok = !half_bad(s) && !half_bad(s >> 16);
-    r.s[0] = half_to_float(s & 0xffff);
-    r.s[1] = half_to_float(s >> 16);
+    case TQ4_K: load_raw<TQ4_K>(row, nch, c, r); return decode_raw<TQ4_K>(r, c, w);
+    case TQ8_0: load_raw<TQ8_0>(row, nch, c, r); return decode_raw<TQ8_0>(r, c, w);
+    case TMXFP4: load_raw<TMXFP4>(row, nch, c, r); return decode_raw<TMXFP4>(r, c, w);
+    default: load_raw<TQ4_0>(row, nch, c, r); return decode_raw<TQ4_0>(r, c, w);
   }
 }
 
@@ -316,25 +415,26 @@ __device__ __forceinline__ void load_lane(const uint8_t* row, int nch, int c, La
 // Q4_0 forms factor the scale and min out of the 32-column groups:
 // sum_j (D*q_j - M)*x_j = D*sum_j q_j*x_j - M*sum_j x_j.
 template <int type>
-__device__ __forceinline__ float lane_dot_f32(const LaneRow& r, const float* xp, float X0, float X1) {
-  const float4* x = reinterpret_cast<const float4*>(xp);
+__device__ __forceinline__ float lane_dot_f32(const LaneRaw& r, const float* sc, const float* mn, const float4* x,
+                                              float X0, float X1) {
   float s0 = 0.f, s1 = 0.f;
   if (type == TQ4_K) {
     // Byte i of the 32-byte chunk: column i (low nibble), 32+i (high).
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t v = word(r.q[i >> 2], i & 3);
+      const uint32_t lo = nib_lo(v), hi = nib_hi(v);
       const float4 a = x[i], b = x[8 + i];
-      s0 = fmaf((float)(v & 15u), a.x, s0);
-      s0 = fmaf((float)((v >> 8) & 15u), a.y, s0);
-      s0 = fmaf((float)((v >> 16) & 15u), a.z, s0);
-      s0 = fmaf((float)((v >> 24) & 15u), a.w, s0);
-      s1 = fmaf((float)((v >> 4) & 15u), b.x, s1);
-      s1 = fmaf((float)((v >> 12) & 15u), b.y, s1);
-      s1 = fmaf((float)((v >> 20) & 15u), b.z, s1);
-      s1 = fmaf((float)(v >> 28), b.w, s1);
+      s0 = fmaf(ub(lo, 0), a.x, s0);
+      s0 = fmaf(ub(lo, 1), a.y, s0);
+      s0 = fmaf(ub(lo, 2), a.z, s0);
+      s0 = fmaf(ub(lo, 3), a.w, s0);
+      s1 = fmaf(ub(hi, 0), b.x, s1);
+      s1 = fmaf(ub(hi, 1), b.y, s1);
+      s1 = fmaf(ub(hi, 2), b.z, s1);
+      s1 = fmaf(ub(hi, 3), b.w, s1);
     }
-    return (r.s[0] * s0 - r.m[0] * X0) + (r.s[1] * s1 - r.m[1] * X1);
+    return (sc[0] * s0 - mn[0] * X0) + (sc[1] * s1 - mn[1] * X1);
   }
   if (type == TQ4_0) {
     // Per 32-column block p, byte i: column i (low nibble), 16+i (high).
@@ -344,19 +444,20 @@ __device__ __forceinline__ float lane_dot_f32(const LaneRow& r, const float* xp,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t v = word(r.q[p], i);
+        const uint32_t lo = nib_lo(v), hi = nib_hi(v);
         const float4 a = x[8 * p + i], b = x[8 * p + 4 + i];
-        s = fmaf((float)(v & 15u), a.x, s);
-        s = fmaf((float)((v >> 8) & 15u), a.y, s);
-        s = fmaf((float)((v >> 16) & 15u), a.z, s);
-        s = fmaf((float)((v >> 24) & 15u), a.w, s);
-        s = fmaf((float)((v >> 4) & 15u), b.x, s);
-        s = fmaf((float)((v >> 12) & 15u), b.y, s);
-        s = fmaf((float)((v >> 20) & 15u), b.z, s);
-        s = fmaf((float)(v >> 28), b.w, s);
+        s = fmaf(ub(lo, 0), a.x, s);
+        s = fmaf(ub(lo, 1), a.y, s);
+        s = fmaf(ub(lo, 2), a.z, s);
+        s = fmaf(ub(lo, 3), a.w, s);
+        s = fmaf(ub(hi, 0), b.x, s);
+        s = fmaf(ub(hi, 1), b.y, s);
+        s = fmaf(ub(hi, 2), b.z, s);
+        s = fmaf(ub(hi, 3), b.w, s);
       }
       if (p) s1 = s; else s0 = s;
     }
-    return r.s[0] * (s0 - 8.f * X0) + r.s[1] * (s1 - 8.f * X1);
+    return sc[0] * (s0 - 8.f * X0) + sc[1] * (s1 - 8.f * X1);
   }
   if (type == TQ8_0) {
 #pragma unroll
@@ -373,7 +474,7 @@ __device__ __forceinline__ float lane_dot_f32(const LaneRow& r, const float* xp,
       }
       if (p < 2) s0 += s; else s1 += s;
     }
-    return r.s[0] * s0 + r.s[1] * s1;
+    return sc[0] * s0 + sc[1] * s1;
   }
   // MXFP4: per 32-column block p, byte i holds element i (low) and 16+i.
 #pragma unroll
@@ -383,37 +484,138 @@ __device__ __forceinline__ float lane_dot_f32(const LaneRow& r, const float* xp,
     for (int i = 0; i < 4; ++i) {
       const uint32_t v = word(r.q[p], i);
       const float4 a = x[8 * p + i], b = x[8 * p + 4 + i];
-      s = fmaf(e2m1(v & 15u), a.x, s);
-      s = fmaf(e2m1((v >> 8) & 15u), a.y, s);
-      s = fmaf(e2m1((v >> 16) & 15u), a.z, s);
-      s = fmaf(e2m1((v >> 24) & 15u), a.w, s);
-      s = fmaf(e2m1((v >> 4) & 15u), b.x, s);
-      s = fmaf(e2m1((v >> 12) & 15u), b.y, s);
-      s = fmaf(e2m1((v >> 20) & 15u), b.z, s);
-      s = fmaf(e2m1(v >> 28), b.w, s);
+      float2 e0 = fp4_pair(v, 1.0f, 0), e1 = fp4_pair(v, 1.0f, 1), e2 = fp4_pair(v, 1.0f, 2), e3 = fp4_pair(v, 1.0f, 3);
+      s = fmaf(e0.x, a.x, s);
+      s = fmaf(e1.x, a.y, s);
+      s = fmaf(e2.x, a.z, s);
+      s = fmaf(e3.x, a.w, s);
+      s = fmaf(e0.y, b.x, s);
+      s = fmaf(e1.y, b.y, s);
+      s = fmaf(e2.y, b.z, s);
+      s = fmaf(e3.y, b.w, s);
     }
     if (p) s1 = s; else s0 = s;
   }
-  return r.s[0] * s0 + r.s[1] * s1;
+  return sc[0] * s0 + sc[1] * s1;
 }
 
 // ------------------------------------------------------------ phase A
 //
-// Task (pair p, neuron group ng): 4 wavefronts, each owning nn/4 neurons.
-// Lane c of a wave owns activation columns 64c..64c+63 of every row it
-// streams; a 64-lane butterfly reduces the row. Tokens are processed in
-// tiles of BT (compile time) so per-token values stay in registers.
+// Task (pair p, neuron group ng of kTaskNeurons): 4 wavefronts, each owning
+// kWaveNeurons neurons (a gate row and an up row each). Lane c of a wave owns
+// activation columns 64c..64c+63 of every row it streams; a DPP tree reduces
+// each row to a wave-uniform value. Each wave publishes its own h values and
+// releases the pair counter once, so a pair is complete at kDoneTarget.
 
-template <int MODE, int BT, int GU>
-__device__ __forceinline__ uint32_t phase_a_rows(const PlanHeader& H, const Scratch& S, unsigned p, unsigned ng,
-                                                 uint64_t slice, uint32_t proj, uint32_t tmask, unsigned t0,
-                                                 unsigned tc, const float* lds) {
-  const unsigned hidden = H.hidden, nch = hidden / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+constexpr int kTaskNeurons = 8;
+constexpr int kWaveNeurons = kTaskNeurons / kWaves;
+constexpr uint32_t kDoneTarget = (kNeurons / kTaskNeurons) * kWaves;
+
+__device__ __forceinline__ float silu_mul(float a, float u, uint32_t& bad) {
+  if (!isfinite(a) || !isfinite(u)) {
+    bad |= kErrRange;
+    return 0.f;
+  }
+  // Stable sigmoid in double, as backends/ref.c:82-83.
+  double ad = a;
+  double sig = ad >= 0 ? 1.0 / (1.0 + exp(-ad)) : exp(ad) / (1.0 + exp(ad));
+  double hv = ad * sig * (double)u;
+  if (!isfinite(hv) || fabs(hv) > (double)FLT_MAX) {
+    bad |= kErrRange;
+    return 0.f;
+  }
+  return (float)hv;
+}
+
+__device__ __forceinline__ float narrow_dot(double s) {
+  return (!isfinite(s) || fabs(s) > (double)FLT_MAX) ? INFINITY : (float)s;
+}
+
+__device__ __forceinline__ void publish_h(const Scratch& S, size_t index, float h) { put(S.hbuf + index, h); }
+
+// The wave's h stores are complete (drained) before its pair counter moves.
+__device__ __forceinline__ void release_pair(const Scratch& S, unsigned p) {
+  drain_stores();
+  if ((threadIdx.x & 63) == 0) bump(S.done + (size_t)S.parity * kMaxPairs + p);
+}
+
+// Single token: the lane's 64 activations live in registers, every row load
+// of the wave is issued before any arithmetic, no LDS and no barrier.
+template <int MODE, int GU>
+__device__ __forceinline__ uint32_t phase_a_single(const PlanHeader& H, const Scratch& S, unsigned p, unsigned n0,
+                                                   uint64_t slice, uint32_t proj, const float* xg) {
+  const unsigned nch = H.hidden / 64;
+  const int lane = threadIdx.x & 63;
   const bool active = lane < (int)nch;
   const int c = active ? lane : 0;
   const uint32_t row_bytes = proj / kNeurons;
-  const unsigned per_wave = H.nn / kWaves;
+  LaneRaw raw[2 * kWaveNeurons];
+#pragma unroll
+  for (int k = 0; k < kWaveNeurons; ++k)
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      load_raw<GU>(reinterpret_cast<const uint8_t*>(slice) + (r ? proj : 0) + (size_t)(n0 + k) * row_bytes, nch, c,
+                   raw[2 * k + r]);
+  float4 x[16];
+  {
+    const float4* xs = reinterpret_cast<const float4*>(xg + 64 * c);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = xs[i];
+  }
+  if (MODE == MODE_Q8) q8_regs64(x);  // the lane chunk is one 64-group
+  float X0 = 0.f, X1 = 0.f;
+  if (MODE == MODE_F32 && (GU == TQ4_K || GU == TQ4_0)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      X0 += (x[i].x + x[i].y) + (x[i].z + x[i].w);
+      X1 += (x[8 + i].x + x[8 + i].y) + (x[8 + i].z + x[8 + i].w);
+    }
+  }
+  uint32_t bad = 0;
+#pragma unroll
+  for (int k = 0; k < kWaveNeurons; ++k) {
+    float au[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const LaneRaw& rr = raw[2 * k + r];
+      if (MODE == MODE_F32) {
+        float sc[2], mn[2];
+        bool ok = raw_scales<GU>(rr, c, sc, mn);
+        if (active && !ok) bad |= kErrScale;
+        float part = lane_dot_f32<GU>(rr, sc, mn, x, X0, X1);
+        au[r] = wave_total(active ? part : 0.f);
+      } else {
+        float w[64];
+        bool ok = decode_raw<GU>(rr, c, w);
+        if (active && !ok) bad |= kErrScale;
+        double acc = 0.0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          acc = fma((double)w[4 * j], (double)x[j].x, acc);
+          acc = fma((double)w[4 * j + 1], (double)x[j].y, acc);
+          acc = fma((double)w[4 * j + 2], (double)x[j].z, acc);
+          acc = fma((double)w[4 * j + 3], (double)x[j].w, acc);
+        }
+        au[r] = narrow_dot(wave_total(active ? acc : 0.0));
+      }
+    }
+    float h = silu_mul(au[0], au[1], bad);
+    if (lane == 0) publish_h(S, (size_t)p * kMaxBurst * kNeurons + n0 + k, h);
+  }
+  return bad;
+}
+
+// Bursts: activations of up to BT tokens staged in LDS per tile; each row's
+// loaded bytes are reused for every token of the tile.
+template <int MODE, int BT, int GU>
+__device__ __forceinline__ uint32_t phase_a_tile(const PlanHeader& H, const Scratch& S, unsigned p, unsigned n0,
+                                                 uint64_t slice, uint32_t proj, uint32_t tmask, unsigned t0,
+                                                 unsigned tc, const float* lds) {
+  const unsigned hidden = H.hidden, nch = hidden / 64;
+  const int lane = threadIdx.x & 63;
+  const bool active = lane < (int)nch;
+  const int c = active ? lane : 0;
+  const uint32_t row_bytes = proj / kNeurons;
   uint32_t bad = 0;
   float X0[BT], X1[BT];
 #pragma unroll
@@ -429,26 +631,33 @@ __device__ __forceinline__ uint32_t phase_a_rows(const PlanHeader& H, const Scra
       }
     }
   }
-  for (unsigned k = 0; k < per_wave; ++k) {
-    const unsigned n = ng * H.nn + wave * per_wave + k;
-    float av[BT], uv[BT];
+  LaneRaw raw[2 * kWaveNeurons];
+#pragma unroll
+  for (int k = 0; k < kWaveNeurons; ++k)
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      load_raw<GU>(reinterpret_cast<const uint8_t*>(slice) + (r ? proj : 0) + (size_t)(n0 + k) * row_bytes, nch, c,
+                   raw[2 * k + r]);
+#pragma unroll
+  for (int k = 0; k < kWaveNeurons; ++k) {
+    float au[2][BT];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const uint8_t* row = reinterpret_cast<const uint8_t*>(slice) + (r ? proj : 0) + (size_t)n * row_bytes;
+      const LaneRaw& rr = raw[2 * k + r];
       if (MODE == MODE_F32) {
-        LaneRow lr;
-        load_lane<GU>(row, nch, c, lr);
-        if (active && !lr.ok) bad |= kErrScale;
+        float sc[2], mn[2];
+        bool ok = raw_scales<GU>(rr, c, sc, mn);
+        if (active && !ok) bad |= kErrScale;
 #pragma unroll
         for (int t = 0; t < BT; ++t) {
           float part = 0.f;
-          if (active && t < (int)tc) part = lane_dot_f32<GU>(lr, lds + t * hidden + 64 * c, X0[t], X1[t]);
-          float sum = wave_sum(part);
-          if (r) uv[t] = sum; else av[t] = sum;
+          if (active && t < (int)tc)
+            part = lane_dot_f32<GU>(rr, sc, mn, reinterpret_cast<const float4*>(lds + t * hidden + 64 * c), X0[t], X1[t]);
+          au[r][t] = wave_total(part);
         }
       } else {
         float w[64];
-        bool ok = decode_lane_t<GU>(row, nch, c, w);
+        bool ok = decode_raw<GU>(rr, c, w);
         if (active && !ok) bad |= kErrScale;
 #pragma unroll
         for (int t = 0; t < BT; ++t) {
@@ -458,29 +667,15 @@ __device__ __forceinline__ uint32_t phase_a_rows(const PlanHeader& H, const Scra
 #pragma unroll
             for (int j = 0; j < 64; ++j) acc = fma((double)w[j], (double)x[j], acc);
           }
-          double sum = wave_sum(acc);
-          float f = (!isfinite(sum) || fabs(sum) > (double)FLT_MAX) ? INFINITY : (float)sum;
-          if (r) uv[t] = f; else av[t] = f;
+          au[r][t] = narrow_dot(wave_total(acc));
         }
       }
     }
-    if (lane == 0) {
 #pragma unroll
-      for (int t = 0; t < BT; ++t) {
-        if (t >= (int)tc || !((tmask >> (t0 + t)) & 1u)) continue;
-        float a = av[t], u = uv[t], h = 0.f;
-        if (!isfinite(a) || !isfinite(u)) {
-          bad |= kErrRange;
-        } else {
-          // Stable sigmoid in double, as backends/ref.c:82-83.
-          double ad = a;
-          double sig = ad >= 0 ? 1.0 / (1.0 + exp(-ad)) : exp(ad) / (1.0 + exp(ad));
-          double hv = ad * sig * (double)u;
-          if (!isfinite(hv) || fabs(hv) > (double)FLT_MAX) bad |= kErrRange;
-          else h = (float)hv;
-        }
-        S.hbuf[((size_t)p * kMaxBurst + t0 + t) * kNeurons + n] = h;
-      }
+    for (int t = 0; t < BT; ++t) {
+      if (t >= (int)tc || !((tmask >> (t0 + t)) & 1u)) continue;
+      float h = silu_mul(au[0][t], au[1][t], bad);
+      if (lane == 0) publish_h(S, ((size_t)p * kMaxBurst + t0 + t) * kNeurons + n0 + k, h);
     }
   }
   return bad;
@@ -489,7 +684,7 @@ __device__ __forceinline__ uint32_t phase_a_rows(const PlanHeader& H, const Scra
 template <int MODE, int BT>
 __device__ void phase_a(const PlanHeader& H, const uint8_t* plan, const Scratch& S, uint32_t* status,
                         unsigned task, float* lds) {
-  const unsigned per_pair = kNeurons / H.nn;
+  constexpr unsigned per_pair = kNeurons / kTaskNeurons;
   const unsigned p = task / per_pair, ng = task % per_pair;
   const PairDesc* P = reinterpret_cast<const PairDesc*>(plan + H.pairs_off) + p;
   const uint64_t slice = P->slice;
@@ -497,37 +692,40 @@ __device__ void phase_a(const PlanHeader& H, const uint8_t* plan, const Scratch&
   const uint8_t gu = P->gu;
   const uint32_t tmask = P->tmask;
   const unsigned hidden = H.hidden, nch = hidden / 64, T = H.burst;
+  const unsigned n0 = ng * kTaskNeurons + (threadIdx.x >> 6) * kWaveNeurons;
   const float* xg = reinterpret_cast<const float*>(plan + H.x_off);
   uint32_t bad = 0;
-
-  for (unsigned t0 = 0; t0 < T; t0 += BT) {
-    const unsigned tc = min((unsigned)BT, T - t0);
-    // Stage tc activation rows in LDS (Q8 mode: quantized per 64-group).
-    if (t0) __syncthreads();
-    {
-      const float4* src = reinterpret_cast<const float4*>(xg + (size_t)t0 * hidden);
-      float4* dst = reinterpret_cast<float4*>(lds);
-      for (unsigned i = threadIdx.x; i < tc * hidden / 4; i += kThreads) dst[i] = src[i];
-    }
-    __syncthreads();
-    if (MODE == MODE_Q8) {
-      // One thread per 64-value group: a lane chunk is one quantizer group.
-      for (unsigned g = threadIdx.x; g < tc * nch; g += kThreads) q8_group(lds + 64 * g, 64);
-      __syncthreads();
-    }
+  if (BT == 1) {
     switch (gu) {
-      case TQ4_K: bad |= phase_a_rows<MODE, BT, TQ4_K>(H, S, p, ng, slice, proj, tmask, t0, tc, lds); break;
-      case TQ8_0: bad |= phase_a_rows<MODE, BT, TQ8_0>(H, S, p, ng, slice, proj, tmask, t0, tc, lds); break;
-      case TMXFP4: bad |= phase_a_rows<MODE, BT, TMXFP4>(H, S, p, ng, slice, proj, tmask, t0, tc, lds); break;
-      default: bad |= phase_a_rows<MODE, BT, TQ4_0>(H, S, p, ng, slice, proj, tmask, t0, tc, lds); break;
+      case TQ4_K: bad = phase_a_single<MODE, TQ4_K>(H, S, p, n0, slice, proj, xg); break;
+      case TQ8_0: bad = phase_a_single<MODE, TQ8_0>(H, S, p, n0, slice, proj, xg); break;
+      case TMXFP4: bad = phase_a_single<MODE, TMXFP4>(H, S, p, n0, slice, proj, xg); break;
+      default: bad = phase_a_single<MODE, TQ4_0>(H, S, p, n0, slice, proj, xg); break;
+    }
+  } else {
+    for (unsigned t0 = 0; t0 < T; t0 += BT) {
+      const unsigned tc = min((unsigned)BT, T - t0);
+      if (t0) __syncthreads();
+      {
+        const float4* src = reinterpret_cast<const float4*>(xg + (size_t)t0 * hidden);
+        float4* dst = reinterpret_cast<float4*>(lds);
+        for (unsigned i = threadIdx.x; i < tc * hidden / 4; i += kThreads) dst[i] = src[i];
+      }
+      __syncthreads();
+      if (MODE == MODE_Q8) {
+        for (unsigned g = threadIdx.x; g < tc * nch; g += kThreads) q8_group(lds + 64 * g, 64);
+        __syncthreads();
+      }
+      switch (gu) {
+        case TQ4_K: bad |= phase_a_tile<MODE, BT, TQ4_K>(H, S, p, n0, slice, proj, tmask, t0, tc, lds); break;
+        case TQ8_0: bad |= phase_a_tile<MODE, BT, TQ8_0>(H, S, p, n0, slice, proj, tmask, t0, tc, lds); break;
+        case TMXFP4: bad |= phase_a_tile<MODE, BT, TMXFP4>(H, S, p, n0, slice, proj, tmask, t0, tc, lds); break;
+        default: bad |= phase_a_tile<MODE, BT, TQ4_0>(H, S, p, n0, slice, proj, tmask, t0, tc, lds); break;
+      }
     }
   }
   if (bad) flag(status, bad);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(S.done + (size_t)S.parity * kMaxPairs + p, 1u, __ATOMIC_RELEASE,
-                           __HIP_MEMORY_SCOPE_AGENT);
-  }
+  release_pair(S, p);
 }
 
 // ------------------------------------------------------------ phase B
@@ -562,9 +760,9 @@ __device__ bool decode_down_row(uint8_t dn, const uint8_t* down, unsigned hidden
       uint32_t v = word(q, i);
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        uint32_t byte = v >> (8 * b);
-        w[4 * i + b] = sc * e2m1(byte & 15u);
-        w[16 + 4 * i + b] = sc * e2m1((byte >> 4) & 15u);
+        float2 f = fp4_pair(v, sc, b);
+        w[4 * i + b] = f.x + 0.0f;
+        w[16 + 4 * i + b] = f.y + 0.0f;
       }
     }
   } else if (dn == TQ8_0) {
@@ -628,31 +826,19 @@ __device__ bool decode_down_q4kt(const uint8_t* down, unsigned sb, int l, float*
   return ok;
 }
 
-template <int MODE, int TB>
-__device__ void phase_b(const PlanHeader& H, const uint8_t* plan, const Scratch& S, uint32_t* status,
-                        unsigned task, float* lds) {
-  const unsigned gi = task / H.nranges, cr = task % H.nranges;
-  const GroupDesc G = reinterpret_cast<const GroupDesc*>(plan + H.groups_off)[gi];
-  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + H.pairs_off);
-  const unsigned hidden = H.hidden, T = H.burst, count = G.count;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Wait (bounded) until every pair of the group has all 32 h values, then
+// stage them in LDS (Q8 mode: quantized per slice, backends/ref.c:85).
+// Called by the whole workgroup after it issued its weight loads.
+template <int MODE>
+__device__ __forceinline__ uint32_t stage_h(const PlanHeader& H, const Scratch& S, const GroupDesc& G, float* hs) {
+  const unsigned T = H.burst, count = G.count;
   uint32_t bad = 0;
-
-  // LDS: hs[count][T][32] floats | per-wave tables | wave reduction.
-  float* hs = lds;
-  const unsigned wstride = 512 + T * 256 + T * 8;
-  float* wtab = hs + H.gmax * T * kNeurons;
-  double* red = reinterpret_cast<double*>(wtab + kWaves * wstride);
-
-  // Bounded wait for the 32 h values of every pair of the group: every
-  // phase-A task has a lower block index than any phase-B task.
-  if (tid == 0) {
-    const uint32_t need = kNeurons / H.nn;
+  if (threadIdx.x == 0) {
     for (unsigned j = 0; j < count; ++j) {
       const uint32_t* ctr = S.done + (size_t)S.parity * kMaxPairs + G.first + j;
       uint32_t spins = 0;
-      while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < need) {
-        __builtin_amdgcn_s_sleep(2);
+      while (get(ctr) < kDoneTarget) {
+        __builtin_amdgcn_s_sleep(1);
         if (++spins > kSpinLimit) {
           bad |= kErrTimeout;
           break;
@@ -661,237 +847,348 @@ __device__ void phase_b(const PlanHeader& H, const uint8_t* plan, const Scratch&
     }
   }
   __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  for (unsigned i = tid; i < count * T * kNeurons; i += kThreads) {
+  for (unsigned i = threadIdx.x; i < count * T * kNeurons; i += kThreads) {
     unsigned j = i / (T * kNeurons), r = i % (T * kNeurons);
-    hs[i] = S.hbuf[((size_t)(G.first + j) * kMaxBurst) * kNeurons + r];
+    hs[i] = get(S.hbuf + ((size_t)(G.first + j) * kMaxBurst) * kNeurons + r);
   }
   __syncthreads();
-  if (MODE == MODE_Q8) {  // ref-q8 quantizes each slice's h (backends/ref.c:85)
-    for (unsigned i = tid; i < count * T; i += kThreads) q8_group(hs + i * kNeurons, kNeurons);
+  if (MODE == MODE_Q8) {
+    for (unsigned i = threadIdx.x; i < count * T; i += kThreads) q8_group(hs + i * kNeurons, kNeurons);
     __syncthreads();
   }
+  return bad;
+}
 
+template <int DN>
+constexpr int group_max() { return DN == TQ8_0 ? 6 : DN == TQ4_KT ? 8 : 12; }
+
+// [H x 32] down formats: thread = output row d of the 256-row range; every
+// pair of the group is prefetched before the dependency wait.
+template <int MODE, int TB, int DN>
+__device__ __forceinline__ uint32_t phase_b_rows(const PlanHeader& H, const Scratch& S, const GroupDesc& G,
+                                                 const PairDesc* pairs, unsigned gi, unsigned cr, float* hs) {
+  constexpr int MAXG = group_max<DN>();
+  const unsigned hidden = H.hidden, T = H.burst, count = G.count;
+  const unsigned d = cr * kCols + threadIdx.x;
+  uint4 q0[MAXG], q1[MAXG];
+  uint32_t sw[MAXG];
+#pragma unroll
+  for (int j = 0; j < MAXG; ++j) {
+    q0[j] = q1[j] = make_uint4(0, 0, 0, 0);
+    sw[j] = 0;
+    if (j >= (int)count) continue;
+    const PairDesc* P = pairs + G.first + j;
+    const uint8_t* down = reinterpret_cast<const uint8_t*>(P->slice) + 2 * (size_t)P->proj;
+    q0[j] = ld16(down + 16 * (size_t)d);
+    if (DN == TQ8_0) {
+      q1[j] = ld16(down + 16 * (size_t)hidden + 16 * (size_t)d);
+      sw[j] = reinterpret_cast<const uint16_t*>(down + 32 * (size_t)hidden)[d];
+    } else if (DN == TMXFP4) {
+      sw[j] = down[16 * (size_t)hidden + d];
+    } else {
+      sw[j] = reinterpret_cast<const uint16_t*>(down + 16 * (size_t)hidden)[d];
+    }
+  }
+  uint32_t bad = stage_h<MODE>(H, S, G, hs);
+  double y[TB];
+#pragma unroll
+  for (int t = 0; t < TB; ++t) y[t] = 0.0;
+#pragma unroll
+  for (int j = 0; j < MAXG; ++j) {
+    if (j >= (int)count) continue;
+    const PairDesc* P = pairs + G.first + j;
+    const uint32_t tmask = P->tmask;
+    if (MODE == MODE_F32) {
+      float sc;
+      if (DN == TMXFP4) {
+        if (sw[j] == 255) bad |= kErrScale;
+        sc = e8m0(sw[j]);
+      } else {
+        if (half_bad(sw[j])) bad |= kErrScale;
+        sc = half_to_float(sw[j]);
+      }
+#pragma unroll
+      for (int t = 0; t < TB; ++t) {
+        if (t >= (int)T || !((tmask >> t) & 1u)) continue;
+        const float4* h4 = reinterpret_cast<const float4*>(hs + (j * T + t) * kNeurons);
+        float sum = 0.f;
+        if (DN == TQ8_0) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t v = word(i < 4 ? q0[j] : q1[j], i & 3);
+            const float4 h = h4[i];
+            sum = fmaf((float)(int8_t)v, h.x, sum);
+            sum = fmaf((float)(int8_t)(v >> 8), h.y, sum);
+            sum = fmaf((float)(int8_t)(v >> 16), h.z, sum);
+            sum = fmaf((float)(int8_t)(v >> 24), h.w, sum);
+          }
+        } else {
+          // Byte i: neuron i (low nibble), neuron 16+i (high nibble).
+          float hsum = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t v = word(q0[j], i);
+            const float4 a = h4[i], b = h4[4 + i];
+            if (DN == TMXFP4) {
+              float2 e0 = fp4_pair(v, 1.0f, 0), e1 = fp4_pair(v, 1.0f, 1), e2 = fp4_pair(v, 1.0f, 2),
+                     e3 = fp4_pair(v, 1.0f, 3);
+              sum = fmaf(e0.x, a.x, sum);
+              sum = fmaf(e1.x, a.y, sum);
+              sum = fmaf(e2.x, a.z, sum);
+              sum = fmaf(e3.x, a.w, sum);
+              sum = fmaf(e0.y, b.x, sum);
+              sum = fmaf(e1.y, b.y, sum);
+              sum = fmaf(e2.y, b.z, sum);
+              sum = fmaf(e3.y, b.w, sum);
+            } else {
+              sum = fmaf((float)(v & 15u), a.x, sum);
+              sum = fmaf((float)((v >> 8) & 15u), a.y, sum);
+              sum = fmaf((float)((v >> 16) & 15u), a.z, sum);
+              sum = fmaf((float)((v >> 24) & 15u), a.w, sum);
+              sum = fmaf((float)((v >> 4) & 15u), b.x, sum);
+              sum = fmaf((float)((v >> 12) & 15u), b.y, sum);
+              sum = fmaf((float)((v >> 20) & 15u), b.z, sum);
+              sum = fmaf((float)(v >> 28), b.w, sum);
+              hsum += ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+            }
+          }
+          if (DN == TQ4_0) sum -= 8.f * hsum;
+        }
+        y[t] += (double)P->gate[t] * ((double)sc * (double)sum);
+      }
+    } else {
+      // Exact decode of the row (decode_down_row semantics) from registers.
+      float w[32];
+      if (DN == TMXFP4) {
+        if (sw[j] == 255) bad |= kErrScale;
+        const float sc = e8m0(sw[j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t v = word(q0[j], i);
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const float2 f = fp4_pair(v, sc, b);
+            w[4 * i + b] = f.x;
+            w[16 + 4 * i + b] = f.y;
+          }
+        }
+      } else if (DN == TQ8_0) {
+        if (half_bad(sw[j])) bad |= kErrScale;
+        const float sc = half_to_float(sw[j]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t v = word(i < 4 ? q0[j] : q1[j], i & 3);
+#pragma unroll
+          for (int b = 0; b < 4; ++b) w[4 * i + b] = sc * (float)(int8_t)(v >> (8 * b));
+        }
+      } else {
+        if (half_bad(sw[j])) bad |= kErrScale;
+        const float sc = half_to_float(sw[j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t v = word(q0[j], i);
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            w[4 * i + b] = (float)((int)((v >> (8 * b)) & 15u) - 8) * sc;
+            w[16 + 4 * i + b] = (float)((int)((v >> (8 * b + 4)) & 15u) - 8) * sc;
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < TB; ++t) {
+        if (t >= (int)T || !((tmask >> t) & 1u)) continue;
+        const float* h = hs + (j * T + t) * kNeurons;
+        double sum = 0.0;
+#pragma unroll
+        for (int n = 0; n < 32; ++n) sum = fma((double)w[n], (double)h[n], sum);
+        y[t] += (double)P->gate[t] * sum;
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TB; ++t)
+    if (t < (int)T) put(S.partial + ((size_t)gi * T + t) * hidden + d, y[t]);
+  return bad;
+}
+
+// Transposed Q4_K down: lane l covers columns 4l..4l+3 of super-block cr
+// (group g = l/8); wave w takes pairs w and w+4. The 8 lanes of a group
+// decode the scales of 4 neurons each and share them through a per-wave LDS
+// table (row stride 36 floats keeps the 8 groups on distinct banks).
+constexpr int kTabStride = 36;
+
+template <int MODE, int TB>
+__device__ __forceinline__ uint32_t phase_b_q4kt(const PlanHeader& H, const Scratch& S, const GroupDesc& G,
+                                                 const PairDesc* pairs, unsigned gi, unsigned cr, float* hs,
+                                                 float* wtab, double* red) {
+  const unsigned hidden = H.hidden, T = H.burst, count = G.count;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t g = (uint32_t)lane >> 3, nb = 4 * (lane & 7);
+  uint4 q[2][4], hd[2][4];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const unsigned j = wave + kWaves * jj;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q[jj][k] = hd[jj][k] = make_uint4(0, 0, 0, 0);
+    if (j >= count) continue;
+    const PairDesc* P = pairs + G.first + j;
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(P->slice) + 2 * (size_t)P->proj + 4608 * (size_t)cr;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q[jj][k] = ld16(base + 1024 * k + 16 * lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hd[jj][i] = ld16(base + 4096 + 16 * (nb + i));
+  }
+  uint32_t bad = stage_h<MODE>(H, S, G, hs);
+  const unsigned wstride = 2 * 8 * kTabStride + T * 8 * kTabStride;
+  float* tD = wtab + wave * wstride;
+  float* tM = tD + 8 * kTabStride;
+  float* cD = tM + 8 * kTabStride;
   double y[TB][4];
 #pragma unroll
   for (int t = 0; t < TB; ++t)
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) y[t][cc] = 0.0;
-
-  if (G.dn != TQ4_KT) {
-    // [H x 32]: thread = output row d; every wave walks every pair.
-    const unsigned d = cr * kCols + tid;
-    for (unsigned j = 0; j < count; ++j) {
-      const PairDesc* P = pairs + G.first + j;
-      const uint8_t* down = reinterpret_cast<const uint8_t*>(P->slice) + 2 * (size_t)P->proj;
-      const uint32_t tmask = P->tmask;
-      if (MODE == MODE_F32) {
-        // Raw codes once, one fp32 dot per token, fp64 accumulation.
-        uint4 q0, q1 = {0, 0, 0, 0};
-        float sc;
-        if (G.dn == TMXFP4) {
-          q0 = ld16(down + 16 * (size_t)d);
-          uint32_t e = down[16 * (size_t)hidden + d];
-          if (e == 255) bad |= kErrScale;
-          sc = e8m0(e);
-        } else if (G.dn == TQ8_0) {
-          q0 = ld16(down + 16 * (size_t)d);
-          q1 = ld16(down + 16 * (size_t)hidden + 16 * (size_t)d);
-          uint32_t sb = reinterpret_cast<const uint16_t*>(down + 32 * (size_t)hidden)[d];
-          if (half_bad(sb)) bad |= kErrScale;
-          sc = half_to_float(sb);
-        } else {
-          q0 = ld16(down + 16 * (size_t)d);
-          uint32_t sb = reinterpret_cast<const uint16_t*>(down + 16 * (size_t)hidden)[d];
-          if (half_bad(sb)) bad |= kErrScale;
-          sc = half_to_float(sb);
-        }
 #pragma unroll
-        for (int t = 0; t < TB; ++t) {
-          if (t >= (int)T || !((tmask >> t) & 1u)) continue;
-          const float* h = hs + (j * T + t) * kNeurons;
-          float sum = 0.f;
-          if (G.dn == TQ8_0) {
+  for (int jj = 0; jj < 2; ++jj) {
+    const unsigned j = wave + kWaves * jj;
+    if (j >= count) continue;
+    const PairDesc* P = pairs + G.first + j;
+    const uint32_t tmask = P->tmask;
+    float D[4], M[4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              uint32_t v = word(i < 4 ? q0 : q1, i & 3);
-#pragma unroll
-              for (int b = 0; b < 4; ++b) sum = fmaf((float)(int8_t)(v >> (8 * b)), h[4 * i + b], sum);
-            }
-          } else if (G.dn == TMXFP4) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              uint32_t v = word(q0, i);
-#pragma unroll
-              for (int b = 0; b < 4; ++b) {
-                uint32_t byte = v >> (8 * b);
-                sum = fmaf(e2m1(byte & 15u), h[4 * i + b], sum);
-                sum = fmaf(e2m1((byte >> 4) & 15u), h[16 + 4 * i + b], sum);
-              }
-            }
-          } else {
-            float hsum = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              uint32_t v = word(q0, i);
-#pragma unroll
-              for (int b = 0; b < 4; ++b) {
-                uint32_t byte = v >> (8 * b);
-                sum = fmaf((float)(byte & 15u), h[4 * i + b], sum);
-                sum = fmaf((float)((byte >> 4) & 15u), h[16 + 4 * i + b], sum);
-                hsum += h[4 * i + b] + h[16 + 4 * i + b];
-              }
-            }
-            sum -= 8.f * hsum;
-          }
-          y[t][0] += (double)P->gate[t] * ((double)sc * (double)sum);
-        }
-      } else {
-        float w[32];
-        if (!decode_down_row(G.dn, down, hidden, d, w)) bad |= kErrScale;
-#pragma unroll
-        for (int t = 0; t < TB; ++t) {
-          if (t >= (int)T || !((tmask >> t) & 1u)) continue;
-          const float* h = hs + (j * T + t) * kNeurons;
-          double sum = 0.0;
-#pragma unroll
-          for (int n = 0; n < 32; ++n) sum = fma((double)w[n], (double)h[n], sum);
-          y[t][0] += (double)P->gate[t] * sum;
-        }
-      }
+    for (int i = 0; i < 4; ++i) {
+      bool ok;
+      hdr_dm(hd[jj][i], g, D[i], M[i], ok);
+      if (!ok) bad |= kErrScale;
     }
-#pragma unroll
-    for (int t = 0; t < TB; ++t)
-      if (t < (int)T) S.partial[((size_t)gi * T + t) * hidden + d] = y[t][0];
-  } else {
-    // Transposed Q4_K: lane = 4 columns of super-block cr; wave w takes
-    // pairs j = w, w+4, ...; the 4 waves are summed in LDS in wave order.
-    float* tab = wtab + wave * wstride;     // D[8][32], M[8][32] | cD[T][8][32] | B[T][8]
-    float* cD = tab + 512;
-    float* Bt = cD + T * 256;
-    const uint32_t g = (uint32_t)lane >> 3;
-    for (unsigned j = wave; j < count; j += kWaves) {
-      const PairDesc* P = pairs + G.first + j;
-      const uint8_t* base = reinterpret_cast<const uint8_t*>(P->slice) + 2 * (size_t)P->proj + 4608 * (size_t)cr;
-      const uint32_t tmask = P->tmask;
-      uint4 q[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) q[k] = ld16(base + 1024 * k + 16 * lane);
-      // Scale/min table: item lane + 64r -> neuron (lane>>3)+8r, group lane&7.
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = (lane >> 3) + 8 * r, gg = lane & 7;
-        uint4 hd = ld16(base + 4096 + 16 * n);
-        float D, M;
-        bool ok;
-        hdr_dm(hd, gg, D, M, ok);
-        if (!ok) bad |= kErrScale;
-        tab[gg * 32 + n] = D;
-        tab[256 + gg * 32 + n] = M;
-        if (MODE == MODE_F32) {
-#pragma unroll
-          for (int t = 0; t < TB; ++t)
-            if (t < (int)T) cD[t * 256 + gg * 32 + n] = D * hs[(j * T + t) * kNeurons + n];
-        }
-      }
-      if (MODE == MODE_F32) {
-        // B[t][g] = sum_n M[g][n]*h[n] in a fixed order: 4 terms per lane,
-        // then a butterfly over the 8 lanes sharing g.
-#pragma unroll
-        for (int t = 0; t < TB; ++t) {
-          if (t >= (int)T) continue;
-          float part = 0.f;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int n = (lane >> 3) + 8 * r;
-            part += tab[256 + (lane & 7) * 32 + n] * hs[(j * T + t) * kNeurons + n];
-          }
-          part += __shfl_xor(part, 8, 64);
-          part += __shfl_xor(part, 16, 64);
-          part += __shfl_xor(part, 32, 64);
-          if (lane < 8) Bt[t * 8 + lane] = part;
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float B[TB];
+    if (MODE == MODE_F32) {
 #pragma unroll
       for (int t = 0; t < TB; ++t) {
-        if (t >= (int)T || !((tmask >> t) & 1u)) continue;
-        const double gate = (double)P->gate[t];
-        if (MODE == MODE_F32) {
-          const float* cd = cD + t * 256 + g * 32;
-          float s4[4] = {0.f, 0.f, 0.f, 0.f};
+        B[t] = 0.f;
+        if (t >= (int)T) continue;
+        const float* h = hs + (j * T + t) * kNeurons;
+        float part = 0.f;
 #pragma unroll
-          for (int k = 0; k < 4; ++k)
-#pragma unroll
-            for (int wd = 0; wd < 4; ++wd) {
-              uint32_t v = word(q[k], wd);
-#pragma unroll
-              for (int sN = 0; sN < 2; ++sN) {
-                float coef = cd[8 * k + 2 * wd + sN];
-#pragma unroll
-                for (int cc = 0; cc < 4; ++cc)
-                  s4[cc] = fmaf((float)((v >> (4 * (4 * sN + cc))) & 15u), coef, s4[cc]);
-              }
-            }
-          float B = Bt[t * 8 + g];
-#pragma unroll
-          for (int cc = 0; cc < 4; ++cc) y[t][cc] += gate * (double)(s4[cc] - B);
-        } else {
-          const float* h = hs + (j * T + t) * kNeurons;
-          double s4[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-#pragma unroll
-            for (int wd = 0; wd < 4; ++wd) {
-              uint32_t v = word(q[k], wd);
-#pragma unroll
-              for (int sN = 0; sN < 2; ++sN) {
-                const int n = 8 * k + 2 * wd + sN;
-                const float D = tab[g * 32 + n], M = tab[256 + g * 32 + n];
-                const double hn = (double)h[n];
-#pragma unroll
-                for (int cc = 0; cc < 4; ++cc) {
-                  float w = fmaf(D, (float)((v >> (4 * (4 * sN + cc))) & 15u), -M);
-                  s4[cc] = fma((double)w, hn, s4[cc]);
-                }
-              }
-            }
-#pragma unroll
-          for (int cc = 0; cc < 4; ++cc) y[t][cc] += gate * s4[cc];
+        for (int i = 0; i < 4; ++i) {
+          cD[t * 8 * kTabStride + g * kTabStride + nb + i] = D[i] * h[nb + i];
+          part = fmaf(M[i], h[nb + i], part);
         }
+        B[t] = oct_sum(part);
       }
-      __builtin_amdgcn_wave_barrier();
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        tD[g * kTabStride + nb + i] = D[i];
+        tM[g * kTabStride + nb + i] = M[i];
+      }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
-      if (t >= (int)T) continue;
-      __syncthreads();
+      if (t >= (int)T || !((tmask >> t) & 1u)) continue;
+      const double gate = (double)P->gate[t];
+      if (MODE == MODE_F32) {
+        const float4* cd = reinterpret_cast<const float4*>(cD + t * 8 * kTabStride + g * kTabStride);
+        float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) red[wave * kCols + 4 * lane + cc] = y[t][cc];
-      __syncthreads();
-      double v = ((red[tid] + red[kCols + tid]) + red[2 * kCols + tid]) + red[3 * kCols + tid];
-      S.partial[((size_t)gi * T + t) * hidden + cr * kCols + tid] = v;
+        for (int k = 0; k < 4; ++k) {
+          const float4 c0 = cd[2 * k], c1 = cd[2 * k + 1];  // neurons 8k..8k+7
+          const float coef[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+          for (int wd = 0; wd < 4; ++wd) {
+            // Nibble j of the dword: neuron 2wd + j/4, column j%4. Low nibbles
+            // of bytes 0..3 are j = 0,2,4,6; high nibbles j = 1,3,5,7.
+            const uint32_t v = word(q[jj][k], wd);
+            const uint32_t lo = nib_lo(v), hi = nib_hi(v);
+            const float ca = coef[2 * wd], cb = coef[2 * wd + 1];
+            s4[0] = fmaf(ub(lo, 0), ca, s4[0]);
+            s4[1] = fmaf(ub(hi, 0), ca, s4[1]);
+            s4[2] = fmaf(ub(lo, 1), ca, s4[2]);
+            s4[3] = fmaf(ub(hi, 1), ca, s4[3]);
+            s4[0] = fmaf(ub(lo, 2), cb, s4[0]);
+            s4[1] = fmaf(ub(hi, 2), cb, s4[1]);
+            s4[2] = fmaf(ub(lo, 3), cb, s4[2]);
+            s4[3] = fmaf(ub(hi, 3), cb, s4[3]);
+          }
+        }
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) y[t][cc] += gate * (double)(s4[cc] - B[t]);
+      } else {
+        const float* h = hs + (j * T + t) * kNeurons;
+        double s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int wd = 0; wd < 4; ++wd) {
+            const uint32_t v = word(q[jj][k], wd);
+#pragma unroll
+            for (int sN = 0; sN < 2; ++sN) {
+              const int n = 8 * k + 2 * wd + sN;
+              const float Dn = tD[g * kTabStride + n], Mn = tM[g * kTabStride + n];
+              const double hn = (double)h[n];
+#pragma unroll
+              for (int cc = 0; cc < 4; ++cc)
+                s4[cc] = fma((double)fmaf(Dn, (float)((v >> (4 * (4 * sN + cc))) & 15u), -Mn), hn, s4[cc]);
+            }
+          }
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) y[t][cc] += gate * s4[cc];
+      }
     }
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int t = 0; t < TB; ++t) {
+    if (t >= (int)T) continue;
+    __syncthreads();
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) red[wave * kCols + 4 * lane + cc] = y[t][cc];
+    __syncthreads();
+    const int tid = threadIdx.x;
+    const double v = ((red[tid] + red[kCols + tid]) + red[2 * kCols + tid]) + red[3 * kCols + tid];
+    put(S.partial + ((size_t)gi * T + t) * hidden + cr * kCols + tid, v);
+  }
+  return bad;
+}
+
+template <int MODE, int TB>
+__device__ void phase_b(const PlanHeader& H, const uint8_t* plan, const Scratch& S, uint32_t* status,
+                        unsigned task, float* lds) {
+  const unsigned gi = task / H.nranges, cr = task % H.nranges;
+  const GroupDesc G = reinterpret_cast<const GroupDesc*>(plan + H.groups_off)[gi];
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + H.pairs_off);
+  const unsigned hidden = H.hidden, T = H.burst;
+  const int tid = threadIdx.x;
+  // LDS: hs[gmax][T][32] | 4 per-wave scale tables | wave reduction.
+  float* hs = lds;
+  const unsigned wstride = 2 * 8 * kTabStride + T * 8 * kTabStride;
+  float* wtab = hs + H.gmax * T * kNeurons;
+  double* red = reinterpret_cast<double*>(wtab + kWaves * wstride);
+  uint32_t bad;
+  switch (G.dn) {
+    case TQ4_KT: bad = phase_b_q4kt<MODE, TB>(H, S, G, pairs, gi, cr, hs, wtab, red); break;
+    case TMXFP4: bad = phase_b_rows<MODE, TB, TMXFP4>(H, S, G, pairs, gi, cr, hs); break;
+    case TQ8_0: bad = phase_b_rows<MODE, TB, TQ8_0>(H, S, G, pairs, gi, cr, hs); break;
+    default: bad = phase_b_rows<MODE, TB, TQ4_0>(H, S, G, pairs, gi, cr, hs); break;
   }
   if (bad) flag(status, bad);
 
   // The last-arriving group of this output range reduces it, in group order.
+  // Every thread drains its partial stores before the ticket is taken.
   __shared__ uint32_t ticket;
+  drain_stores();
   __syncthreads();
-  if (tid == 0) {
-    ticket = __hip_atomic_fetch_add(S.fin + (size_t)S.parity * kMaxRanges + cr, 1u, __ATOMIC_ACQ_REL,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (tid == 0) ticket = bump(S.fin + (size_t)S.parity * kMaxRanges + cr);
   __syncthreads();
   if (ticket != H.ngroups - 1) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   float* yout = reinterpret_cast<float*>(status + 4);
   const unsigned col = cr * kCols + tid;
   for (unsigned t = 0; t < T; ++t) {
     double v = 0.0;
-    for (unsigned g2 = 0; g2 < H.ngroups; ++g2) v += S.partial[((size_t)g2 * T + t) * hidden + col];
+    for (unsigned g2 = 0; g2 < H.ngroups; ++g2) v += get(S.partial + ((size_t)g2 * T + t) * hidden + col);
     float f = 0.f;
     if (!isfinite(v) || fabs(v) > (double)FLT_MAX) flag(status, kErrRange);
     else f = (float)v;
@@ -1141,17 +1438,17 @@ struct Engine {
   hipStream_t stream = nullptr;
   uint8_t* block[kBlocks] = {};
   Layout lay[kBlocks];
-  uint32_t* done = nullptr;
-  uint32_t* fin = nullptr;
-  float* hbuf = nullptr;
+  uint32_t* done = nullptr;       // [2][kMaxPairs]
+  uint32_t* fin = nullptr;        // [2][kMaxRanges]
+  float* hbuf = nullptr;          // [kMaxPairs][8][32]
   double* partial = nullptr;
   size_t partial_bytes = 0;
-  uint32_t* out = nullptr;
+  uint32_t* out = nullptr;        // [2][out_words]
   uint32_t out_words = 0;
   uint8_t* plan_dev = nullptr;
   uint8_t* plan_host = nullptr;   // pinned
   size_t plan_cap = 0;
-  uint32_t* out_host = nullptr;   // pinned
+  uint32_t* out_host = nullptr;   // pinned: status, pad x3, y
   uint8_t* staging = nullptr;     // device staging for uploads
   size_t staging_bytes = 0;
   uint32_t parity = 0;
@@ -1175,9 +1472,10 @@ int env_int(const char* name, int dflt) {
 // Pairs per down-phase group: about 48 KB of down weights per task.
 uint32_t group_pairs(uint8_t dn) {
   uint32_t per = dn == TQ4_KT ? 4608u : kCols * (uint32_t)row_bytes(dn, kNeurons);
+  uint32_t cap = dn == TQ8_0 ? group_max<TQ8_0>() : dn == TQ4_KT ? group_max<TQ4_KT>() : group_max<TMXFP4>();
   int over = env_int("FRONK_HIP_GROUP_BYTES", 49152);
   uint32_t g = (uint32_t)over / per;
-  return g < 1 ? 1 : g > 64 ? 64 : g;
+  return g < 1 ? 1 : g > cap ? cap : g;
 }
 
 int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, unsigned* grid) {
@@ -1248,8 +1546,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
       if (G.count > gmax) gmax = G.count;
     }
   }
-  const uint32_t nn = (uint32_t)env_int("FRONK_HIP_NEURONS_PER_TASK", 8);
-  if (nn < 4 || nn > 32 || kNeurons % nn || nn % kWaves) return FR_HIP_INVALID;
+  const uint32_t nn = kTaskNeurons;
   H->hidden = hidden;
   H->burst = T;
   H->mode = r->mode;
@@ -1269,9 +1566,9 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   H->x_off = (uint32_t)((H->groups_off + ng * sizeof(GroupDesc) + 255) & ~255u);
   memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
   H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
-  size_t ldsA = (size_t)tchunk * hidden * sizeof(float);
-  size_t wstride = 512 + T * 256 + T * 8;
-  size_t ldsB = (size_t)gmax * T * kNeurons * sizeof(float) + kWaves * wstride * sizeof(float) + 8 +
+  size_t ldsA = T == 1 ? 0 : (size_t)tchunk * hidden * sizeof(float);
+  size_t wstride = 2 * 8 * kTabStride + T * 8 * kTabStride;
+  size_t ldsB = (size_t)gmax * T * kNeurons * sizeof(float) + kWaves * wstride * sizeof(float) +
                 kWaves * kCols * sizeof(double);
   H->lds = (uint32_t)(ldsA > ldsB ? ldsA : ldsB);
   if (H->lds > (uint32_t)kLdsLimit) return FR_HIP_UNSUPPORTED;
@@ -1286,6 +1583,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
 }
 
 int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream) {
+  if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
   Scratch S;
   S.done = E.done;
   S.fin = E.fin;
@@ -1294,7 +1592,6 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
   S.out = E.out;
   S.out_words = E.out_words;
   S.parity = E.parity;
-  if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
   const dim3 g(grid), blk(kThreads);
   const bool one = H.burst == 1;
   switch (H.mode) {
@@ -1318,6 +1615,19 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
 }
 
 #define CK(x) do { if ((x) != hipSuccess) return FR_HIP_IO; } while (0)
+
+// Copy the last launch's status word and fp32 outputs to pinned host memory,
+// stream-ordered. The kernel already applied the reference's narrowing rule
+// (backends/ref.c:37-40, 95): a non-finite or beyond-FLT_MAX sum sets a
+// status bit and the caller returns FR_NUMERIC.
+int fetch_output(hipStream_t s, size_t count, float* y, unsigned* status_out) {
+  const uint32_t* src = E.out + (size_t)E.last_parity * E.out_words;
+  CK(hipMemcpyAsync(E.out_host, src, (4 + count) * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  CK(hipStreamSynchronize(s));
+  if (status_out) *status_out = E.out_host[0];
+  if (y && !E.out_host[0]) memcpy(y, E.out_host + 4, count * sizeof(float));
+  return FR_HIP_OK;
+}
 
 }  // namespace
 
@@ -1348,7 +1658,7 @@ int fr_hip_open(int device) {
   CK(hipMalloc(&E.done, 2 * kMaxPairs * sizeof(uint32_t)));
   CK(hipMalloc(&E.fin, 2 * kMaxRanges * sizeof(uint32_t)));
   CK(hipMalloc(&E.hbuf, (size_t)kMaxPairs * kMaxBurst * kNeurons * sizeof(float)));
-  // Worst case groups: every pair its own group.
+  // Group partials: at most one group per pair, bounded by the group byte cap.
   E.partial_bytes = (size_t)kMaxPairs * kMaxBurst * kMaxHidden * sizeof(double) / 4;
   CK(hipMalloc(&E.partial, E.partial_bytes));
   E.out_words = 4 + kMaxBurst * kMaxHidden;
@@ -1501,14 +1811,8 @@ int fr_hip_launch(const void* host_plan, const void* device_plan, void* stream) 
 
 int fr_hip_last_output(void* stream, float* y, size_t count, unsigned* status) {
   if (!g_open) return FR_HIP_STATE;
-  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : E.stream;
   if (count > (size_t)kMaxBurst * kMaxHidden) return FR_HIP_INVALID;
-  CK(hipStreamSynchronize(s));
-  const uint32_t* src = E.out + (size_t)E.last_parity * E.out_words;
-  CK(hipMemcpy(E.out_host, src, (4 + count) * sizeof(uint32_t), hipMemcpyDeviceToHost));
-  if (status) *status = E.out_host[0];
-  if (y) memcpy(y, E.out_host + 4, count * sizeof(float));
-  return FR_HIP_OK;
+  return fetch_output(stream ? static_cast<hipStream_t>(stream) : E.stream, count, y, status);
 }
 
 int fr_hip_run(const fr_hip_request* req, float* y) {
@@ -1526,15 +1830,15 @@ int fr_hip_run(const fr_hip_request* req, float* y) {
   if (rc) return rc;
   CK(hipEventRecord(E.ev1, E.stream));
   const size_t count = (size_t)H.burst * H.hidden;
-  const uint32_t* src = E.out + (size_t)E.last_parity * E.out_words;
-  CK(hipMemcpyAsync(E.out_host, src, (4 + count) * sizeof(uint32_t), hipMemcpyDeviceToHost, E.stream));
-  CK(hipStreamSynchronize(E.stream));
+  unsigned status = 0;
+  rc = fetch_output(E.stream, count, nullptr, &status);
+  if (rc) return rc;
   float ms = 0.f;
   if (hipEventElapsedTime(&ms, E.ev0, E.ev1) == hipSuccess) E.sample.last_kernel_ns = ms * 1e6;
   ++E.sample.runs;
-  uint32_t status = E.out_host[0];
   if (status & kErrTimeout) return FR_HIP_IO;
   if (status) return FR_HIP_NUMERIC;
+  // y is written only on success: untouched on failure.
   memcpy(y, E.out_host + 4, count * sizeof(float));
   return FR_HIP_OK;
 }
