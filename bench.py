@@ -1,0 +1,304 @@
+#!/usr/bin/env python3
+"""Layer-share measurement of the expert neuron-slice path on one MI355X.
+
+A step is one layer call of the node backend's run() (src/backend.h:63): one
+kernel launch over every (routed expert, owned 32-neuron slice) pair of a
+request. Default workload: 512 experts x 20 owned slices resident at
+hidden=4096, all Q4_K (down stored transposed), one token, 10 experts drawn
+uniformly without replacement, gates = softmax of N(0,1) logits, x ~ N(0,1).
+Weights are synthetic (seeded, generated on the device), resident in HBM
+before timing; calls rotate over 8 resident layers so that the working set
+between reuses is far beyond the 256 MB Infinity Cache. Each step's launch
+plan (routing, gates, x) is also resident in HBM when timing starts.
+
+stdout: exactly one JSON line. Everything else goes to stderr.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload q4k]
+                  [--cpu-seconds S] [--no-cpu]
+  python bench.py --copy-kernel BYTES   plain device copy, for scaling the
+                                        FETCH_SIZE/WRITE_SIZE counters
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "quantized-weight GB/s (% HBM peak) + MoE layer-share tokens/s, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+HIDDEN = 4096
+SLICES = 20
+LAYERS = 8
+SEED = 0x4652_4F4E_4B00_0002
+
+WORKLOADS = {
+    "q4k": dict(fmt="FMT_Q4KT", burst=1, routing="uniform",
+                text="MoE layer-share decode: 10 of 512 experts x 20 owned slices x 32 neurons, hidden 4096, "
+                     "Q4_K gate/up/down (down stored transposed), 1 token"),
+    "q8": dict(fmt="FMT_Q8", burst=1, routing="uniform",
+               text="MoE layer-share decode: 10 of 512 experts x 20 slices, hidden 4096, Q8_0 gate/up/down, 1 token"),
+    "mxfp4": dict(fmt="FMT_MXFP4", burst=1, routing="uniform",
+                  text="MoE layer-share decode: 10 of 512 experts x 20 slices, hidden 4096, MXFP4 gate/up/down, "
+                       "1 token"),
+    "native": dict(fmt="FMT_NATIVE", burst=1, routing="uniform",
+                   text="MoE layer-share decode: 10 of 512 experts x 20 slices, hidden 4096, Q4_K gate/up, "
+                        "MXFP4 down [H x 32], 1 token"),
+    "mtp4": dict(fmt="FMT_Q4KT", burst=4, routing="zipf",
+                 text="MoE layer-share burst: 4 tokens, per-token top-10 of 512 under Zipf(1.1), 20 slices, "
+                      "hidden 4096, Q4_K (down transposed); bytes counted once per unique expert"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def softmax_gates(rng, burst):
+    logits = rng.standard_normal((burst, 10))
+    g = np.exp(logits - logits.max(axis=1, keepdims=True))
+    out = np.zeros((burst, 11), np.float32)
+    out[:, :10] = g / g.sum(axis=1, keepdims=True)
+    return out
+
+
+def draw_routes(rng, burst, routing, zipf_perm, zipf_p):
+    if routing == "uniform":
+        return np.stack([rng.choice(512, 10, replace=False) for _ in range(burst)]).astype(np.uint16)
+    return np.stack([zipf_perm[rng.choice(512, 10, replace=False, p=zipf_p)] for _ in range(burst)]).astype(np.uint16)
+
+
+def make_requests(n, burst, routing, seed):
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(512)
+    p = 1.0 / np.arange(1, 513) ** 1.1
+    p /= p.sum()
+    reqs = []
+    for i in range(n):
+        experts = draw_routes(rng, burst, routing, perm, p)
+        gates = softmax_gates(rng, burst)
+        x = rng.standard_normal((burst, HIDDEN)).astype(np.float32)
+        reqs.append((i % LAYERS, experts, gates, x))
+    return reqs
+
+
+def algorithmic_bytes(fa, fmt, experts, gates):
+    """Weight bytes read once per unique (expert, owned slice), plus x and y
+    (4*T*H bytes each)."""
+    T = experts.shape[0]
+    lay_slice, lay_shared = slice_sizes(fa, fmt)
+    unique = len(set(int(e) for e in experts.ravel()))
+    weights = unique * SLICES * lay_slice
+    if np.any(gates[:, 10] != 0):
+        weights += SLICES * lay_shared
+    return weights, weights + 8 * T * HIDDEN
+
+
+def slice_sizes(fa, fmt):
+    # Slice sizes follow from the unit size: 48 layers x (512 routed + shared).
+    routed = {fa.FMT_Q4KT: 221184, fa.FMT_Q8: 417792, fa.FMT_MXFP4: 208896, fa.FMT_NATIVE: 217088}[fmt]
+    shared = 3 * (HIDDEN // 32) * 34 * 32
+    assert fa.unit_bytes(HIDDEN, fmt) == 48 * (512 * routed + shared)
+    return routed, shared
+
+
+def copy_kernel(nbytes):
+    import torch
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "launches": 5}))
+
+
+def cpu_baseline(fa, eng, fmt, reqs, budget_s):
+    """The oracle's scalar restatement of the reference ref backend
+    (backends/ref.c:57-98), one host thread, on a bounded sample of the same
+    requests; the GPU's outputs for the same requests are compared with it."""
+    import oracle
+    from fixtures import host_units
+    lay = oracle.layout(HIDDEN, fmt)
+    done, seconds, wbytes = 0, 0.0, 0
+    worst = [0.0, 0.0]
+    for layer, experts, gates, x in reqs:
+        units = host_units(lay, SEED, layer, experts)
+        req = oracle.Req()
+        req.layer, req.burst, req.hidden = layer, experts.shape[0], HIDDEN
+        req.experts()[:req.burst] = experts
+        req.gates()[:req.burst] = gates
+        req.xs()[:req.burst, :HIDDEN] = x
+        t0 = time.perf_counter()
+        rc, ref = oracle.ref_run(units, fmt, False, req)
+        seconds += time.perf_counter() - t0
+        if rc != 0:
+            raise RuntimeError(f"oracle ref_run failed with {rc}")
+        rc, y = eng.run(layer, experts, gates, x, fa.MODE_F32)
+        if rc != fa.OK:
+            raise RuntimeError(f"fr_hip_run failed with {rc}")
+        for t in range(req.burst):
+            rc, err = oracle.compare(ref[t], y[t])
+            worst = [max(worst[0], err[0]), max(worst[1], err[1])]
+        wbytes += algorithmic_bytes(fa, fmt, experts, gates)[0]
+        done += 1
+        del units
+        if seconds >= budget_s:
+            break
+    return {
+        "value": wbytes / seconds / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"{done} calls of this workload through the oracle's scalar restatement of ref "
+                  f"(backends/ref.c:57-98), 1 thread, {seconds:.1f} s",
+        "tokens_per_s": done * reqs[0][1].shape[0] / seconds,
+        "gpu_vs_oracle": {"rel_l2_max": worst[0], "normalized_max": worst[1], "calls": done},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", default="q4k", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--run-calls", type=int, default=200)
+    ap.add_argument("--copy-kernel", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the layer share is built and timed on a "
+              "single MI355X, and its multi-GPU sharding is a design, not a measured path.", file=sys.stderr)
+        sys.exit(2)
+    if args.copy_kernel:
+        copy_kernel(args.copy_kernel)
+        return
+
+    import torch
+    import fronk_amd as fa
+
+    wl = WORKLOADS[args.workload]
+    fmt = getattr(fa, wl["fmt"])
+    burst = wl["burst"]
+    lib = fa.lib()
+    eng = fa.Engine(0)
+    t0 = time.perf_counter()
+    for b in range(SLICES):
+        fa.check(eng.synthetic(b, HIDDEN, fmt, LAYERS, SEED), "fr_hip_synthetic")
+    log(f"resident: {SLICES} blocks x {LAYERS} layers generated in {time.perf_counter() - t0:.1f} s")
+
+    n = args.warmup + args.steps
+    reqs = make_requests(n, burst, wl["routing"], SEED + 1)
+    cap = lib.fr_hip_plan_bytes(burst, HIDDEN)
+    stride = (cap + 255) // 256 * 256
+    host = np.zeros((n, stride), np.uint8)
+    alg = np.zeros(n)
+    wts = np.zeros(n)
+    grid = 0
+    for i, (layer, experts, gates, x) in enumerate(reqs):
+        plan, grid = eng.plan(layer, experts, gates, x, fa.MODE_F32)
+        host[i, :plan.size] = plan
+        wts[i], alg[i] = algorithmic_bytes(fa, fmt, experts, gates)
+    dev = torch.from_numpy(host).to("cuda")
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    hptr = host.ctypes.data
+    dptr = dev.data_ptr()
+    sptr = C.c_void_p(stream.cuda_stream)
+    launch = lib.fr_hip_launch
+
+    def enqueue(i):
+        rc = launch(C.c_void_p(hptr + i * stride), C.c_void_p(dptr + i * stride), sptr)
+        if rc != fa.OK:
+            raise RuntimeError(f"fr_hip_launch failed with {rc}")
+
+    for i in range(args.warmup):
+        enqueue(i)
+    stream.synchronize()
+    torch.cuda.synchronize()
+
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for i in range(args.warmup, n):
+            enqueue(i)
+        ev1.record(stream)
+    stream.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = ev0.elapsed_time(ev1) / args.steps
+
+    status = C.c_uint(0)
+    fa.check(lib.fr_hip_last_output(sptr, None, 0, C.byref(status)), "fr_hip_last_output")
+    if status.value:
+        raise RuntimeError(f"layer kernel reported status {status.value}")
+
+    timed = slice(args.warmup, n)
+    ms_per_step = wall * 1e3 / args.steps
+    weight_gbs = wts[timed].sum() / wall / 1e9
+    alg_per_launch = float(alg[timed].mean())
+    achieved = alg_per_launch / (kernel_ms * 1e-3) / 1e9
+
+    # run() wall time: plan build, H2D, launch, D2H and narrowing per call.
+    run_us = []
+    for layer, experts, gates, x in reqs[:args.run_calls]:
+        t1 = time.perf_counter()
+        rc, _ = eng.run(layer, experts, gates, x, fa.MODE_F32)
+        run_us.append((time.perf_counter() - t1) * 1e6)
+        if rc != fa.OK:
+            raise RuntimeError(f"fr_hip_run failed with {rc}")
+    run_us = np.array(run_us)
+
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"layer_kernel_{args.workload}_traffic.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        cpu = cpu_baseline(fa, eng, fmt, reqs[args.warmup:], args.cpu_seconds)
+
+    for b in range(SLICES):
+        eng.release(b)
+
+    out = {
+        "metric": METRIC,
+        "value": round(weight_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded device generator; Q4_K d/dmin fp16 U[1e-3,1e-2], x ~ N(0,1))",
+        "config": {"workload": wl["text"], "hidden": HIDDEN, "experts": 512, "active_experts": 10,
+                   "slices": SLICES, "burst": burst, "format": wl["fmt"][4:], "mode": "f32",
+                   "layers_rotated": LAYERS},
+        "hbm_frac": round(weight_gbs / HBM_PEAK_GBS, 4),
+        "tokens_per_s": round(burst * args.steps / wall, 1),
+        "kernel_us": round(kernel_ms * 1e3, 3),
+        "weight_bytes_per_call": float(wts[timed].mean()),
+        "grid": grid,
+        "run_wall_us": {"p50": round(float(np.percentile(run_us, 50)), 2),
+                        "p99": round(float(np.percentile(run_us, 99)), 2)},
+        "run_wall_gbs": round(float(wts[:args.run_calls].mean() / (np.median(run_us) * 1e-6) / 1e9), 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -40,6 +40,7 @@ SIGNATURES = {
     "fr_hip_upload": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint64, C.c_uint, C.c_uint]),
     "fr_hip_reserve": (C.c_int, [C.c_uint, C.c_uint, C.c_uint]),
     "fr_hip_refresh": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.c_uint]),
+    "fr_hip_synthetic": (C.c_int, [C.c_uint, C.c_uint, C.c_uint, C.c_uint, C.c_uint64]),
     "fr_hip_release": (C.c_int, [C.c_uint]),
     "fr_hip_unit_bytes": (C.c_uint64, [C.c_uint, C.c_uint]),
     "fr_hip_run": (C.c_int, [C.POINTER(Request), C.POINTER(C.c_float)]),
@@ -52,6 +53,7 @@ SIGNATURES = {
     "fr_hip_debug_dequant": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_dequant_down": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_quantize": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.POINTER(C.c_float)]),
+    "fr_hip_debug_read": (C.c_int, [C.c_uint, C.c_uint64, C.c_void_p, C.c_uint64]),
 }
 
 _lib = None
@@ -128,6 +130,14 @@ class Engine:
 
     def refresh(self, block, unit, layer, expert):
         return lib().fr_hip_refresh(block, np.asarray(unit).ctypes.data, layer, expert)
+
+    def synthetic(self, block, hidden, fmt, layers, seed):
+        return lib().fr_hip_synthetic(block, hidden, fmt, layers, seed)
+
+    def read(self, block, offset, length):
+        out = np.zeros(length, np.uint8)
+        check(lib().fr_hip_debug_read(block, offset, out.ctypes.data, length), "fr_hip_debug_read")
+        return out
 
     def release(self, block):
         return lib().fr_hip_release(block)

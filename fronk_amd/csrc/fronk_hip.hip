@@ -1276,36 +1276,123 @@ __device__ __forceinline__ uint32_t down_source(uint8_t dn, uint32_t hidden, uin
   return 18 * (r / 2) + r % 2;
 }
 
-// Nibble (neuron n, column j) of a native transposed Q4_K down.
-__device__ __forceinline__ uint32_t q4kt_nibble(const uint8_t* src, uint32_t row_bytes, uint32_t n, uint32_t j) {
-  const uint8_t* b = src + (size_t)n * row_bytes + 144 * (j / 256);
+// Nibble (neuron n, column j) of a native transposed Q4_K down whose first
+// byte is src[base]. Src is a byte source: a pointer or the generator below.
+template <class Src>
+__device__ __forceinline__ uint32_t q4kt_nibble(const Src& src, uint32_t base, uint32_t row_bytes, uint32_t n,
+                                                uint32_t j) {
+  const uint32_t b = base + n * row_bytes + 144 * (j / 256);
   uint32_t jj = j % 256, chunk = jj / 64, i = jj % 32, half = (jj % 64) / 32;
-  return (b[16 + 32 * chunk + i] >> (4 * half)) & 15u;
+  return (src[b + 16 + 32 * chunk + i] >> (4 * half)) & 15u;
 }
 
-__device__ __forceinline__ uint8_t q4kt_byte(const uint8_t* src, uint32_t hidden, uint32_t o) {
+template <class Src>
+__device__ __forceinline__ uint8_t q4kt_byte(const Src& src, uint32_t base, uint32_t hidden, uint32_t o) {
   const uint32_t row_bytes = 144 * (hidden / 256);
   uint32_t sb = o / 4608, r = o % 4608;
   if (r >= 4096) {
     uint32_t n = (r - 4096) / 16, i = (r - 4096) % 16;
-    return src[(size_t)n * row_bytes + 144 * sb + i];
+    return src[base + n * row_bytes + 144 * sb + i];
   }
   uint32_t k = r / 1024, l = (r % 1024) / 16, m = r % 16, wd = m / 4, bb = m % 4;
   uint32_t n = 8 * k + 2 * wd + bb / 2;
   uint32_t j = 256 * sb + 4 * l + 2 * (bb % 2);
-  return (uint8_t)(q4kt_nibble(src, row_bytes, n, j) | (q4kt_nibble(src, row_bytes, n, j + 1) << 4));
+  return (uint8_t)(q4kt_nibble(src, base, row_bytes, n, j) | (q4kt_nibble(src, base, row_bytes, n, j + 1) << 4));
 }
 
-__device__ uint8_t retile_byte(const SliceShape& s, const uint8_t* src, uint32_t o) {
+// Byte o of a re-tiled slice whose reference-layout bytes are src[0..).
+template <class Src>
+__device__ uint8_t retile_byte(const SliceShape& s, const Src& src, uint32_t o) {
   const uint32_t nch = s.hidden / 64;
   if (o < 2 * s.proj) {
     uint32_t row_bytes = s.proj / kNeurons, rbase = (o / row_bytes) * row_bytes;
     return src[rbase + gu_source((uint8_t)s.gu, nch, o - rbase)];
   }
   uint32_t od = o - 2 * s.proj;
-  const uint8_t* dsrc = src + 2 * s.proj;
-  if (s.dn == TQ4_KT) return q4kt_byte(dsrc, s.hidden, od);
-  return dsrc[down_source((uint8_t)s.dn, s.hidden, od)];
+  if (s.dn == TQ4_KT) return q4kt_byte(src, 2 * s.proj, s.hidden, od);
+  return src[2 * s.proj + down_source((uint8_t)s.dn, s.hidden, od)];
+}
+
+// ------------------------------------------------------------ synthetic data
+//
+// Measurement weights generated on the device: every byte of a slice in the
+// reference layout is a pure function of (seed, block, layer, expert, byte
+// offset), so the generator is a byte source for retile_byte and writes the
+// re-tiled block directly. Distributions: Q4_K nibbles and 6-bit scales
+// uniform, d and dmin = fp16(U[1e-3, 1e-2]); Q8_0 int8 uniform on [-127, 127]
+// with an fp16(U[1e-3, 1e-2]) scale; MXFP4 codes uniform, E8M0 uniform on
+// [118, 130]; Q4_0 nibbles uniform with an fp16(U[1e-3, 1e-2]) scale. The hash
+// is the splitmix64 finaliser (Steele, Lea, Flood 2014).
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t synth_hash(uint64_t key, unsigned domain, uint64_t word) {
+  return mix64(key ^ ((uint64_t)domain << 60) ^ word);
+}
+
+// fp16 bits of 1e-3 + 9e-3*u (u = top 24 bits of h / 2^24), round to nearest
+// even. Explicitly rounded fp64 operations: no contraction into an fma.
+__device__ __forceinline__ uint16_t synth_scale(uint64_t h) {
+  const double u = (double)(h >> 40) * 0x1p-24;
+  const double v = __dadd_rn(1e-3, __dmul_rn(9e-3, u));
+  const uint64_t bits = (uint64_t)__double_as_longlong(v);
+  int e = (int)((bits >> 52) & 0x7ff) - 1023 + 15;
+  uint64_t mant = bits & ((1ull << 52) - 1), q = mant >> 42, rem = mant & ((1ull << 42) - 1);
+  if (rem > (1ull << 41) || (rem == (1ull << 41) && (q & 1))) ++q;
+  if (q == 1024) {
+    q = 0;
+    ++e;
+  }
+  return (uint16_t)((unsigned)e << 10 | (unsigned)q);
+}
+
+__device__ __forceinline__ uint32_t type_block_bytes(uint32_t type) {
+  return type == TQ4_K ? 144 : type == TQ8_0 ? 34 : type == TMXFP4 ? 17 : 18;
+}
+
+__device__ __forceinline__ uint8_t synth_block_byte(uint32_t type, uint64_t key, uint32_t s, uint32_t k) {
+  const uint32_t o = s + k;
+  if (type == TQ4_K) {
+    if (k < 4) {
+      const uint16_t h = synth_scale(synth_hash(key, 1, s + (k & 2)));
+      return (uint8_t)(k & 1 ? h >> 8 : h);
+    }
+  } else if (type == TQ8_0) {
+    if (k < 2) {
+      const uint16_t h = synth_scale(synth_hash(key, 1, s));
+      return (uint8_t)(k & 1 ? h >> 8 : h);
+    }
+    return (uint8_t)(int8_t)((int)((synth_hash(key, 2, o) >> 32) % 255u) - 127);
+  } else if (type == TMXFP4) {
+    if (k == 0) return (uint8_t)(118 + (synth_hash(key, 1, s) >> 32) % 13u);
+  } else if (k < 2) {
+    const uint16_t h = synth_scale(synth_hash(key, 1, s));
+    return (uint8_t)(k & 1 ? h >> 8 : h);
+  }
+  return (uint8_t)(synth_hash(key, 0, o >> 3) >> (8 * (o & 7)));
+}
+
+// Byte source: slice bytes in the reference layout, generated on demand.
+struct SynthSrc {
+  uint64_t key;
+  uint32_t gu, dn;            // block types of gate/up rows and of down rows
+  uint32_t proj, gu_row, dn_row;
+  __device__ __forceinline__ uint8_t operator[](uint32_t o) const {
+    if (o < 2 * proj) {
+      const uint32_t rl = (o < proj ? o : o - proj) % gu_row, k = rl % type_block_bytes(gu);
+      return synth_block_byte(gu, key, o - k, k);
+    }
+    const uint32_t k = (o - 2 * proj) % dn_row % type_block_bytes(dn);
+    return synth_block_byte(dn, key, o - k, k);
+  }
+};
+
+__host__ __device__ __forceinline__ uint64_t synth_key(uint64_t seed, uint32_t block, uint32_t layer, uint32_t expert) {
+  return mix64(seed) ^ ((uint64_t)block << 54) ^ ((uint64_t)layer << 44) ^ ((uint64_t)expert << 32);
 }
 
 // Slices [first, first+count) of consecutive layout: routed slices of one
@@ -1320,6 +1407,29 @@ __global__ void retile_kernel(const uint8_t* __restrict__ src, uint8_t* __restri
   const uint8_t* in = src + off;
   uint8_t* out = dst + off;
   for (uint32_t o = threadIdx.x; o < s.slice; o += blockDim.x) out[o] = retile_byte(s, in, o);
+}
+
+// Synthetic slices [first, first+n) written re-tiled into dst (one workgroup
+// per slice, four bytes per thread and step; slice sizes are multiples of 16).
+__global__ void synth_kernel(uint8_t* __restrict__ dst, SliceShape routed, SliceShape shared, uint64_t layer_bytes,
+                             uint32_t first_slice, uint32_t nslices, uint64_t seed, uint32_t block) {
+  if (blockIdx.x >= nslices) return;
+  const uint32_t sidx = first_slice + blockIdx.x, layer = sidx / 513, e = sidx % 513;
+  const bool sh = e == kShared;
+  const SliceShape& s = sh ? shared : routed;
+  SynthSrc src;
+  src.key = synth_key(seed, block, layer, e);
+  src.gu = s.gu;
+  src.dn = s.dn == TQ4_KT ? TQ4_K : s.dn;
+  src.proj = s.proj;
+  src.gu_row = s.proj / kNeurons;
+  src.dn_row = s.dn == TQ4_KT ? (s.hidden / 256) * 144 : type_block_bytes(s.dn);
+  uint32_t* out = reinterpret_cast<uint32_t*>(dst + layer * layer_bytes + (uint64_t)e * routed.slice);
+  for (uint32_t w = threadIdx.x; w < s.slice / 4; w += blockDim.x) {
+    uint32_t v = 0;
+    for (uint32_t i = 0; i < 4; ++i) v |= (uint32_t)retile_byte(s, src, 4 * w + i) << (8 * i);
+    out[w] = v;
+  }
 }
 
 // Debug: decode re-tiled gate/up row(s) with the hot path's decoder.
@@ -1362,7 +1472,7 @@ __global__ void debug_retile_row(SliceShape s, const uint8_t* in, uint8_t* outb,
 
 __global__ void debug_retile_down(uint8_t dn, uint32_t hidden, const uint8_t* in, uint8_t* outb, uint32_t bytes) {
   for (uint32_t o = threadIdx.x; o < bytes; o += blockDim.x)
-    outb[o] = dn == TQ4_KT ? q4kt_byte(in, hidden, o) : in[down_source(dn, hidden, o)];
+    outb[o] = dn == TQ4_KT ? q4kt_byte(in, 0u, hidden, o) : in[down_source(dn, hidden, o)];
 }
 
 __global__ void debug_quantize(float* x, uint32_t groups) {
@@ -1438,6 +1548,7 @@ struct Engine {
   hipStream_t stream = nullptr;
   uint8_t* block[kBlocks] = {};
   Layout lay[kBlocks];
+  uint32_t layers[kBlocks] = {};  // resident layers [0, layers) of each block
   uint32_t* done = nullptr;       // [2][kMaxPairs]
   uint32_t* fin = nullptr;        // [2][kMaxRanges]
   float* hbuf = nullptr;          // [kMaxPairs][8][32]
@@ -1490,6 +1601,8 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     ++nloaded;
   }
   if (!nloaded) return FR_HIP_STATE;
+  for (int b = 0; b < kBlocks; ++b)
+    if (E.block[b] && r->layer >= E.layers[b]) return FR_HIP_STATE;
   if (cap < plan_capacity(T, hidden)) return FR_HIP_INVALID;
   // Unique experts, token-major first appearance (backends/avx2.c:661-672).
   uint16_t ids[kMaxUnique];
@@ -1742,6 +1855,7 @@ int fr_hip_upload(unsigned block, const void* unit, uint64_t len, unsigned hidde
   if (hipMalloc(&dev, l.block) != hipSuccess) return FR_HIP_IO;
   E.block[block] = dev;
   E.lay[block] = l;
+  E.layers[block] = kLayers;
   const uint8_t* src = static_cast<const uint8_t*>(unit);
   // Two layers per step bound the staging buffer.
   for (uint32_t layer = 0; layer < (uint32_t)kLayers; layer += 2) {
@@ -1771,6 +1885,41 @@ int fr_hip_reserve(unsigned block, unsigned hidden, unsigned format) {
   }
   E.block[block] = dev;
   E.lay[block] = l;
+  E.layers[block] = kLayers;
+  return FR_HIP_OK;
+}
+
+int fr_hip_synthetic(unsigned block, unsigned hidden, unsigned format, unsigned layers, uint64_t seed) {
+  if (!g_open) return FR_HIP_STATE;
+  if (block >= (unsigned)kBlocks || !layers || layers > (unsigned)kLayers) return FR_HIP_INVALID;
+  Layout l;
+  if (!layout_of(hidden, format, l)) return FR_HIP_INVALID;
+  if (E.block[block]) return FR_HIP_STATE;
+  CK(hipSetDevice(E.device));
+  uint8_t* dev = nullptr;
+  if (hipMalloc(&dev, (size_t)layers * l.layer) != hipSuccess) return FR_HIP_IO;
+  const uint32_t n = layers * 513;
+  hipLaunchKernelGGL(synth_kernel, dim3(n), dim3(256), 0, E.stream, dev, shape_of(l, false), shape_of(l, true),
+                     l.layer, 0u, n, seed, (uint32_t)block);
+  if (hipGetLastError() != hipSuccess || hipStreamSynchronize(E.stream) != hipSuccess) {
+    (void)hipFree(dev);
+    return FR_HIP_IO;
+  }
+  E.block[block] = dev;
+  E.lay[block] = l;
+  E.layers[block] = layers;
+  return FR_HIP_OK;
+}
+
+int fr_hip_debug_read(unsigned block, uint64_t offset, void* out, uint64_t len) {
+  if (!g_open) return FR_HIP_STATE;
+  if (block >= (unsigned)kBlocks || !out) return FR_HIP_INVALID;
+  if (!E.block[block]) return FR_HIP_STATE;
+  const uint64_t have = (uint64_t)E.layers[block] * E.lay[block].layer;
+  if (offset > have || len > have - offset) return FR_HIP_INVALID;
+  CK(hipSetDevice(E.device));
+  CK(hipStreamSynchronize(E.stream));
+  CK(hipMemcpy(out, E.block[block] + offset, len, hipMemcpyDeviceToHost));
   return FR_HIP_OK;
 }
 
@@ -1779,6 +1928,7 @@ int fr_hip_refresh(unsigned block, const void* unit, unsigned layer, unsigned ex
   if (block >= (unsigned)kBlocks || !unit || layer >= (unsigned)kLayers || expert > (unsigned)kShared)
     return FR_HIP_INVALID;
   if (!E.block[block]) return FR_HIP_STATE;
+  if (layer >= E.layers[block]) return FR_HIP_INVALID;
   CK(hipSetDevice(E.device));
   return upload_slices((int)block, static_cast<const uint8_t*>(unit), layer * 513 + expert, 1);
 }
@@ -1790,6 +1940,7 @@ int fr_hip_release(unsigned block) {
   (void)hipStreamSynchronize(E.stream);
   (void)hipFree(E.block[block]);
   E.block[block] = nullptr;
+  E.layers[block] = 0;
   return FR_HIP_OK;
 }
 

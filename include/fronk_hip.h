@@ -76,6 +76,16 @@ int fr_hip_reserve(unsigned block, unsigned hidden, unsigned format);
  * borrowed host bytes, so that run() sees later host-side changes
  * (src/native.c:118-130 mutates the unit after load). */
 int fr_hip_refresh(unsigned block, const void *unit, unsigned layer, unsigned expert);
+/* Measurement data without a host unit (no reference counterpart; the
+ * reference's bench fills host units, src/bench.c:279-334): allocate layers
+ * [0, layers) of block `block` and fill every slice with seeded synthetic
+ * weights, written re-tiled by a device generator. Byte o of slice (layer,
+ * expert) in the reference slice layout is a pure function of (seed, block,
+ * layer, expert, o): Q4_K d/dmin = fp16(U[1e-3,1e-2]) with uniform nibbles
+ * and 6-bit scales, Q8_0 int8 U[-127,127] with an fp16(U[1e-3,1e-2]) scale,
+ * MXFP4 E8M0 U[118,130] with uniform codes. run() on a layer >= `layers`
+ * returns FR_HIP_STATE. */
+int fr_hip_synthetic(unsigned block, unsigned hidden, unsigned format, unsigned layers, uint64_t seed);
 /* Free one block's device copy (unload: src/backend.h:62). */
 int fr_hip_release(unsigned block);
 /* Unit bytes of a (hidden, format) pair, 0 if unsupported. */
@@ -110,6 +120,8 @@ int fr_hip_debug_dequant(unsigned type, const void *row, unsigned n, float *out)
  * (element (d, n) = weight of neuron n for output d) for every down format. */
 int fr_hip_debug_dequant_down(unsigned format, const void *down, unsigned hidden, float *out);
 int fr_hip_debug_quantize(const float *x, unsigned n, float *out);
+/* Copy `len` re-tiled device bytes of a block, from byte `offset`. */
+int fr_hip_debug_read(unsigned block, uint64_t offset, void *out, uint64_t len);
 
 #ifdef __cplusplus
 }

@@ -98,6 +98,14 @@ def lib():
         L.fo_fill_slice.argtypes = [u8p, P(Layout), C.c_uint, P(C.c_uint32)]
         L.fo_sha256.restype = None
         L.fo_sha256.argtypes = [C.c_void_p, C.c_size_t, u8p]
+        L.fo_synth_key.restype = C.c_uint64
+        L.fo_synth_key.argtypes = [C.c_uint64, C.c_uint, C.c_uint, C.c_uint]
+        L.fo_synth_scale.restype = C.c_uint16
+        L.fo_synth_scale.argtypes = [C.c_uint64]
+        L.fo_synth_byte.restype = C.c_uint8
+        L.fo_synth_byte.argtypes = [P(Layout), C.c_uint64, C.c_uint, C.c_uint64]
+        L.fo_synth_slice.restype = None
+        L.fo_synth_slice.argtypes = [u8p, P(Layout), C.c_uint64, C.c_uint, C.c_uint, C.c_uint]
         _lib = L
     return _lib
 
@@ -194,3 +202,16 @@ def lcg(seed):
     s = C.c_uint32(seed)
     v = lib().fo_lcg(C.byref(s))
     return v, s.value
+
+
+def synth_slice(lay, seed, block, layer, expert):
+    """Synthetic measurement slice (layer, expert) of ownership block `block`
+    in the reference slice layout, as a new uint8 array."""
+    n = lay.shared_slice if expert == 512 else lay.slice
+    out = np.zeros(n, np.uint8)
+    lib().fo_synth_slice(u8ptr(out), C.byref(lay), seed, block, layer, expert)
+    return out
+
+
+def synth_scale(h):
+    return lib().fo_synth_scale(h)

@@ -647,3 +647,102 @@ void fo_fill_slice(uint8_t *p, const fo_layout *l, unsigned id, uint32_t *seed) 
         for (unsigned d = 0; d < l->hidden; ++d) fixture_row(p + 2 * proj + d * drow, dn, FO_NEURONS, seed);
     }
 }
+
+/* ------------------------------------------------------------------------
+ * Synthetic measurement weights (not a reference function). Distributions:
+ * Q4_K nibbles and 6-bit scales/mins uniform, d and dmin = fp16(U[1e-3,1e-2]);
+ * Q8_0 int8 uniform on [-127, 127] with an fp16(U[1e-3,1e-2]) scale; MXFP4
+ * codes uniform over the 16 values with E8M0 uniform on [118, 130]; Q4_0
+ * nibbles uniform with an fp16(U[1e-3,1e-2]) scale. Every byte is a pure
+ * function of (seed, block, layer, expert, byte offset in the slice), so a
+ * generator on the device can write the same bytes in any order or layout.
+ * The hash is the splitmix64 finaliser (Steele, Lea, Flood 2014). */
+static uint64_t mix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+uint64_t fo_synth_key(uint64_t seed, unsigned block, unsigned layer, unsigned expert) {
+    return mix64(seed) ^ ((uint64_t)block << 54) ^ ((uint64_t)layer << 44) ^ ((uint64_t)expert << 32);
+}
+
+static uint64_t synth_hash(uint64_t key, unsigned domain, uint64_t word) {
+    return mix64(key ^ ((uint64_t)domain << 60) ^ word);
+}
+
+/* fp16 bits of 1e-3 + 9e-3*u, u = the top 24 bits of h over 2^24, rounded to
+ * nearest even; the value is a normal binary16 (exponent field 5..8). */
+uint16_t fo_synth_scale(uint64_t h) {
+    double u = (double)(h >> 40) * 0x1p-24;
+    double v = 1e-3 + 9e-3 * u;
+    uint64_t bits;
+    memcpy(&bits, &v, sizeof(bits));
+    int e = (int)((bits >> 52) & 0x7ff) - 1023 + 15;
+    uint64_t mant = bits & ((1ull << 52) - 1), q = mant >> 42, rem = mant & ((1ull << 42) - 1);
+    if (rem > (1ull << 41) || (rem == (1ull << 41) && (q & 1))) ++q;
+    if (q == 1024) {
+        q = 0;
+        ++e;
+    }
+    return (uint16_t)((unsigned)e << 10 | (unsigned)q);
+}
+
+static unsigned type_block_bytes(unsigned type) {
+    return type == FO_Q4_K ? 144 : type == FO_Q8_0 ? 34 : type == FO_MXFP4 ? 17 : 18;
+}
+
+/* Byte k of the quantization block of `type` that starts at slice offset s. */
+static uint8_t synth_block_byte(unsigned type, uint64_t key, uint64_t s, unsigned k) {
+    uint64_t o = s + k;
+    switch (type) {
+    case FO_Q4_K:
+        if (k < 4) {
+            uint16_t h = fo_synth_scale(synth_hash(key, 1, s + (k & 2)));
+            return (uint8_t)(k & 1 ? h >> 8 : h);
+        }
+        break;
+    case FO_Q8_0:
+        if (k < 2) {
+            uint16_t h = fo_synth_scale(synth_hash(key, 1, s));
+            return (uint8_t)(k & 1 ? h >> 8 : h);
+        }
+        return (uint8_t)(int8_t)((int)((synth_hash(key, 2, o) >> 32) % 255u) - 127);
+    case FO_MXFP4:
+        if (k == 0) return (uint8_t)(118 + (synth_hash(key, 1, s) >> 32) % 13u);
+        break;
+    default: /* Q4_0 */
+        if (k < 2) {
+            uint16_t h = fo_synth_scale(synth_hash(key, 1, s));
+            return (uint8_t)(k & 1 ? h >> 8 : h);
+        }
+        break;
+    }
+    return (uint8_t)(synth_hash(key, 0, o >> 3) >> (8 * (o & 7)));
+}
+
+/* Byte o of the slice (layer, expert) of ownership block `block`, in the
+ * reference's slice layout: 32 gate rows, 32 up rows, then the down rows
+ * (src/native.h:9-15; transposed for FO_FMT_Q4KT). */
+uint8_t fo_synth_byte(const fo_layout *l, uint64_t key, unsigned expert, uint64_t o) {
+    int shared = expert == FO_SHARED;
+    unsigned gu = shared ? l->shared_gu_type : l->gu_type, dn = shared ? l->shared_down_type : l->down_type;
+    uint64_t proj = shared ? l->shared_proj : l->proj;
+    if (o < 2 * proj) {
+        uint64_t row = fo_row_bytes(gu, l->hidden), rl = (o < proj ? o : o - proj) % row;
+        unsigned k = (unsigned)(rl % type_block_bytes(gu));
+        return synth_block_byte(gu, key, o - k, k);
+    }
+    uint64_t od = o - 2 * proj;
+    uint64_t drow = (!shared && l->down_transposed) ? fo_row_bytes(dn, l->hidden) : fo_row_bytes(dn, FO_NEURONS);
+    unsigned k = (unsigned)(od % drow % type_block_bytes(dn));
+    return synth_block_byte(dn, key, o - k, k);
+}
+
+void fo_synth_slice(uint8_t *slice, const fo_layout *l, uint64_t seed, unsigned block, unsigned layer,
+                    unsigned expert) {
+    uint64_t key = fo_synth_key(seed, block, layer, expert);
+    uint64_t n = expert == FO_SHARED ? l->shared_slice : l->slice;
+    for (uint64_t o = 0; o < n; ++o) slice[o] = fo_synth_byte(l, key, expert, o);
+}

@@ -94,5 +94,13 @@ int fo_vector_format(unsigned index, const fo_req *req, uint32_t mask, const cha
 uint32_t fo_lcg(uint32_t *seed);
 void fo_fill_slice(uint8_t *slice, const fo_layout *l, unsigned expert, uint32_t *seed);
 
+/* Synthetic measurement weights (distributions in fronk_oracle.c): byte o of
+ * slice (layer, expert) of ownership block `block`, reference slice layout. */
+uint64_t fo_synth_key(uint64_t seed, unsigned block, unsigned layer, unsigned expert);
+uint16_t fo_synth_scale(uint64_t h);
+uint8_t fo_synth_byte(const fo_layout *l, uint64_t key, unsigned expert, uint64_t o);
+void fo_synth_slice(uint8_t *slice, const fo_layout *l, uint64_t seed, unsigned block, unsigned layer,
+                    unsigned expert);
+
 void fo_sha256(const void *data, size_t len, uint8_t out[32]);
 #endif

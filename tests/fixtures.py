@@ -120,3 +120,16 @@ def native_fixture(lay, layer=47):
             v = lib.fo_lcg(C.byref(s))
             x[t, j] = np.float32((v % 257) - 128) / np.float32(128)
     return data, gates, x
+
+
+def host_units(lay, seed, layer, experts, blocks=20):
+    """Sparse host copies of the device's synthetic blocks 0..blocks-1 holding
+    just the slices of `experts` (and the shared slice) at `layer`."""
+    used = sorted(set(int(e) for e in np.asarray(experts).ravel()) | {oracle.SHARED})
+    units = []
+    for b in range(blocks):
+        u = sparse_unit(lay)
+        for e in used:
+            slice_view(u, lay, layer, e)[:] = oracle.synth_slice(lay, seed, b, layer, e)
+        units.append(u)
+    return units

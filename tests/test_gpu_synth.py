@@ -1,0 +1,103 @@
+"""Device-side synthetic measurement data (fr_hip_synthetic).
+
+The device generator must write, re-tiled, exactly the bytes that the oracle's
+generator (fo_synth_slice) writes in the reference slice layout: a block filled
+on the device is compared byte for byte with a block whose slices were
+generated on the host and uploaded through the ordinary load path. Then a full
+20-block layer share filled on the device is run end to end against the oracle
+on the host-generated copy of the routed slices.
+"""
+import numpy as np
+import pytest
+
+import fronk_amd as fa
+import oracle
+from fixtures import oracle_request, slice_view, softmax_gates, sparse_unit, zipf_routes
+from test_gpu_parity import check_close
+
+pytestmark = pytest.mark.gpu
+
+H = 4096
+
+
+@pytest.fixture(scope="module")
+def eng():
+    e = fa.Engine(0)
+    yield e
+    for b in range(20):
+        e.release(b)
+
+
+@pytest.mark.parametrize("fmt", [fa.FMT_Q4KT, fa.FMT_NATIVE, fa.FMT_Q8, fa.FMT_MXFP4])
+def test_device_generator_matches_oracle_bytes(eng, fmt):
+    lay = oracle.layout(H, fmt)
+    seed = 0x5EED + fmt
+    print(f"synthetic bytes fmt={fmt}", flush=True)
+    assert eng.synthetic(6, H, fmt, 2, seed) == fa.OK
+    assert eng.reserve(7, H, fmt) == fa.OK
+    try:
+        unit = sparse_unit(lay)
+        for layer, e in [(0, 0), (1, 511), (1, 512), (0, 137)]:
+            view = slice_view(unit, lay, layer, e)
+            view[:] = oracle.synth_slice(lay, seed, 6, layer, e)
+            assert eng.refresh(7, unit, layer, e) == fa.OK
+            off = oracle.slice_offset(lay, layer, e)
+            a = eng.read(6, off, view.size)
+            b = eng.read(7, off, view.size)
+            assert np.array_equal(a, b), (fmt, layer, e, int(np.argmax(a != b)))
+        # Layers beyond the generated ones are not resident.
+        assert eng.refresh(6, unit, 2, 0) == fa.INVALID
+    finally:
+        assert eng.release(6) == fa.OK
+        assert eng.release(7) == fa.OK
+
+
+def test_absent_layer_is_state(eng):
+    assert eng.synthetic(2, H, fa.FMT_Q4KT, 1, 1) == fa.OK
+    try:
+        x = np.zeros((1, H), np.float32)
+        gates = np.zeros((1, 11), np.float32)
+        gates[0, :10] = 0.1
+        rc, _ = eng.run(1, np.arange(10).reshape(1, 10), gates, x)
+        assert rc == fa.STATE
+        rc, _ = eng.run(0, np.arange(10).reshape(1, 10), gates, x)
+        assert rc == fa.OK
+    finally:
+        eng.release(2)
+
+
+@pytest.mark.parametrize("fmt", [fa.FMT_Q4KT, fa.FMT_MXFP4])
+def test_layer_share_on_synthetic_blocks(eng, fmt):
+    """The measurement workload itself: 20 owned slices of every expert, T=1
+    with 10 uniform experts and a Zipf T=4 burst, against the oracle on the
+    host-generated copies of the routed slices."""
+    lay = oracle.layout(H, fmt)
+    seed = 77 + fmt
+    rng = np.random.default_rng(fmt)
+    for b in range(20):
+        assert eng.synthetic(b, H, fmt, 1, seed) == fa.OK
+    try:
+        cases = [rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10), zipf_routes(rng, 4)]
+        used = sorted(set(np.concatenate([c.ravel() for c in cases]).tolist()))
+        units = []
+        for b in range(20):
+            u = sparse_unit(lay)
+            for e in used:
+                slice_view(u, lay, 0, e)[:] = oracle.synth_slice(lay, seed, b, 0, e)
+            units.append(u)
+        for experts in cases:
+            T = experts.shape[0]
+            gates = np.zeros((T, 11), np.float32)
+            gates[:, :10] = softmax_gates(rng, T)
+            x = rng.standard_normal((T, H)).astype(np.float32)
+            for mode in (fa.MODE_F32, fa.MODE_Q8):
+                print(f"layer share fmt={fmt} T={T} mode={mode}", flush=True)
+                rc, y = eng.run(0, experts, gates, x, mode)
+                assert rc == fa.OK
+                req = oracle_request(0, experts, gates, x)
+                rc, ref = oracle.ref_run(units, fmt, mode == fa.MODE_Q8, req)
+                assert rc == 0
+                check_close(ref, y, mode, (fmt, T, mode))
+    finally:
+        for b in range(20):
+            eng.release(b)
