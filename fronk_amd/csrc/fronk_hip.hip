@@ -50,6 +50,9 @@ constexpr int kMaxHidden = 4096;
 constexpr int kMaxRanges = kMaxHidden / kCols;
 constexpr int kLdsLimit = 64 * 1024;
 constexpr uint32_t kSpinLimit = 1u << 16;   // about 0.1 s of polling
+constexpr int kDecodeThreads = 512;         // decode kernel: 8 wavefronts
+constexpr int kDecodeWaves = kDecodeThreads / 64;
+constexpr int kDecodeGridMax = 256;         // decode workgroups (one per CU at most)
 
 // Status bits of the output word.
 constexpr uint32_t kErrScale = 1;     // referenced non-finite scale
@@ -78,8 +81,13 @@ struct PlanHeader {
   uint32_t ngroups, nranges, ntA, ntB;
   uint32_t nn, tchunk, pairs_off, groups_off;
   uint32_t x_off, total, gmax, lds;
+  uint32_t kind, grid, tpw, pad;   // kernel (KIND_*), its grid, decode tasks per workgroup
 };
-static_assert(sizeof(PlanHeader) == 64, "header layout");
+static_assert(sizeof(PlanHeader) == 80, "header layout");
+
+// Which kernel a plan runs: the two-phase layer kernel, or the single-token
+// decode kernel for all-Q4_K units with the transposed down.
+enum : uint32_t { KIND_LAYER = 0, KIND_DECODE = 1 };
 
 struct Scratch {
   uint32_t* done;            // [2][kMaxPairs] phase-A wave completions per pair
@@ -87,6 +95,8 @@ struct Scratch {
   float* hbuf;               // [kMaxPairs][8][32]
   double* partial;           // [groups][burst][hidden]
   uint32_t* out;             // [2][out_words]: status, pad x3, y
+  float* wgpart;             // [kDecodeGridMax][hidden]: decode workgroup partials
+  uint32_t* bar;             // [2]: decode workgroups past their partial store
   uint32_t out_words;
   uint32_t parity;
 };
@@ -232,7 +242,19 @@ __device__ __forceinline__ uint32_t nib_hi(uint32_t v) {
   return r;
 }
 
-__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+// Weight and plan addresses arrive as 64-bit integers, so the compiler sees
+// generic pointers and would emit FLAT loads; a FLAT load also counts against
+// the LDS/scalar counter, which makes every LDS wait and barrier wait for all
+// outstanding weight loads. These go through the global address space.
+template <typename T>
+__device__ __forceinline__ T gld(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) {
+  const u32x4 v = gld<u32x4>(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ uint32_t word(const uint4& v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
@@ -307,15 +329,15 @@ __device__ __forceinline__ void load_raw(const uint8_t* row, int nch, int c, Lan
   } else if (type == TQ8_0) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) r.q[p] = ld16(row + 16 * nch * p + 16 * c);
-    r.h.x = *reinterpret_cast<const uint32_t*>(row + 64 * nch + 4 * c);
+    r.h.x = gld<uint32_t>(row + 64 * nch + 4 * c);
   } else if (type == TMXFP4) {
     r.q[0] = ld16(row + 16 * c);
     r.q[1] = ld16(row + 16 * nch + 16 * c);
-    r.h.x = *reinterpret_cast<const uint16_t*>(row + 32 * nch + 2 * c);
+    r.h.x = gld<uint16_t>(row + 32 * nch + 2 * c);
   } else {
     r.q[0] = ld16(row + 16 * c);
     r.q[1] = ld16(row + 16 * nch + 16 * c);
-    r.h.x = *reinterpret_cast<const uint32_t*>(row + 32 * nch + 4 * c);
+    r.h.x = gld<uint32_t>(row + 32 * nch + 4 * c);
   }
 }
 
@@ -882,11 +904,11 @@ __device__ __forceinline__ uint32_t phase_b_rows(const PlanHeader& H, const Scra
     q0[j] = ld16(down + 16 * (size_t)d);
     if (DN == TQ8_0) {
       q1[j] = ld16(down + 16 * (size_t)hidden + 16 * (size_t)d);
-      sw[j] = reinterpret_cast<const uint16_t*>(down + 32 * (size_t)hidden)[d];
+      sw[j] = gld<uint16_t>(down + 32 * (size_t)hidden + 2 * (size_t)d);
     } else if (DN == TMXFP4) {
-      sw[j] = down[16 * (size_t)hidden + d];
+      sw[j] = gld<uint8_t>(down + 16 * (size_t)hidden + d);
     } else {
-      sw[j] = reinterpret_cast<const uint16_t*>(down + 16 * (size_t)hidden)[d];
+      sw[j] = gld<uint16_t>(down + 16 * (size_t)hidden + 2 * (size_t)d);
     }
   }
   uint32_t bad = stage_h<MODE>(H, S, G, hs);
@@ -1197,21 +1219,379 @@ __device__ void phase_b(const PlanHeader& H, const uint8_t* plan, const Scratch&
 }
 
 // TILE = 1 for single-token requests, 8 for bursts (phase A in tiles of 4).
+// Clear the other parity's counters and status for the next launch (whichever
+// kernel it runs). Called by workgroup 0.
+__device__ __forceinline__ void clear_other_parity(const Scratch& S) {
+  const uint32_t other = S.parity ^ 1u;
+  for (unsigned i = threadIdx.x; i < kMaxPairs; i += blockDim.x) S.done[(size_t)other * kMaxPairs + i] = 0;
+  if (threadIdx.x < kMaxRanges) S.fin[(size_t)other * kMaxRanges + threadIdx.x] = 0;
+  if (threadIdx.x == 0) {
+    S.out[(size_t)other * S.out_words] = 0;
+    S.bar[other] = 0;
+  }
+}
+
 template <int MODE, int TILE>
 __global__ __launch_bounds__(kThreads) void layer_kernel(const uint8_t* __restrict__ plan, Scratch S) {
   extern __shared__ __align__(16) float lds[];
   const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
   uint32_t* status = S.out + (size_t)S.parity * S.out_words;
-  if (blockIdx.x == 0) {
-    // Clear the other parity's counters and status for the next launch.
-    const uint32_t other = S.parity ^ 1u;
-    for (unsigned i = threadIdx.x; i < kMaxPairs; i += kThreads) S.done[(size_t)other * kMaxPairs + i] = 0;
-    if (threadIdx.x < kMaxRanges) S.fin[(size_t)other * kMaxRanges + threadIdx.x] = 0;
-    if (threadIdx.x == 0) S.out[(size_t)other * S.out_words] = 0;
-  }
+  if (blockIdx.x == 0) clear_other_parity(S);
   const unsigned b = blockIdx.x;
   if (b < H.ntA) phase_a<MODE, TILE == 1 ? 1 : 4>(H, plan, S, status, b, lds);
   else phase_b<MODE, TILE>(H, plan, S, status, b - H.ntA, lds);
+}
+
+// ------------------------------------------------------------ decode kernel
+//
+// Single token, every pair routed Q4_K with the transposed Q4_K down (the
+// down rows are per neuron). Because the down of neuron n needs only h_n, a
+// task (pair, 8 neurons) carries its own gate/up rows, h and down rows: no
+// h crosses workgroups. Workgroup w of G (at most one per CU) runs tasks w,
+// w+G, w+2G, ... in order, so the result does not depend on timing. Per task, wavefront i streams the gate
+// and up rows of neuron i (lane c: columns 64c..64c+63), a DPP tree gives a
+// and u, h = SiLU(a)*u (backends/ref.c:82-83, in fp32: this kernel serves the
+// F32 mode only). For the down, wavefront i owns super-blocks 2i and 2i+1
+// for the whole kernel: lane l accumulates the 8 columns 8(l%32)..8(l%32)+7
+// of super-block 2i + l/32 over the task's 8 neurons in registers. After the
+// last task each workgroup stores its fp32 partial with plain stores, and a
+// second small kernel on the same stream, decode_reduce, sums the G partials
+// in a fixed order: the kernel boundary is the global barrier and makes the
+// partials visible across XCDs, which in-kernel coherent stores, counters and
+// polling would do at about 2 us per hop.
+
+// The next task's bytes are copied by the load units straight into LDS
+// (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16*i), so no
+// registers are tied up by the prefetch. The copies are issued from inline
+// assembly with explicit waits: the compiler, which cannot tell these LDS
+// writes from its own LDS reads, would otherwise wait for every copy in
+// flight before each read. Each wave issues the same number of copies per
+// task on every path, so the waits are exact, and each wave reads back only
+// what it copied except the table headers, which a barrier covers.
+__device__ __forceinline__ void dma16(const void* g, const void* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+
+constexpr int kDecodeGuCopies = 7;   // gate/up quants 4, gate/up headers 2, table headers 1
+constexpr int kDecodeDnCopies = 2;   // down nibbles
+
+struct DecodeGu {                     // one task's gate/up bytes and down headers
+  uint4 q[kDecodeWaves][2][2][64];   // [wave][gate, up][part][lane]
+  uint4 h[kDecodeWaves][2][16];      // [wave][gate, up][super-block] row headers
+  uint4 th[128];                     // down headers [super-block * 8 + neuron]
+};
+struct DecodeDn {
+  uint4 q[kDecodeWaves][2][64];      // [wave][columns 8j..8j+3, 8j+4..8j+7][lane]
+};
+struct DecodeLds {
+  DecodeGu gu[2];
+  DecodeDn dn[2];
+  float D[16][8][8];                 // [super-block][group][neuron] d*sc*gate*h
+  float M[16][8][8];                 // dmin*mi*gate*h
+  float h[kDecodeWaves];
+};
+
+// Gate/up rows of neuron 8*ng + wave (lane c: parts 0 and 1 of chunk c; lanes
+// 0..15: super-block headers, clamped) and table headers 16*wave + lane.
+__device__ __forceinline__ void issue_gu(const PlanHeader& H, const PairDesc* pairs, unsigned task, int wave,
+                                         int lane, DecodeGu& st) {
+  const unsigned ng = task & 3, nch = H.hidden / 64, nsb = H.hidden / 256;
+  const PairDesc* P = pairs + (task >> 2);
+  const uint8_t* slice = reinterpret_cast<const uint8_t*>(P->slice);
+  const uint32_t proj = P->proj, row = proj / kNeurons, n = 8 * ng + (unsigned)wave;
+  const unsigned c = min((unsigned)lane, nch - 1), s16 = min((unsigned)lane & 15, nsb - 1);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const uint8_t* rp = slice + (r ? proj : 0) + (size_t)n * row;
+    dma16(rp + 16 * c, &st.q[wave][r][0][0]);
+    dma16(rp + 16 * nch + 16 * c, &st.q[wave][r][1][0]);
+    if (lane < 16) dma16(rp + 32 * nch + 16 * s16, &st.h[wave][r][0]);
+  }
+  const unsigned idx = 16 * (unsigned)wave + ((unsigned)lane & 15);
+  const unsigned tsb = min(idx >> 3, nsb - 1), tn = idx & 7;
+  if (lane < 16)
+    dma16(slice + 2 * (size_t)proj + 4608 * (size_t)tsb + 4096 + 16 * (8 * ng + tn), &st.th[16 * wave]);
+}
+
+// Down nibbles: super-block 2*wave + lane/32 (clamped), chunks 2j, 2j+1.
+__device__ __forceinline__ void issue_dn(const PlanHeader& H, const PairDesc* pairs, unsigned task, int wave,
+                                         int lane, DecodeDn& st) {
+  const unsigned ng = task & 3, nsb = H.hidden / 256;
+  const PairDesc* P = pairs + (task >> 2);
+  const uint8_t* down = reinterpret_cast<const uint8_t*>(P->slice) + 2 * (size_t)P->proj;
+  const unsigned sb = min(2 * (unsigned)wave + ((unsigned)lane >> 5), nsb - 1), j = (unsigned)lane & 31;
+  const uint8_t* q = down + 4608 * (size_t)sb + 1024 * ng + 32 * j;
+  dma16(q, &st.q[wave][0][0]);
+  dma16(q + 16, &st.q[wave][1][0]);
+}
+
+// SiLU(a)*u in fp32 with the stable sigmoid form; a, u or h outside fp32
+// is the reference's FR_NUMERIC (backends/ref.c:37-40).
+__device__ __forceinline__ float silu_mul_f32(float a, float u, uint32_t& bad) {
+  const float e = __expf(-fabsf(a));
+  const float sig = a >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
+  const float h = a * sig * u;
+  if (!isfinite(a) || !isfinite(u) || !isfinite(h)) {
+    bad |= kErrRange;
+    return 0.f;
+  }
+  return h;
+}
+
+// x of one 32-column group as three signed int8 digits of a 24-bit fixed
+// point value: X_j = rint(x_j * 2^(22 - E)) with 2^E > max|x_j| (so
+// |X_j| <= 2^22), X_j = D0 + 256*D1 + 65536*D2, D0, D1 in [-128, 127],
+// |D2| <= 64. words[d][i] packs digit d of columns 4i..4i+3. Returns
+// 2^(E - 22), the value of one unit. The rounding error of each x_j is at
+// most 2^-23 of the group's largest |x|.
+__device__ __forceinline__ float x_digits(const float4* x4, uint32_t (&words)[3][8]) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = fmaxf(m, fmaxf(fmaxf(fabsf(x4[i].x), fabsf(x4[i].y)), fmaxf(fabsf(x4[i].z), fabsf(x4[i].w))));
+  int e = 0;
+  if (m > 0.f) (void)frexpf(m, &e);   // m = f * 2^e, f in [0.5, 1)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float c[4] = {x4[i].x, x4[i].y, x4[i].z, x4[i].w};
+    uint32_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int X = __float2int_rn(ldexpf(c[b], 22 - e));
+      const int d0 = (int)(int8_t)(X & 0xff);
+      const int x1 = (X - d0) >> 8;
+      const int d1 = (int)(int8_t)(x1 & 0xff);
+      const int d2 = (x1 - d1) >> 8;
+      w0 |= (uint32_t)(d0 & 0xff) << (8 * b);
+      w1 |= (uint32_t)(d1 & 0xff) << (8 * b);
+      w2 |= (uint32_t)(d2 & 0xff) << (8 * b);
+    }
+    words[0][i] = w0;
+    words[1][i] = w1;
+    words[2][i] = w2;
+  }
+  return ldexpf(1.f, e - 22);
+}
+
+// Lane partial of a Q4_K row in integer arithmetic: per 32-column group,
+// sum_j q_j * X_j from three v_dot4_i32_i8 chains (one per digit), combined
+// exactly in 32 bits (|sum| < 2^31), then scaled: d*sc*unit*S - dmin*mi*X.
+__device__ __forceinline__ float lane_dot_q4k_i8(const LaneRaw& r, const float sc[2], const float mn[2],
+                                                 const uint32_t (&xa)[3][8], const uint32_t (&xb)[3][8], float ua,
+                                                 float ub_, float X0, float X1) {
+  int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    // Byte k of dword i: column 4i+k (low nibble, group A), 32+4i+k (high, group B).
+    const uint32_t v = word(r.q[i >> 2], i & 3);
+    const int lo = (int)nib_lo(v), hi = (int)nib_hi(v);
+    a0 = __builtin_amdgcn_sdot4(lo, (int)xa[0][i], a0, false);
+    a1 = __builtin_amdgcn_sdot4(lo, (int)xa[1][i], a1, false);
+    a2 = __builtin_amdgcn_sdot4(lo, (int)xa[2][i], a2, false);
+    b0 = __builtin_amdgcn_sdot4(hi, (int)xb[0][i], b0, false);
+    b1 = __builtin_amdgcn_sdot4(hi, (int)xb[1][i], b1, false);
+    b2 = __builtin_amdgcn_sdot4(hi, (int)xb[2][i], b2, false);
+  }
+  const int sa = (int)((uint32_t)a0 + ((uint32_t)a1 << 8) + ((uint32_t)a2 << 16));
+  const int sb = (int)((uint32_t)b0 + ((uint32_t)b1 << 8) + ((uint32_t)b2 << 16));
+  return (sc[0] * ((float)sa * ua) - mn[0] * X0) + (sc[1] * ((float)sb * ub_) - mn[1] * X1);
+}
+
+// Device-coherent 16-byte store: written through to memory so that a
+// workgroup on another XCD reads it after the writer has drained.
+__device__ __forceinline__ void store16_coherent(float* p, float4 v) {
+  const u32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(w) : "memory");
+}
+
+__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* __restrict__ plan, Scratch S) {
+  const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
+  uint32_t* status = S.out + (size_t)S.parity * S.out_words;
+  if (blockIdx.x == 0) clear_other_parity(S);
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + H.pairs_off);
+  const unsigned hidden = H.hidden, nch = hidden / 64, nsb = hidden / 256, G = gridDim.x;
+  const unsigned ntask = 4 * H.npairs, lastt = ntask - 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool active = lane < (int)nch;
+  const int c = active ? lane : 0;
+  __shared__ __align__(16) DecodeLds L;
+
+  float4 x[16];
+  {
+    const float4* xs = reinterpret_cast<const float4*>(plan + H.x_off) + 16 * c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = xs[i];
+  }
+  float X0 = 0.f, X1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    X0 += (x[i].x + x[i].y) + (x[i].z + x[i].w);
+    X1 += (x[8 + i].x + x[8 + i].y) + (x[8 + i].z + x[8 + i].w);
+  }
+  // x as int8 digits per 32-column group (A: columns 0..31 of the lane's
+  // chunk, B: 32..63). Computing them waits for the x loads here, before
+  // the first copy is issued, not inside the loop.
+  uint32_t xa[3][8], xb[3][8];
+  const float ua = x_digits(x, xa), ubs = x_digits(x + 8, xb);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(xa[0][i]), "+v"(xa[1][i]), "+v"(xa[2][i]));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(xb[0][i]), "+v"(xb[1][i]), "+v"(xb[2][i]));
+  asm volatile("" : "+v"(X0), "+v"(X1));
+  float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  uint32_t bad = 0;
+
+  unsigned task = blockIdx.x;
+  issue_gu(H, pairs, min(task, lastt), wave, lane, L.gu[0]);
+  issue_dn(H, pairs, min(task, lastt), wave, lane, L.dn[0]);
+  for (unsigned k = 0; task < ntask; ++k, task += G) {
+    const unsigned b = k & 1;
+    const unsigned nxt = min(task + G, lastt);
+    issue_gu(H, pairs, nxt, wave, lane, L.gu[b ^ 1]);
+    // In flight, oldest first: gu(k), dn(k), gu(k+1). Wait for gu(k).
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDecodeDnCopies + kDecodeGuCopies) : "memory");
+    const DecodeGu& G0 = L.gu[b];
+    float au[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      LaneRaw rr;
+      rr.q[0] = G0.q[wave][r][0][c];
+      rr.q[1] = G0.q[wave][r][1][c];
+      rr.h = G0.h[wave][r][c >> 2];
+      float sc[2], mn[2];
+      const bool ok = raw_scales<TQ4_K>(rr, c, sc, mn);
+      if (active && !ok) bad |= kErrScale;
+      const float part = lane_dot_q4k_i8(rr, sc, mn, xa, xb, ua, ubs, X0, X1);
+      au[r] = wave_total(active ? part : 0.f);
+    }
+    const float h = silu_mul_f32(au[0], au[1], bad);
+    if (lane == 0) L.h[wave] = pairs[task >> 2].gate[0] * h;
+    __syncthreads();
+    // Every wave is past the down of task k-1: its buffer can be refilled.
+    issue_dn(H, pairs, nxt, wave, lane, L.dn[b ^ 1]);
+    {
+      const unsigned sb = (unsigned)tid >> 5, tn = ((unsigned)tid >> 2) & 7, g0 = 2 * (tid & 3);
+      if (sb < nsb) {
+        const uint4 hdr = G0.th[8 * sb + tn];
+        const float gh = L.h[tn];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          float D, M;
+          bool ok;
+          hdr_dm(hdr, g0 + kk, D, M, ok);
+          if (!ok) bad |= kErrScale;
+          L.D[sb][g0 + kk][tn] = D * gh;
+          L.M[sb][g0 + kk][tn] = M * gh;
+        }
+      }
+    }
+    __syncthreads();
+    // In flight: dn(k), gu(k+1), dn(k+1). Wait for dn(k).
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDecodeGuCopies + kDecodeDnCopies) : "memory");
+    const unsigned sb = 2 * (unsigned)wave + ((unsigned)lane >> 5), j = (unsigned)lane & 31;
+    if (sb < nsb) {
+      const unsigned g = j >> 2;   // columns 8j..8j+7 lie in group 8j/32
+      const float4* cd = reinterpret_cast<const float4*>(&L.D[sb][g][0]);
+      const float4* cm = reinterpret_cast<const float4*>(&L.M[sb][g][0]);
+      const float4 d0 = cd[0], d1 = cd[1], m0 = cm[0], m1 = cm[1];
+      const float coef[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      const float msum = ((m0.x + m0.y) + (m0.z + m0.w)) + ((m1.x + m1.y) + (m1.z + m1.w));
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const uint4 dq = L.dn[b].q[wave][half][lane];
+        float s4[4] = {-msum, -msum, -msum, -msum};
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+          // Dword wd: neurons 2wd (bytes 0,1) and 2wd+1 (bytes 2,3); low
+          // nibbles columns 0 and 2, high nibbles columns 1 and 3.
+          const uint32_t v = word(dq, wd);
+          const uint32_t lo = nib_lo(v), hi = nib_hi(v);
+          const float ca = coef[2 * wd], cb = coef[2 * wd + 1];
+          s4[0] = fmaf(ub(lo, 0), ca, s4[0]);
+          s4[1] = fmaf(ub(hi, 0), ca, s4[1]);
+          s4[2] = fmaf(ub(lo, 1), ca, s4[2]);
+          s4[3] = fmaf(ub(hi, 1), ca, s4[3]);
+          s4[0] = fmaf(ub(lo, 2), cb, s4[0]);
+          s4[1] = fmaf(ub(hi, 2), cb, s4[1]);
+          s4[2] = fmaf(ub(lo, 3), cb, s4[2]);
+          s4[3] = fmaf(ub(hi, 3), cb, s4[3]);
+        }
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) y[4 * half + cc] += s4[cc];
+      }
+    }
+  }
+  // Copies past the last task (clamped prefetches) land before exit.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (bad) flag(status, bad);
+  // Workgroup partial, position-major so that each store instruction covers
+  // 1 KB: wavefront w, half h, lane l -> positions 4*(128w + 64h + l)..+3,
+  // columns 256*sb + 8j + 4h..+3 (sb = 2w + l/32, j = l%32). The kernel
+  // boundary makes the partials visible to decode_reduce.
+  float* mine = S.wgpart + (size_t)blockIdx.x * kMaxHidden;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+    *reinterpret_cast<float4*>(mine + 4 * (128 * wave + 64 * hh + lane)) =
+        make_float4(y[4 * hh], y[4 * hh + 1], y[4 * hh + 2], y[4 * hh + 3]);
+}
+
+// Position p of a decode partial -> output column (see above).
+__device__ __forceinline__ unsigned decode_column(unsigned p) {
+  const unsigned w = p >> 9, hh = (p >> 8) & 1, l = (p >> 2) & 63, cc = p & 3;
+  return 256 * (2 * w + (l >> 5)) + 8 * (l & 31) + 4 * hh + cc;
+}
+
+// Sum of the G decode partials, 16 positions per workgroup: thread (ps, q)
+// adds partials ps, ps+128 of positions 16*blockIdx + 4q..4q+3 in fp64,
+// then a fixed binary tree over the 128 ps; narrowing with the reference's
+// overflow rule (backends/ref.c:95) and the status word of decode_kernel.
+constexpr int kReduceThreads = 512;
+constexpr int kReducePositions = 16;
+static_assert(kDecodeGridMax <= 2 * (kReduceThreads / (kReducePositions / 4)), "two partials per reduce lane");
+__global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* __restrict__ plan, Scratch S,
+                                                                unsigned G) {
+  const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
+  uint32_t* status = S.out + (size_t)S.parity * S.out_words;
+  float* yout = reinterpret_cast<float*>(status + 4);
+  constexpr unsigned kLanes = kReduceThreads / (kReducePositions / 4);   // partial lanes
+  const unsigned tid = threadIdx.x, q = tid & 3, ps = tid >> 2;
+  const unsigned p0 = kReducePositions * blockIdx.x + 4 * q;
+  double v[4] = {0.0, 0.0, 0.0, 0.0};
+  float4 r[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const unsigned g = ps + kLanes * k;
+    r[k] = g < G ? *reinterpret_cast<const float4*>(S.wgpart + (size_t)g * kMaxHidden + p0)
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    v[0] += (double)r[k].x;
+    v[1] += (double)r[k].y;
+    v[2] += (double)r[k].z;
+    v[3] += (double)r[k].w;
+  }
+  __shared__ double red[kLanes][kReducePositions + 1];
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) red[ps][4 * q + cc] = v[cc];
+  __syncthreads();
+#pragma unroll
+  for (unsigned stride = kLanes / 2; stride > 0; stride >>= 1) {
+    if (ps < stride)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) red[ps][4 * q + cc] += red[ps + stride][4 * q + cc];
+    __syncthreads();
+  }
+  if (tid < kReducePositions) {
+    const unsigned col = decode_column(kReducePositions * blockIdx.x + tid);
+    if (col < H.hidden) {
+      const double t = red[0][tid];
+      float f = 0.f;
+      if (!isfinite(t) || fabs(t) > (double)FLT_MAX) flag(status, kErrRange);
+      else f = (float)t;
+      yout[col] = f;
+    }
+  }
 }
 
 // ------------------------------------------------------- load re-tiling
@@ -1545,6 +1925,7 @@ SliceShape shape_of(const Layout& l, bool shared) {
 
 struct Engine {
   int device = -1;
+  unsigned cus = 0;               // compute units: bound on co-resident decode workgroups
   hipStream_t stream = nullptr;
   uint8_t* block[kBlocks] = {};
   Layout lay[kBlocks];
@@ -1556,6 +1937,8 @@ struct Engine {
   size_t partial_bytes = 0;
   uint32_t* out = nullptr;        // [2][out_words]
   uint32_t out_words = 0;
+  float* wgpart = nullptr;        // [kDecodeGridMax][kMaxHidden]
+  uint32_t* bar = nullptr;        // [2]
   uint8_t* plan_dev = nullptr;
   uint8_t* plan_host = nullptr;   // pinned
   size_t plan_cap = 0;
@@ -1685,8 +2068,27 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
                 kWaves * kCols * sizeof(double);
   H->lds = (uint32_t)(ldsA > ldsB ? ldsA : ldsB);
   if (H->lds > (uint32_t)kLdsLimit) return FR_HIP_UNSUPPORTED;
+  // Single token, F32, every pair Q4_K with the transposed down: the decode
+  // kernel, with ceil(tasks/256) tasks per workgroup spread over the fewest
+  // workgroups that keeps that count.
+  bool decode = T == 1 && r->mode == MODE_F32 && np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
+  for (uint32_t i = 0; decode && i < np; ++i) decode = pairs[i].gu == TQ4_K && pairs[i].dn == TQ4_KT;
+  if (decode && !env_int("FRONK_HIP_NO_DECODE", 0)) {
+    // One workgroup per CU at most (each uses most of a CU's LDS).
+    const uint32_t cap = E.cus < (unsigned)kDecodeGridMax ? E.cus : (unsigned)kDecodeGridMax;
+    // Equal task counts per workgroup where possible: the fewest workgroups
+    // that keep ceil(tasks / cap) tasks each, so none runs an extra round.
+    const uint32_t ntask = 4 * np, tpw = (ntask + cap - 1) / cap;
+    H->kind = KIND_DECODE;
+    H->tpw = tpw;
+    H->grid = (ntask + tpw - 1) / tpw;
+  } else {
+    H->kind = KIND_LAYER;
+    H->tpw = 0;
+    H->grid = H->ntA + H->ntB;
+  }
   *used = H->total;
-  *grid = H->ntA + H->ntB;
+  *grid = H->grid;
   E.sample.unique_experts = (unsigned)nu;
   E.sample.pairs = np;
   E.sample.grid = *grid;
@@ -1697,17 +2099,24 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
 
 int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream) {
   if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
+  if (H.kind == KIND_DECODE && (grid > (unsigned)kDecodeGridMax || H.burst != 1)) return FR_HIP_INVALID;
   Scratch S;
   S.done = E.done;
   S.fin = E.fin;
   S.hbuf = E.hbuf;
   S.partial = E.partial;
   S.out = E.out;
+  S.wgpart = E.wgpart;
+  S.bar = E.bar;
   S.out_words = E.out_words;
   S.parity = E.parity;
   const dim3 g(grid), blk(kThreads);
   const bool one = H.burst == 1;
-  switch (H.mode) {
+  if (H.kind == KIND_DECODE) {
+    hipLaunchKernelGGL(decode_kernel, g, dim3(kDecodeThreads), 0, stream, dev_plan, S);
+    hipLaunchKernelGGL(decode_reduce, dim3(kMaxHidden / kReducePositions), dim3(kReduceThreads), 0, stream, dev_plan,
+                       S, grid);
+  } else switch (H.mode) {
     case MODE_F32:
       if (one) hipLaunchKernelGGL((layer_kernel<MODE_F32, 1>), g, blk, H.lds, stream, dev_plan, S);
       else hipLaunchKernelGGL((layer_kernel<MODE_F32, 8>), g, blk, H.lds, stream, dev_plan, S);
@@ -1767,6 +2176,9 @@ int fr_hip_open(int device) {
   CK(hipSetDevice(device));
   E = Engine();
   E.device = device;
+  int cus = 0;
+  CK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  E.cus = cus > 0 ? (unsigned)cus : 1u;
   CK(hipStreamCreateWithFlags(&E.stream, hipStreamNonBlocking));
   CK(hipMalloc(&E.done, 2 * kMaxPairs * sizeof(uint32_t)));
   CK(hipMalloc(&E.fin, 2 * kMaxRanges * sizeof(uint32_t)));
@@ -1776,6 +2188,9 @@ int fr_hip_open(int device) {
   CK(hipMalloc(&E.partial, E.partial_bytes));
   E.out_words = 4 + kMaxBurst * kMaxHidden;
   CK(hipMalloc(&E.out, 2 * (size_t)E.out_words * sizeof(uint32_t)));
+  CK(hipMalloc(&E.wgpart, (size_t)kDecodeGridMax * kMaxHidden * sizeof(float)));
+  CK(hipMalloc(&E.bar, 2 * sizeof(uint32_t)));
+  CK(hipMemset(E.bar, 0, 2 * sizeof(uint32_t)));
   CK(hipMemset(E.done, 0, 2 * kMaxPairs * sizeof(uint32_t)));
   CK(hipMemset(E.fin, 0, 2 * kMaxRanges * sizeof(uint32_t)));
   CK(hipMemset(E.out, 0, 2 * (size_t)E.out_words * sizeof(uint32_t)));
@@ -1801,6 +2216,8 @@ int fr_hip_close(void) {
   (void)hipFree(E.hbuf);
   (void)hipFree(E.partial);
   (void)hipFree(E.out);
+  (void)hipFree(E.wgpart);
+  (void)hipFree(E.bar);
   (void)hipFree(E.plan_dev);
   (void)hipFree(E.staging);
   (void)hipHostFree(E.plan_host);
@@ -1956,7 +2373,8 @@ int fr_hip_launch(const void* host_plan, const void* device_plan, void* stream) 
   if (!host_plan || !device_plan) return FR_HIP_INVALID;
   const PlanHeader& H = *static_cast<const PlanHeader*>(host_plan);
   if (!H.burst || H.burst > (unsigned)kMaxBurst || !H.ntA || !H.ntB) return FR_HIP_INVALID;
-  return launch(static_cast<const uint8_t*>(device_plan), H, H.ntA + H.ntB,
+  if (H.kind == KIND_LAYER ? H.grid != H.ntA + H.ntB : (H.kind != KIND_DECODE || !H.grid)) return FR_HIP_INVALID;
+  return launch(static_cast<const uint8_t*>(device_plan), H, H.grid,
                 stream ? static_cast<hipStream_t>(stream) : E.stream);
 }
 

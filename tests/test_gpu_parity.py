@@ -36,6 +36,10 @@ def check_close(ref, got, mode, what=""):
 
 
 def run_both(eng, blocks, fmt, layer, experts, gates, x, mode):
+    # Name the case before the launch so that a failure that ends the process
+    # still says which one it was.
+    print(f"case fmt={fmt} layer={layer} burst={x.shape[0]} hidden={x.shape[1]} mode={mode} "
+          f"experts={np.asarray(experts).ravel()[:4].tolist()}...", flush=True)
     rc, y = eng.run(layer, experts, gates, x, mode)
     assert rc == fa.OK, (rc, mode)
     req = oracle_request(layer, experts, gates, x)

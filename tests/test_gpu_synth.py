@@ -101,3 +101,52 @@ def test_layer_share_on_synthetic_blocks(eng, fmt):
     finally:
         for b in range(20):
             eng.release(b)
+
+
+def plan_kind(eng, layer, experts, gates, x):
+    plan, grid = eng.plan(layer, experts, gates, x, fa.MODE_F32)
+    return int(np.frombuffer(plan[64:68].tobytes(), np.uint32)[0]), grid
+
+
+@pytest.mark.parametrize("hidden", [4096, 2560])
+def test_decode_kernel_and_layer_kernel_agree_with_oracle(eng, hidden, monkeypatch):
+    """Single-token all-Q4_K requests run on the decode kernel (tasks of 8
+    neurons, no h exchange); the same request forced onto the two-phase
+    layer kernel must match the oracle as well."""
+    lay = oracle.layout(hidden, fa.FMT_Q4KT)
+    seed = 4242 + hidden
+    rng = np.random.default_rng(hidden)
+    for b in range(20):
+        assert eng.synthetic(b, hidden, fa.FMT_Q4KT, 1, seed) == fa.OK
+    try:
+        experts = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+        units = []
+        for b in range(20):
+            u = sparse_unit(lay)
+            for e in experts.ravel():
+                slice_view(u, lay, 0, int(e))[:] = oracle.synth_slice(lay, seed, b, 0, int(e))
+            units.append(u)
+        gates = np.zeros((1, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, 1)
+        x = rng.standard_normal((1, hidden)).astype(np.float32)
+        req = oracle_request(0, experts, gates, x)
+        rc, ref = oracle.ref_run(units, fa.FMT_Q4KT, False, req)
+        assert rc == 0
+        kind, grid = plan_kind(eng, 0, experts, gates, x)
+        assert kind == 1 and 0 < grid <= 256, (kind, grid)
+        print(f"decode kernel hidden={hidden} grid={grid}", flush=True)
+        rc, y_dec = eng.run(0, experts, gates, x, fa.MODE_F32)
+        assert rc == fa.OK
+        check_close(ref, y_dec, fa.MODE_F32, ("decode", hidden))
+        rc, again = eng.run(0, experts, gates, x, fa.MODE_F32)
+        assert np.array_equal(y_dec.view(np.uint32), again.view(np.uint32))
+        monkeypatch.setenv("FRONK_HIP_NO_DECODE", "1")
+        kind, grid = plan_kind(eng, 0, experts, gates, x)
+        assert kind == 0
+        print(f"layer kernel hidden={hidden} grid={grid}", flush=True)
+        rc, y_lay = eng.run(0, experts, gates, x, fa.MODE_F32)
+        assert rc == fa.OK
+        check_close(ref, y_lay, fa.MODE_F32, ("layer", hidden))
+    finally:
+        for b in range(20):
+            eng.release(b)
