@@ -107,6 +107,12 @@ def slice_sizes(fa, fmt):
     return routed, shared
 
 
+def grid_kernels(lib, plan):
+    """The kernels one launch of this plan runs (plan header field `kind`)."""
+    kind = int(np.frombuffer(plan[64:68].tobytes(), np.uint32)[0])
+    return "decode_kernel + decode_reduce" if kind == 1 else "layer_kernel"
+
+
 def copy_kernel(nbytes):
     import torch
     a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
@@ -244,7 +250,22 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     weight_gbs = wts[timed].sum() / wall / 1e9
     alg_per_launch = float(alg[timed].mean())
+
+    # Roofline: algorithmic bytes over the launch's own time, from the HIP
+    # events around the timed region on the launch stream. A single-token
+    # Q4_K launch is decode_kernel followed by decode_reduce (its fixed-order
+    # partial sum); their rocprofv3 averages add up to this figure. The split
+    # between them comes from a second pass with events between the kernels
+    # (the extra markers add a little to each).
     achieved = alg_per_launch / (kernel_ms * 1e-3) / 1e9
+    nt = min(args.steps, 500)
+    fa.check(lib.fr_hip_timing(nt), "fr_hip_timing")
+    for i in range(args.warmup, args.warmup + nt):
+        enqueue(i)
+    main_ms, total_ms, counted = C.c_double(), C.c_double(), C.c_uint()
+    fa.check(lib.fr_hip_timing_read(C.byref(main_ms), C.byref(total_ms), C.byref(counted)), "fr_hip_timing_read")
+    main_us = main_ms.value * 1e3 / counted.value
+    launch_us = total_ms.value * 1e3 / counted.value
 
     # run() wall time: plan build, H2D, launch, D2H and narrowing per call.
     run_us = []
@@ -257,7 +278,7 @@ def main():
     run_us = np.array(run_us)
 
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"layer_kernel_{args.workload}_traffic.json")
+    tfile = os.path.join(ROOT, "profiles", f"decode_{args.workload}_traffic.json")
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
 
@@ -288,13 +309,16 @@ def main():
         "hbm_frac": round(weight_gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(burst * args.steps / wall, 1),
         "kernel_us": round(kernel_ms * 1e3, 3),
+        "kernel_split_us": {"main": round(main_us, 3), "rest": round(launch_us - main_us, 3),
+                            "note": "events between the kernels of each launch, second pass"},
         "weight_bytes_per_call": float(wts[timed].mean()),
         "grid": grid,
         "run_wall_us": {"p50": round(float(np.percentile(run_us, 50)), 2),
                         "p99": round(float(np.percentile(run_us, 99)), 2)},
         "run_wall_gbs": round(float(wts[:args.run_calls].mean() / (np.median(run_us) * 1e-6) / 1e9), 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": grid_kernels(lib, host[args.warmup])},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

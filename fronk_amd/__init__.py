@@ -50,6 +50,8 @@ SIGNATURES = {
     "fr_hip_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "fr_hip_last_output": (C.c_int, [C.c_void_p, C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_uint)]),
     "fr_hip_sample_get": (C.c_int, [C.POINTER(Sample)]),
+    "fr_hip_timing": (C.c_int, [C.c_uint]),
+    "fr_hip_timing_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_uint)]),
     "fr_hip_debug_dequant": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_dequant_down": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_quantize": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.POINTER(C.c_float)]),

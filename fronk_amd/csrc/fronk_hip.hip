@@ -1949,6 +1949,11 @@ struct Engine {
   uint32_t last_parity = 0;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   fr_hip_sample sample = {};
+  // Launch timing (fr_hip_timing): events before, between and after the
+  // kernels of each launch, for the first `timed_cap` launches.
+  hipEvent_t* tev = nullptr;
+  unsigned timed_cap = 0, timed = 0;
+  bool timing = false;
 };
 Engine E;
 bool g_open = false;
@@ -2112,8 +2117,11 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
   S.parity = E.parity;
   const dim3 g(grid), blk(kThreads);
   const bool one = H.burst == 1;
+  hipEvent_t* te = E.timing && E.timed < E.timed_cap ? E.tev + 3 * E.timed++ : nullptr;
+  if (te && hipEventRecord(te[0], stream) != hipSuccess) return FR_HIP_IO;
   if (H.kind == KIND_DECODE) {
     hipLaunchKernelGGL(decode_kernel, g, dim3(kDecodeThreads), 0, stream, dev_plan, S);
+    if (te && hipEventRecord(te[1], stream) != hipSuccess) return FR_HIP_IO;
     hipLaunchKernelGGL(decode_reduce, dim3(kMaxHidden / kReducePositions), dim3(kReduceThreads), 0, stream, dev_plan,
                        S, grid);
   } else switch (H.mode) {
@@ -2129,6 +2137,10 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
       if (one) hipLaunchKernelGGL((layer_kernel<MODE_Q8, 1>), g, blk, H.lds, stream, dev_plan, S);
       else hipLaunchKernelGGL((layer_kernel<MODE_Q8, 8>), g, blk, H.lds, stream, dev_plan, S);
       break;
+  }
+  if (te) {
+    if (H.kind != KIND_DECODE && hipEventRecord(te[1], stream) != hipSuccess) return FR_HIP_IO;
+    if (hipEventRecord(te[2], stream) != hipSuccess) return FR_HIP_IO;
   }
   if (hipGetLastError() != hipSuccess) return FR_HIP_IO;
   E.last_parity = E.parity;
@@ -2224,6 +2236,8 @@ int fr_hip_close(void) {
   (void)hipHostFree(E.out_host);
   (void)hipEventDestroy(E.ev0);
   (void)hipEventDestroy(E.ev1);
+  for (unsigned i = 0; i < 3 * E.timed_cap; ++i) (void)hipEventDestroy(E.tev[i]);
+  free(E.tev);
   (void)hipStreamDestroy(E.stream);
   E = Engine();
   g_open = false;
@@ -2409,6 +2423,40 @@ int fr_hip_run(const fr_hip_request* req, float* y) {
   if (status) return FR_HIP_NUMERIC;
   // y is written only on success: untouched on failure.
   memcpy(y, E.out_host + 4, count * sizeof(float));
+  return FR_HIP_OK;
+}
+
+int fr_hip_timing(unsigned launches) {
+  if (!g_open) return FR_HIP_STATE;
+  CK(hipSetDevice(E.device));
+  if (launches > E.timed_cap) {
+    for (unsigned i = 0; i < 3 * E.timed_cap; ++i) (void)hipEventDestroy(E.tev[i]);
+    free(E.tev);
+    E.tev = static_cast<hipEvent_t*>(calloc(3 * (size_t)launches, sizeof(hipEvent_t)));
+    E.timed_cap = 0;
+    if (!E.tev) return FR_HIP_IO;
+    for (unsigned i = 0; i < 3 * launches; ++i) CK(hipEventCreate(&E.tev[i]));
+    E.timed_cap = launches;
+  }
+  E.timed = 0;
+  E.timing = launches > 0;
+  return FR_HIP_OK;
+}
+
+int fr_hip_timing_read(double* main_ms, double* total_ms, unsigned* launches) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!main_ms || !total_ms || !launches) return FR_HIP_INVALID;
+  *main_ms = *total_ms = 0.0;
+  for (unsigned i = 0; i < E.timed; ++i) {
+    float a = 0.f, b = 0.f;
+    CK(hipEventSynchronize(E.tev[3 * i + 2]));
+    CK(hipEventElapsedTime(&a, E.tev[3 * i], E.tev[3 * i + 1]));
+    CK(hipEventElapsedTime(&b, E.tev[3 * i], E.tev[3 * i + 2]));
+    *main_ms += a;
+    *total_ms += b;
+  }
+  *launches = E.timed;
+  E.timing = false;
   return FR_HIP_OK;
 }
 

@@ -111,6 +111,16 @@ int fr_hip_last_output(void *stream, float *y, size_t count, unsigned *status);
 
 int fr_hip_sample_get(fr_hip_sample *out);
 
+/* Launch timing for measurement (no reference counterpart): after
+ * fr_hip_timing(n), the next n launches record HIP events on their stream
+ * before the main kernel, after it and after the launch's last kernel (a
+ * single-token all-Q4_K launch is the decode kernel followed by its
+ * fixed-order partial reduction). fr_hip_timing_read waits for them and
+ * returns the summed main-kernel and whole-launch times in ms, then stops
+ * timing. fr_hip_timing(0) stops without reading. */
+int fr_hip_timing(unsigned launches);
+int fr_hip_timing_read(double *main_ms, double *total_ms, unsigned *launches);
+
 /* Parity hooks (no reference counterpart): the hot path's own device
  * decoder and quantizer on caller data, for bit-exact checks against the
  * reference's fr_native_dot decode (src/native.c:13-31) and fr_q8_activation

@@ -1,0 +1,24 @@
+"""The reference's own conformance harness against the "hip" backend on the
+GPU: self_test runs fr_vectors_check over the committed golden corpus
+(src/vectors.c:136-174, backend tolerance src/backend.c:11-13) and then
+fr_native_self_test (src/native.c:66-135: bursts 1..8 against the
+reference's ref backend, corrupt scales -> FR_NUMERIC with the caller's
+output preserved), both compiled from the reference sources in oracle/_ref.
+"""
+import ctypes as C
+
+import pytest
+
+import vtable as vt
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not vt.available(), reason="oracle/_ref or libfr_hip.so not built")]
+
+
+def test_probe_finds_gfx950():
+    buf = C.create_string_buffer(4096)
+    assert vt.backend().probe(buf) == vt.OK
+
+
+def test_reference_self_test():
+    print("hip self_test: golden corpus, then native self-test", flush=True)
+    assert vt.backend().self_test(vt.GOLDEN.encode()) == vt.OK
