@@ -441,21 +441,26 @@ __device__ __forceinline__ float lane_dot_f32(const LaneRaw& r, const float* sc,
                                               float X0, float X1) {
   float s0 = 0.f, s1 = 0.f;
   if (type == TQ4_K) {
-    // Byte i of the 32-byte chunk: column i (low nibble), 32+i (high).
+    // Byte i of the 32-byte chunk: column i (low nibble), 32+i (high). Eight
+    // independent chains (one per byte position and nibble) so that the
+    // FMAs of a wave do not wait on each other.
+    float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t v = word(r.q[i >> 2], i & 3);
       const uint32_t lo = nib_lo(v), hi = nib_hi(v);
-      const float4 a = x[i], b = x[8 + i];
-      s0 = fmaf(ub(lo, 0), a.x, s0);
-      s0 = fmaf(ub(lo, 1), a.y, s0);
-      s0 = fmaf(ub(lo, 2), a.z, s0);
-      s0 = fmaf(ub(lo, 3), a.w, s0);
-      s1 = fmaf(ub(hi, 0), b.x, s1);
-      s1 = fmaf(ub(hi, 1), b.y, s1);
-      s1 = fmaf(ub(hi, 2), b.z, s1);
-      s1 = fmaf(ub(hi, 3), b.w, s1);
+      const float4 xa = x[i], xb = x[8 + i];
+      a[0] = fmaf(ub(lo, 0), xa.x, a[0]);
+      a[1] = fmaf(ub(lo, 1), xa.y, a[1]);
+      a[2] = fmaf(ub(lo, 2), xa.z, a[2]);
+      a[3] = fmaf(ub(lo, 3), xa.w, a[3]);
+      b[0] = fmaf(ub(hi, 0), xb.x, b[0]);
+      b[1] = fmaf(ub(hi, 1), xb.y, b[1]);
+      b[2] = fmaf(ub(hi, 2), xb.z, b[2]);
+      b[3] = fmaf(ub(hi, 3), xb.w, b[3]);
     }
+    s0 = (a[0] + a[1]) + (a[2] + a[3]);
+    s1 = (b[0] + b[1]) + (b[2] + b[3]);
     return (sc[0] * s0 - mn[0] * X0) + (sc[1] * s1 - mn[1] * X1);
   }
   if (type == TQ4_0) {
@@ -1339,71 +1344,6 @@ __device__ __forceinline__ float silu_mul_f32(float a, float u, uint32_t& bad) {
   return h;
 }
 
-// x of one 32-column group as three signed int8 digits of a 24-bit fixed
-// point value: X_j = rint(x_j * 2^(22 - E)) with 2^E > max|x_j| (so
-// |X_j| <= 2^22), X_j = D0 + 256*D1 + 65536*D2, D0, D1 in [-128, 127],
-// |D2| <= 64. words[d][i] packs digit d of columns 4i..4i+3. Returns
-// 2^(E - 22), the value of one unit. The rounding error of each x_j is at
-// most 2^-23 of the group's largest |x|.
-__device__ __forceinline__ float x_digits(const float4* x4, uint32_t (&words)[3][8]) {
-  float m = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) m = fmaxf(m, fmaxf(fmaxf(fabsf(x4[i].x), fabsf(x4[i].y)), fmaxf(fabsf(x4[i].z), fabsf(x4[i].w))));
-  int e = 0;
-  if (m > 0.f) (void)frexpf(m, &e);   // m = f * 2^e, f in [0.5, 1)
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float c[4] = {x4[i].x, x4[i].y, x4[i].z, x4[i].w};
-    uint32_t w0 = 0, w1 = 0, w2 = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int X = __float2int_rn(ldexpf(c[b], 22 - e));
-      const int d0 = (int)(int8_t)(X & 0xff);
-      const int x1 = (X - d0) >> 8;
-      const int d1 = (int)(int8_t)(x1 & 0xff);
-      const int d2 = (x1 - d1) >> 8;
-      w0 |= (uint32_t)(d0 & 0xff) << (8 * b);
-      w1 |= (uint32_t)(d1 & 0xff) << (8 * b);
-      w2 |= (uint32_t)(d2 & 0xff) << (8 * b);
-    }
-    words[0][i] = w0;
-    words[1][i] = w1;
-    words[2][i] = w2;
-  }
-  return ldexpf(1.f, e - 22);
-}
-
-// Lane partial of a Q4_K row in integer arithmetic: per 32-column group,
-// sum_j q_j * X_j from three v_dot4_i32_i8 chains (one per digit), combined
-// exactly in 32 bits (|sum| < 2^31), then scaled: d*sc*unit*S - dmin*mi*X.
-__device__ __forceinline__ float lane_dot_q4k_i8(const LaneRaw& r, const float sc[2], const float mn[2],
-                                                 const uint32_t (&xa)[3][8], const uint32_t (&xb)[3][8], float ua,
-                                                 float ub_, float X0, float X1) {
-  int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    // Byte k of dword i: column 4i+k (low nibble, group A), 32+4i+k (high, group B).
-    const uint32_t v = word(r.q[i >> 2], i & 3);
-    const int lo = (int)nib_lo(v), hi = (int)nib_hi(v);
-    a0 = __builtin_amdgcn_sdot4(lo, (int)xa[0][i], a0, false);
-    a1 = __builtin_amdgcn_sdot4(lo, (int)xa[1][i], a1, false);
-    a2 = __builtin_amdgcn_sdot4(lo, (int)xa[2][i], a2, false);
-    b0 = __builtin_amdgcn_sdot4(hi, (int)xb[0][i], b0, false);
-    b1 = __builtin_amdgcn_sdot4(hi, (int)xb[1][i], b1, false);
-    b2 = __builtin_amdgcn_sdot4(hi, (int)xb[2][i], b2, false);
-  }
-  const int sa = (int)((uint32_t)a0 + ((uint32_t)a1 << 8) + ((uint32_t)a2 << 16));
-  const int sb = (int)((uint32_t)b0 + ((uint32_t)b1 << 8) + ((uint32_t)b2 << 16));
-  return (sc[0] * ((float)sa * ua) - mn[0] * X0) + (sc[1] * ((float)sb * ub_) - mn[1] * X1);
-}
-
-// Device-coherent 16-byte store: written through to memory so that a
-// workgroup on another XCD reads it after the writer has drained.
-__device__ __forceinline__ void store16_coherent(float* p, float4 v) {
-  const u32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(w) : "memory");
-}
-
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
   uint32_t* status = S.out + (size_t)S.parity * S.out_words;
@@ -1428,15 +1368,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
     X0 += (x[i].x + x[i].y) + (x[i].z + x[i].w);
     X1 += (x[8 + i].x + x[8 + i].y) + (x[8 + i].z + x[8 + i].w);
   }
-  // x as int8 digits per 32-column group (A: columns 0..31 of the lane's
-  // chunk, B: 32..63). Computing them waits for the x loads here, before
-  // the first copy is issued, not inside the loop.
-  uint32_t xa[3][8], xb[3][8];
-  const float ua = x_digits(x, xa), ubs = x_digits(x + 8, xb);
+  // x stays in registers for the whole kernel; the pins keep the compiler
+  // from re-reading it inside the task loop.
 #pragma unroll
-  for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(xa[0][i]), "+v"(xa[1][i]), "+v"(xa[2][i]));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(xb[0][i]), "+v"(xb[1][i]), "+v"(xb[2][i]));
+  for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(x[i].x), "+v"(x[i].y), "+v"(x[i].z), "+v"(x[i].w));
   asm volatile("" : "+v"(X0), "+v"(X1));
   float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   uint32_t bad = 0;
@@ -1461,7 +1396,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
       float sc[2], mn[2];
       const bool ok = raw_scales<TQ4_K>(rr, c, sc, mn);
       if (active && !ok) bad |= kErrScale;
-      const float part = lane_dot_q4k_i8(rr, sc, mn, xa, xb, ua, ubs, X0, X1);
+      const float part = lane_dot_f32<TQ4_K>(rr, sc, mn, x, X0, X1);
       au[r] = wave_total(active ? part : 0.f);
     }
     const float h = silu_mul_f32(au[0], au[1], bad);
