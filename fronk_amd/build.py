@@ -34,7 +34,7 @@ def build_hip(verbose=False):
 
 def build_vtable(verbose=False):
     cmd = ["gcc", "-std=c11", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-Werror",
-           "-D_POSIX_C_SOURCE=200809L", "-D_DEFAULT_SOURCE", "-DFR_BENCH_RUNTIME=1", "-I" + REFERENCE_SRC, "-I" + os.path.join(ROOT, "include"),
+           "-D_POSIX_C_SOURCE=200809L", "-D_DEFAULT_SOURCE", "-DFR_BENCH_RUNTIME=1", "-DFR_HIP_MODULE=1", "-I" + REFERENCE_SRC, "-I" + os.path.join(ROOT, "include"),
            VTABLE_SRC, "-o", VTABLE_LIB + ".tmp", "-L" + HERE, "-lfronk_hip", "-Wl,-rpath,$ORIGIN", "-lm"]
     subprocess.run(cmd, check=True, capture_output=not verbose)
     os.replace(VTABLE_LIB + ".tmp", VTABLE_LIB)

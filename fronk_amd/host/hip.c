@@ -21,6 +21,7 @@
  *   bench   fr_bench_execute_backend (backends/user-template.c:93).
  *   self_test  FR_STATE when a block is loaded; the golden corpus, then the
  *           native self-test (backends/avx2.c:773-777).
+ *   fr_hip_backend_close  the bench's close hook (src/bench.c:265-278).
  * During self_test, load only reserves device memory and run copies the
  * slices a request references from the borrowed bytes first: the corpus
  * fixtures are sparse multi-GB units, and the native self-test corrupts the
@@ -37,8 +38,7 @@
 #include <string.h>
 
 #include "fronk_hip.h"
-
-extern const fr_backend fr_hip;
+#include "hip.h"
 
 static const unsigned char *unit[FR_BLOCKS];   /* borrowed until unload */
 static int opened;
@@ -156,3 +156,20 @@ static int self_test(const char *dir) {
 }
 
 const fr_backend fr_hip = {"hip", probe, load, unload, run, bench, self_test};
+
+/* The bench's backend_close hook (src/bench.c:265-278), like fr_avx2_close
+ * (backends/avx2.c:718): FR_STATE while a block is loaded, otherwise release
+ * the device so that the next load opens it afresh. */
+int fr_hip_backend_close(void) {
+    if (loaded()) return FR_STATE;
+    if (!opened) return FR_OK;
+    int rc = fr_hip_close();
+    if (!rc) opened = 0;
+    return rc;
+}
+
+#ifdef FR_HIP_MODULE
+/* Module form (tools/backend-module.py): the table under the name the module
+ * registry expects (src/backend.c:56-58). */
+const fr_backend fr_module_hip = {"hip", probe, load, unload, run, bench, self_test};
+#endif

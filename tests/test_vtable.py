@@ -21,6 +21,20 @@ def test_name_and_table():
     assert b.name == b"hip"
     for f in ("probe", "load", "unload", "run", "bench", "self_test"):
         assert getattr(b, f)
+    # The module form's table (src/backend.c:56-58) is the same backend.
+    m = vt.Backend.in_dll(vt.library(), "fr_module_hip")
+    assert m.name == b"hip"
+    for f in ("probe", "load", "unload", "run", "bench", "self_test"):
+        assert C.cast(getattr(m, f), C.c_void_p).value == C.cast(getattr(b, f), C.c_void_p).value
+
+
+def test_backend_close_without_blocks():
+    """The bench's close hook (src/bench.c:265-278) succeeds, and is
+    repeatable, when no block is loaded."""
+    close = vt.library().fr_hip_backend_close
+    close.restype = C.c_int
+    assert close() == vt.OK
+    assert close() == vt.OK
 
 
 def test_probe():

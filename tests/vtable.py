@@ -40,18 +40,26 @@ class Backend(C.Structure):       # fr_backend (src/backend.h:52-67)
 
 
 _vt = None
+_lib = None
 
 
 def available():
     return os.path.exists(REF_LIB) and os.path.exists(VTABLE_LIB)
 
 
+def library():
+    """libfr_hip.so; the reference library is loaded first, globally, so that
+    the vtable's reference symbols resolve."""
+    global _lib
+    if _lib is None:
+        C.CDLL(REF_LIB, mode=C.RTLD_GLOBAL)
+        _lib = C.CDLL(VTABLE_LIB, mode=C.RTLD_GLOBAL)
+    return _lib
+
+
 def backend():
-    """The fr_hip vtable; the reference library is loaded first, globally, so
-    that the vtable's reference symbols resolve."""
+    """The fr_hip vtable."""
     global _vt
     if _vt is None:
-        C.CDLL(REF_LIB, mode=C.RTLD_GLOBAL)
-        lib = C.CDLL(VTABLE_LIB, mode=C.RTLD_GLOBAL)
-        _vt = Backend.in_dll(lib, "fr_hip")
+        _vt = Backend.in_dll(library(), "fr_hip")
     return _vt
