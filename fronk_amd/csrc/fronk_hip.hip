@@ -81,7 +81,7 @@ struct PlanHeader {
   uint32_t ngroups, nranges, ntA, ntB;
   uint32_t nn, tchunk, pairs_off, groups_off;
   uint32_t x_off, total, gmax, lds;
-  uint32_t kind, grid, tpw, pad;   // kernel (KIND_*), its grid, decode tasks per workgroup
+  uint32_t kind, grid, tpw, pad;   // kernel (KIND_*), its grid, decode pairs per workgroup
 };
 static_assert(sizeof(PlanHeader) == 80, "header layout");
 
@@ -128,16 +128,16 @@ __device__ __forceinline__ float2 fp4_pair(uint32_t v, float scale, int b) {
 
 // Q4_K 6-bit scale/min of group g from the 12 packed bytes s0|s1|s2
 // (src/native.c:14-19).
+// Both cases are computed and one is selected, so that lanes holding
+// different groups do not diverge.
 __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t g,
                                               uint32_t& sc, uint32_t& mi) {
-  if (g < 4) {
-    sc = (s0 >> (8 * g)) & 63u;
-    mi = (s1 >> (8 * g)) & 63u;
-  } else {
-    uint32_t k = 8 * (g - 4);
-    sc = ((s2 >> k) & 15u) | (((s0 >> k) >> 6 & 3u) << 4);
-    mi = ((s2 >> k) >> 4 & 15u) | (((s1 >> k) >> 6 & 3u) << 4);
-  }
+  const uint32_t k = 8 * (g & 3u);
+  const uint32_t a0 = s0 >> k, a1 = s1 >> k, a2 = s2 >> k;
+  const uint32_t sc_hi = (a2 & 15u) | ((a0 >> 2) & 48u);         // low 4 bits | top 2 bits of byte g-4
+  const uint32_t mi_hi = ((a2 >> 4) & 15u) | ((a1 >> 2) & 48u);
+  sc = g < 4 ? a0 & 63u : sc_hi;
+  mi = g < 4 ? a1 & 63u : mi_hi;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -1250,92 +1250,84 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(const uint8_t* __restri
 // ------------------------------------------------------------ decode kernel
 //
 // Single token, every pair routed Q4_K with the transposed Q4_K down (the
-// down rows are per neuron). Because the down of neuron n needs only h_n, a
-// task (pair, 8 neurons) carries its own gate/up rows, h and down rows: no
-// h crosses workgroups. Workgroup w of G (at most one per CU) runs tasks w,
-// w+G, w+2G, ... in order, so the result does not depend on timing. Per task, wavefront i streams the gate
-// and up rows of neuron i (lane c: columns 64c..64c+63), a DPP tree gives a
-// and u, h = SiLU(a)*u (backends/ref.c:82-83, in fp32: this kernel serves the
-// F32 mode only). For the down, wavefront i owns super-blocks 2i and 2i+1
-// for the whole kernel: lane l accumulates the 8 columns 8(l%32)..8(l%32)+7
-// of super-block 2i + l/32 over the task's 8 neurons in registers. After the
-// last task each workgroup stores its fp32 partial with plain stores, and a
-// second small kernel on the same stream, decode_reduce, sums the G partials
-// in a fixed order: the kernel boundary is the global barrier and makes the
+// down rows are per neuron): one workgroup of 8 wavefronts per (expert,
+// block) pair (pairs b, b+G, ...), so that no h crosses workgroups. A pair is
+// processed in 4 rounds of 8 neurons. In round t, wavefront w computes gate
+// and up of neuron 8(t%4) + w in fp32 (this kernel serves the F32 mode only),
+// h = SiLU(a)*u in fp32 (backends/ref.c:82-83), and publishes gate*h in LDS
+// with a counter; it then applies the down projection of round t-1's 8
+// neurons, whose h the other wavefronts published a round earlier, to
+// super-blocks 2w and 2w+1 (outputs 512w..512w+511), accumulating an fp32
+// partial over all outputs in registers. No barrier separates the rounds:
+// a wavefront waits only for a counter, which is normally complete. A second
+// small kernel on the same stream, decode_reduce, sums the workgroup partials
+// in workgroup order: the kernel boundary is the global barrier and makes the
 // partials visible across XCDs, which in-kernel coherent stores, counters and
 // polling would do at about 2 us per hop.
+//
+// Every lane loads exactly the bytes it uses into registers, with the
+// non-temporal policy, one round ahead of the round that uses them; the
+// rounds of a pair are unrolled, so each round's bytes have registers of
+// their own and the compiler's waits are exact. LDS holds x (read back per
+// neuron), h, the down headers and the down coefficients.
 
-// The next task's bytes are copied by the load units straight into LDS
-// (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16*i), so no
-// registers are tied up by the prefetch. The copies are issued from inline
-// assembly with explicit waits: the compiler, which cannot tell these LDS
-// writes from its own LDS reads, would otherwise wait for every copy in
-// flight before each read. Each wave issues the same number of copies per
-// task on every path, so the waits are exact, and each wave reads back only
-// what it copied except the table headers, which a barrier covers.
-__device__ __forceinline__ void dma16(const void* g, const void* lds) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+// Non-temporal 16-byte load through a global-space pointer: a generic
+// pointer would make it a FLAT load, which also counts in lgkmcnt, so every
+// LDS wait would wait for the weight bytes in flight too.
+__device__ __forceinline__ uint4 ldnt(const uint8_t* p) {
+  const u32x4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-constexpr int kDecodeGuCopies = 7;   // gate/up quants 4, gate/up headers 2, table headers 1
-constexpr int kDecodeDnCopies = 2;   // down nibbles
-
-struct DecodeGu {                     // one task's gate/up bytes and down headers
-  uint4 q[kDecodeWaves][2][2][64];   // [wave][gate, up][part][lane]
-  uint4 h[kDecodeWaves][2][16];      // [wave][gate, up][super-block] row headers
-  uint4 th[128];                     // down headers [super-block * 8 + neuron]
+struct DecodeRound {                   // one lane's bytes of one round
+  uint4 gq[2][2];                      // [gate, up][part]: nibbles of chunk c of neuron 8r + w
+  uint4 gh[2];                         // [gate, up]: header of super-block c/4
+  uint4 dq[2];                         // down nibbles: super-block 2w + l/32, neurons 8r..8r+7,
+                                       // outputs 8j..8j+3 and 8j+4..8j+7 (j = l%32)
+  uint4 dh;                            // down header: super-block 2w + (l%16)/8, neuron 8r + l%8
 };
-struct DecodeDn {
-  uint4 q[kDecodeWaves][2][64];      // [wave][columns 8j..8j+3, 8j+4..8j+7][lane]
+struct DecodeTable {                   // one wavefront's down coefficients of one round
+  float D[2][8][8];                    // [super-block][group][neuron] d*sc*gate*h
+  float M[2][8][8];                    // dmin*mi*gate*h
 };
 struct DecodeLds {
-  DecodeGu gu[2];
-  DecodeDn dn[2];
-  float D[16][8][8];                 // [super-block][group][neuron] d*sc*gate*h
-  float M[16][8][8];                 // dmin*mi*gate*h
-  float h[kDecodeWaves];
+  float4 x[16][64];                    // [k][lane c] = x[64c + 4k .. 64c + 4k + 3]
+  uint4 dh[kDecodeWaves][16];          // [wave][super-block 2w + i/8, neuron 8r + i%8]
+  DecodeTable table[kDecodeWaves];
+  float h[4][8];                       // gate*h of round t's 8 neurons in slot t%4
+  uint32_t published[4];               // h values written to slot s, over all pairs
+  uint32_t consumed[4];                // wavefronts past their reads of slot s, over all pairs
 };
 
-// Gate/up rows of neuron 8*ng + wave (lane c: parts 0 and 1 of chunk c; lanes
-// 0..15: super-block headers, clamped) and table headers 16*wave + lane.
-__device__ __forceinline__ void issue_gu(const PlanHeader& H, const PairDesc* pairs, unsigned task, int wave,
-                                         int lane, DecodeGu& st) {
-  const unsigned ng = task & 3, nch = H.hidden / 64, nsb = H.hidden / 256;
-  const PairDesc* P = pairs + (task >> 2);
-  const uint8_t* slice = reinterpret_cast<const uint8_t*>(P->slice);
-  const uint32_t proj = P->proj, row = proj / kNeurons, n = 8 * ng + (unsigned)wave;
-  const unsigned c = min((unsigned)lane, nch - 1), s16 = min((unsigned)lane & 15, nsb - 1);
+// Round r of pair P for lane (wave, lane): gate and up rows of neuron
+// 8r + w (chunk c and the header of its super-block), the lane's down
+// nibbles and one down header. Super-blocks past the matrix are clamped to
+// its last one.
+__device__ __forceinline__ void load_round(const PairDesc& P, unsigned r, unsigned nch, unsigned nsb, int wave,
+                                           int lane, unsigned c, DecodeRound& R) {
+  const uint8_t* slice = reinterpret_cast<const uint8_t*>(P.slice);
+  const uint32_t proj = P.proj, row = proj / kNeurons, n = 8 * r + (unsigned)wave;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const uint8_t* rp = slice + (r ? proj : 0) + (size_t)n * row;
-    dma16(rp + 16 * c, &st.q[wave][r][0][0]);
-    dma16(rp + 16 * nch + 16 * c, &st.q[wave][r][1][0]);
-    if (lane < 16) dma16(rp + 32 * nch + 16 * s16, &st.h[wave][r][0]);
+  for (int k = 0; k < 2; ++k) {
+    const uint8_t* rp = slice + (k ? proj : 0) + (size_t)n * row;
+    R.gq[k][0] = ldnt(rp + 16 * c);
+    R.gq[k][1] = ldnt(rp + 16 * nch + 16 * c);
+    R.gh[k] = ldnt(rp + 32 * nch + 16 * (c >> 2));
   }
-  const unsigned idx = 16 * (unsigned)wave + ((unsigned)lane & 15);
-  const unsigned tsb = min(idx >> 3, nsb - 1), tn = idx & 7;
-  if (lane < 16)
-    dma16(slice + 2 * (size_t)proj + 4608 * (size_t)tsb + 4096 + 16 * (8 * ng + tn), &st.th[16 * wave]);
-}
-
-// Down nibbles: super-block 2*wave + lane/32 (clamped), chunks 2j, 2j+1.
-__device__ __forceinline__ void issue_dn(const PlanHeader& H, const PairDesc* pairs, unsigned task, int wave,
-                                         int lane, DecodeDn& st) {
-  const unsigned ng = task & 3, nsb = H.hidden / 256;
-  const PairDesc* P = pairs + (task >> 2);
-  const uint8_t* down = reinterpret_cast<const uint8_t*>(P->slice) + 2 * (size_t)P->proj;
+  const uint8_t* down = slice + 2 * (size_t)proj;
   const unsigned sb = min(2 * (unsigned)wave + ((unsigned)lane >> 5), nsb - 1), j = (unsigned)lane & 31;
-  const uint8_t* q = down + 4608 * (size_t)sb + 1024 * ng + 32 * j;
-  dma16(q, &st.q[wave][0][0]);
-  dma16(q + 16, &st.q[wave][1][0]);
+  R.dq[0] = ldnt(down + 4608 * (size_t)sb + 1024 * r + 32 * j);
+  R.dq[1] = ldnt(down + 4608 * (size_t)sb + 1024 * r + 32 * j + 16);
+  const unsigned hs = min(2 * (unsigned)wave + (((unsigned)lane & 15) >> 3), nsb - 1);
+  R.dh = ldnt(down + 4608 * (size_t)hs + 4096 + 16 * (8 * r + ((unsigned)lane & 7)));
 }
 
 // SiLU(a)*u in fp32 with the stable sigmoid form; a, u or h outside fp32
 // is the reference's FR_NUMERIC (backends/ref.c:37-40).
 __device__ __forceinline__ float silu_mul_f32(float a, float u, uint32_t& bad) {
   const float e = __expf(-fabsf(a));
-  const float sig = a >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
+  const float inv = __builtin_amdgcn_rcpf(1.f + e);
+  const float sig = a >= 0.f ? inv : e * inv;
   const float h = a * sig * u;
   if (!isfinite(a) || !isfinite(u) || !isfinite(h)) {
     bad |= kErrRange;
@@ -1344,120 +1336,224 @@ __device__ __forceinline__ float silu_mul_f32(float a, float u, uint32_t& bad) {
   return h;
 }
 
+// h of the round's neuron from its gate and up rows. The gate and up dots
+// share each x value (read from LDS in two halves of 8 float4, so that only
+// half of the lane's x is in registers at once) and run as 16 independent
+// FMA chains; the two sums are reduced side by side.
+__device__ __forceinline__ float neuron_h(const DecodeRound& R, int c, bool active, const float4 (&xl)[16][64],
+                                          float X0, float X1, uint32_t& bad) {
+  LaneRaw rg, ru;
+  rg.q[0] = R.gq[0][0];
+  rg.q[1] = R.gq[0][1];
+  rg.h = R.gh[0];
+  ru.q[0] = R.gq[1][0];
+  ru.q[1] = R.gq[1][1];
+  ru.h = R.gh[1];
+  float gs[2], gm[2], us[2], um[2];
+  const bool ok = raw_scales<TQ4_K>(rg, c, gs, gm) & raw_scales<TQ4_K>(ru, c, us, um);
+  if (active && !ok) bad |= kErrScale;
+  // Byte i of the 32-byte chunk: column i (low nibble, group A), 32+i (high, group B).
+  float ga[4] = {0.f, 0.f, 0.f, 0.f}, gb[4] = {0.f, 0.f, 0.f, 0.f};
+  float ua[4] = {0.f, 0.f, 0.f, 0.f}, ub_[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int hlf = 0; hlf < 2; ++hlf) {
+    float4 xa[4], xb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xa[i] = xl[4 * hlf + i][c];
+      xb[i] = xl[8 + 4 * hlf + i][c];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int wi = 4 * hlf + i;
+      const uint32_t vg = word(rg.q[wi >> 2], wi & 3), vu = word(ru.q[wi >> 2], wi & 3);
+      const uint32_t glo = nib_lo(vg), ghi = nib_hi(vg), ulo = nib_lo(vu), uhi = nib_hi(vu);
+      const float xav[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w};
+      const float xbv[4] = {xb[i].x, xb[i].y, xb[i].z, xb[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        ga[k] = fmaf(ub(glo, k), xav[k], ga[k]);
+        gb[k] = fmaf(ub(ghi, k), xbv[k], gb[k]);
+        ua[k] = fmaf(ub(ulo, k), xav[k], ua[k]);
+        ub_[k] = fmaf(ub(uhi, k), xbv[k], ub_[k]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const float g0 = (ga[0] + ga[1]) + (ga[2] + ga[3]), g1 = (gb[0] + gb[1]) + (gb[2] + gb[3]);
+  const float u0 = (ua[0] + ua[1]) + (ua[2] + ua[3]), u1 = (ub_[0] + ub_[1]) + (ub_[2] + ub_[3]);
+  float a = (gs[0] * g0 - gm[0] * X0) + (gs[1] * g1 - gm[1] * X1);
+  float u = (us[0] * u0 - um[0] * X0) + (us[1] * u1 - um[1] * X1);
+  a = row_sum(active ? a : 0.f);
+  u = row_sum(active ? u : 0.f);
+  a = (readlane_f(a, 0) + readlane_f(a, 16)) + (readlane_f(a, 32) + readlane_f(a, 48));
+  u = (readlane_f(u, 0) + readlane_f(u, 16)) + (readlane_f(u, 32) + readlane_f(u, 48));
+  return silu_mul_f32(a, u, bad);
+}
+
+// Bounded wait (wave-uniform) until LDS counter *p reaches `target`; a wait
+// past the bound sets the timeout bit and returns, so every wave exits.
+__device__ __forceinline__ void lds_wait(const uint32_t* p, uint32_t target, uint32_t& bad) {
+  uint32_t spins = 0;
+  while (__hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+    if (++spins > kSpinLimit) {
+      bad |= kErrTimeout;
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Publish gate*h of round t (pair iteration k) in slot t%4.
+__device__ __forceinline__ void publish_round(float gh, unsigned t, unsigned k, int wave, int lane, DecodeLds& L,
+                                              uint32_t& bad) {
+  const unsigned s = t & 3;
+  // The slot's previous use (pair iteration k-1) is read by every wavefront.
+  if (k) lds_wait(&L.consumed[s], kDecodeWaves * k, bad);
+  if (lane == 0) {
+    L.h[s][wave] = gh;
+    __hip_atomic_fetch_add(&L.published[s], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
+
+// Down projection of round t (pair iteration k) from the round's down bytes
+// and the 8 published h: coefficients, then 8 outputs per lane.
+__device__ __forceinline__ void down_round(const DecodeRound& R, unsigned t, unsigned k, int wave, int lane,
+                                           unsigned nsb, DecodeLds& L, float (&y)[8], uint32_t& bad) {
+  const unsigned s = t & 3;
+  lds_wait(&L.published[s], kDecodeWaves * (k + 1), bad);
+  const float* hs = L.h[s];
+  if (lane < 16) L.dh[wave][lane] = R.dh;
+  DecodeTable& T = L.table[wave];
+  {
+    // Lane (s, group, neurons 2q, 2q+1) of this wavefront's two super-blocks.
+    const unsigned ts = (unsigned)lane >> 5, tg = ((unsigned)lane >> 2) & 7, n0 = 2 * ((unsigned)lane & 3);
+    const bool tvalid = 2 * (unsigned)wave + ts < nsb;
+    float Dv[2], Mv[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint4 hdr = L.dh[wave][8 * ts + n0 + q];
+      bool ok;
+      hdr_dm(hdr, tg, Dv[q], Mv[q], ok);
+      if (tvalid && !ok) bad |= kErrScale;
+      const float gh = hs[n0 + q];
+      Dv[q] *= gh;
+      Mv[q] *= gh;
+    }
+    *reinterpret_cast<float2*>(&T.D[ts][tg][n0]) = make_float2(Dv[0], Dv[1]);
+    *reinterpret_cast<float2*>(&T.M[ts][tg][n0]) = make_float2(Mv[0], Mv[1]);
+  }
+  // This wavefront is past its reads of the slot's h.
+  if (lane == 0) __hip_atomic_fetch_add(&L.consumed[s], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __builtin_amdgcn_wave_barrier();
+  const unsigned sbl = (unsigned)lane >> 5, j = (unsigned)lane & 31, g = j >> 2;   // 8 outputs
+  if (2 * (unsigned)wave + sbl < nsb) {
+    const float4* cd = reinterpret_cast<const float4*>(&T.D[sbl][g][0]);
+    const float4* cm = reinterpret_cast<const float4*>(&T.M[sbl][g][0]);
+    const float4 d0 = cd[0], d1 = cd[1], m0 = cm[0], m1 = cm[1];
+    const float coef[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+    const float msum = ((m0.x + m0.y) + (m0.z + m0.w)) + ((m1.x + m1.y) + (m1.z + m1.w));
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const uint4 dq = R.dq[half];
+      float s4[4] = {-msum, -msum, -msum, -msum};
+#pragma unroll
+      for (int wd = 0; wd < 4; ++wd) {
+        // Dword wd: neurons 2wd (bytes 0,1) and 2wd+1 (bytes 2,3); low
+        // nibbles columns 0 and 2, high nibbles columns 1 and 3.
+        const uint32_t v = word(dq, wd);
+        const uint32_t lo = nib_lo(v), hi = nib_hi(v);
+        const float ca = coef[2 * wd], cb = coef[2 * wd + 1];
+        s4[0] = fmaf(ub(lo, 0), ca, s4[0]);
+        s4[1] = fmaf(ub(hi, 0), ca, s4[1]);
+        s4[2] = fmaf(ub(lo, 1), ca, s4[2]);
+        s4[3] = fmaf(ub(hi, 1), ca, s4[3]);
+        s4[0] = fmaf(ub(lo, 2), cb, s4[0]);
+        s4[1] = fmaf(ub(hi, 2), cb, s4[1]);
+        s4[2] = fmaf(ub(lo, 3), cb, s4[2]);
+        s4[3] = fmaf(ub(hi, 3), cb, s4[3]);
+      }
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) y[4 * half + cc] += s4[cc];
+    }
+  }
+}
+
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
   uint32_t* status = S.out + (size_t)S.parity * S.out_words;
   if (blockIdx.x == 0) clear_other_parity(S);
   const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + H.pairs_off);
-  const unsigned hidden = H.hidden, nch = hidden / 64, nsb = hidden / 256, G = gridDim.x;
-  const unsigned ntask = 4 * H.npairs, lastt = ntask - 1;
+  const unsigned hidden = H.hidden, nch = hidden / 64, nsb = hidden / 256, G = gridDim.x, np = H.npairs;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool active = lane < (int)nch;
-  const int c = active ? lane : 0;
+  const unsigned c = active ? (unsigned)lane : nch - 1;   // idle lanes re-read the last chunk
   __shared__ __align__(16) DecodeLds L;
 
-  float4 x[16];
-  {
-    const float4* xs = reinterpret_cast<const float4*>(plan + H.x_off) + 16 * c;
+  // x first (the compiler then waits for x alone), then round 0; x goes to
+  // LDS as [k][lane] so that the per-neuron reads of a wavefront are
+  // contiguous.
+  const unsigned nx = hidden / 4;   // float4 of x
+  float4 xv[2];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = xs[i];
+  for (int k = 0; k < 2; ++k) {
+    const unsigned f = (unsigned)tid + kDecodeThreads * k;
+    const u32x4 v = gld<u32x4>(plan + H.x_off + 16 * (size_t)(f < nx ? f : 0));
+    xv[k] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
   }
+  unsigned p = blockIdx.x;   // the grid never exceeds the pair count
+  DecodeRound R0, R1, R2, R3;
+  load_round(pairs[p], 0, nch, nsb, wave, lane, c, R0);
+  if (tid < 4) L.published[tid] = L.consumed[tid] = 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const unsigned f = (unsigned)tid + kDecodeThreads * k;
+    if (f < nx) L.x[f & 15][f >> 4] = xv[k];
+  }
+  __syncthreads();
   float X0 = 0.f, X1 = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    X0 += (x[i].x + x[i].y) + (x[i].z + x[i].w);
-    X1 += (x[8 + i].x + x[8 + i].y) + (x[8 + i].z + x[8 + i].w);
+    const float4 a = L.x[i][c], b = L.x[8 + i][c];
+    X0 += (a.x + a.y) + (a.z + a.w);
+    X1 += (b.x + b.y) + (b.z + b.w);
   }
-  // x stays in registers for the whole kernel; the pins keep the compiler
-  // from re-reading it inside the task loop.
-#pragma unroll
-  for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(x[i].x), "+v"(x[i].y), "+v"(x[i].z), "+v"(x[i].w));
-  asm volatile("" : "+v"(X0), "+v"(X1));
   float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   uint32_t bad = 0;
-
-  unsigned task = blockIdx.x;
-  issue_gu(H, pairs, min(task, lastt), wave, lane, L.gu[0]);
-  issue_dn(H, pairs, min(task, lastt), wave, lane, L.dn[0]);
-  for (unsigned k = 0; task < ntask; ++k, task += G) {
-    const unsigned b = k & 1;
-    const unsigned nxt = min(task + G, lastt);
-    issue_gu(H, pairs, nxt, wave, lane, L.gu[b ^ 1]);
-    // In flight, oldest first: gu(k), dn(k), gu(k+1). Wait for gu(k).
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDecodeDnCopies + kDecodeGuCopies) : "memory");
-    const DecodeGu& G0 = L.gu[b];
-    float au[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      LaneRaw rr;
-      rr.q[0] = G0.q[wave][r][0][c];
-      rr.q[1] = G0.q[wave][r][1][c];
-      rr.h = G0.h[wave][r][c >> 2];
-      float sc[2], mn[2];
-      const bool ok = raw_scales<TQ4_K>(rr, c, sc, mn);
-      if (active && !ok) bad |= kErrScale;
-      const float part = lane_dot_f32<TQ4_K>(rr, sc, mn, x, X0, X1);
-      au[r] = wave_total(active ? part : 0.f);
+  // Round t: request round t+1 (the next pair's round 0 after round 3),
+  // compute h of round t, apply the down of round t-1. The scheduling
+  // barriers keep the loads where they are written.
+  for (unsigned k = 0;; ++k) {
+    const PairDesc& P = pairs[p];
+    const float gate = P.gate[0];
+    const unsigned q = p + G, t = 4 * k;
+    const bool more = q < np;
+    load_round(P, 1, nch, nsb, wave, lane, c, R1);
+    __builtin_amdgcn_sched_barrier(0);
+    publish_round(gate * neuron_h(R0, (int)c, active, L.x, X0, X1, bad), t, k, wave, lane, L, bad);
+    if (k) down_round(R3, t - 1, k - 1, wave, lane, nsb, L, y, bad);
+    __builtin_amdgcn_sched_barrier(0);
+    load_round(P, 2, nch, nsb, wave, lane, c, R2);
+    __builtin_amdgcn_sched_barrier(0);
+    publish_round(gate * neuron_h(R1, (int)c, active, L.x, X0, X1, bad), t + 1, k, wave, lane, L, bad);
+    down_round(R0, t, k, wave, lane, nsb, L, y, bad);
+    __builtin_amdgcn_sched_barrier(0);
+    load_round(P, 3, nch, nsb, wave, lane, c, R3);
+    __builtin_amdgcn_sched_barrier(0);
+    publish_round(gate * neuron_h(R2, (int)c, active, L.x, X0, X1, bad), t + 2, k, wave, lane, L, bad);
+    down_round(R1, t + 1, k, wave, lane, nsb, L, y, bad);
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) load_round(pairs[q], 0, nch, nsb, wave, lane, c, R0);
+    __builtin_amdgcn_sched_barrier(0);
+    publish_round(gate * neuron_h(R3, (int)c, active, L.x, X0, X1, bad), t + 3, k, wave, lane, L, bad);
+    down_round(R2, t + 2, k, wave, lane, nsb, L, y, bad);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!more) {
+      down_round(R3, t + 3, k, wave, lane, nsb, L, y, bad);
+      break;
     }
-    const float h = silu_mul_f32(au[0], au[1], bad);
-    if (lane == 0) L.h[wave] = pairs[task >> 2].gate[0] * h;
-    __syncthreads();
-    // Every wave is past the down of task k-1: its buffer can be refilled.
-    issue_dn(H, pairs, nxt, wave, lane, L.dn[b ^ 1]);
-    {
-      const unsigned sb = (unsigned)tid >> 5, tn = ((unsigned)tid >> 2) & 7, g0 = 2 * (tid & 3);
-      if (sb < nsb) {
-        const uint4 hdr = G0.th[8 * sb + tn];
-        const float gh = L.h[tn];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          float D, M;
-          bool ok;
-          hdr_dm(hdr, g0 + kk, D, M, ok);
-          if (!ok) bad |= kErrScale;
-          L.D[sb][g0 + kk][tn] = D * gh;
-          L.M[sb][g0 + kk][tn] = M * gh;
-        }
-      }
-    }
-    __syncthreads();
-    // In flight: dn(k), gu(k+1), dn(k+1). Wait for dn(k).
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDecodeGuCopies + kDecodeDnCopies) : "memory");
-    const unsigned sb = 2 * (unsigned)wave + ((unsigned)lane >> 5), j = (unsigned)lane & 31;
-    if (sb < nsb) {
-      const unsigned g = j >> 2;   // columns 8j..8j+7 lie in group 8j/32
-      const float4* cd = reinterpret_cast<const float4*>(&L.D[sb][g][0]);
-      const float4* cm = reinterpret_cast<const float4*>(&L.M[sb][g][0]);
-      const float4 d0 = cd[0], d1 = cd[1], m0 = cm[0], m1 = cm[1];
-      const float coef[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-      const float msum = ((m0.x + m0.y) + (m0.z + m0.w)) + ((m1.x + m1.y) + (m1.z + m1.w));
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const uint4 dq = L.dn[b].q[wave][half][lane];
-        float s4[4] = {-msum, -msum, -msum, -msum};
-#pragma unroll
-        for (int wd = 0; wd < 4; ++wd) {
-          // Dword wd: neurons 2wd (bytes 0,1) and 2wd+1 (bytes 2,3); low
-          // nibbles columns 0 and 2, high nibbles columns 1 and 3.
-          const uint32_t v = word(dq, wd);
-          const uint32_t lo = nib_lo(v), hi = nib_hi(v);
-          const float ca = coef[2 * wd], cb = coef[2 * wd + 1];
-          s4[0] = fmaf(ub(lo, 0), ca, s4[0]);
-          s4[1] = fmaf(ub(hi, 0), ca, s4[1]);
-          s4[2] = fmaf(ub(lo, 1), ca, s4[2]);
-          s4[3] = fmaf(ub(hi, 1), ca, s4[3]);
-          s4[0] = fmaf(ub(lo, 2), cb, s4[0]);
-          s4[1] = fmaf(ub(hi, 2), cb, s4[1]);
-          s4[2] = fmaf(ub(lo, 3), cb, s4[2]);
-          s4[3] = fmaf(ub(hi, 3), cb, s4[3]);
-        }
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) y[4 * half + cc] += s4[cc];
-      }
-    }
+    p = q;
   }
-  // Copies past the last task (clamped prefetches) land before exit.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if (bad) flag(status, bad);
   // Workgroup partial, position-major so that each store instruction covers
   // 1 KB: wavefront w, half h, lane l -> positions 4*(128w + 64h + l)..+3,
@@ -2014,14 +2110,13 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   bool decode = T == 1 && r->mode == MODE_F32 && np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
   for (uint32_t i = 0; decode && i < np; ++i) decode = pairs[i].gu == TQ4_K && pairs[i].dn == TQ4_KT;
   if (decode && !env_int("FRONK_HIP_NO_DECODE", 0)) {
-    // One workgroup per CU at most (each uses most of a CU's LDS).
+    // One workgroup per pair, one per CU at most (each uses most of a CU's
+    // LDS): the fewest workgroups that keep ceil(pairs / cap) pairs each.
     const uint32_t cap = E.cus < (unsigned)kDecodeGridMax ? E.cus : (unsigned)kDecodeGridMax;
-    // Equal task counts per workgroup where possible: the fewest workgroups
-    // that keep ceil(tasks / cap) tasks each, so none runs an extra round.
-    const uint32_t ntask = 4 * np, tpw = (ntask + cap - 1) / cap;
+    const uint32_t ppw = (np + cap - 1) / cap;
     H->kind = KIND_DECODE;
-    H->tpw = tpw;
-    H->grid = (ntask + tpw - 1) / tpw;
+    H->tpw = ppw;
+    H->grid = (np + ppw - 1) / ppw;
   } else {
     H->kind = KIND_LAYER;
     H->tpw = 0;
