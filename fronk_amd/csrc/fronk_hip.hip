@@ -1266,10 +1266,13 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(const uint8_t* __restri
 // polling would do at about 2 us per hop.
 //
 // Every lane loads exactly the bytes it uses into registers, with the
-// non-temporal policy, one round ahead of the round that uses them; the
-// rounds of a pair are unrolled, so each round's bytes have registers of
-// their own and the compiler's waits are exact. LDS holds x (read back per
-// neuron), h, the down headers and the down coefficients.
+// non-temporal policy: a round's gate/up bytes one round ahead of its h, its
+// down bytes together with the next round's gate/up bytes, one round ahead of
+// its down projection. Only x and round 0's gate/up bytes are requested
+// before the first h, so that they arrive early. The rounds of a pair are
+// unrolled, so each round's bytes have registers of their own and the
+// compiler's waits are exact. LDS holds x (read back per neuron), h, the
+// down headers and the down coefficients.
 
 // Non-temporal 16-byte load through a global-space pointer: a generic
 // pointer would make it a FLAT load, which also counts in lgkmcnt, so every
@@ -1279,12 +1282,14 @@ __device__ __forceinline__ uint4 ldnt(const uint8_t* p) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-struct DecodeRound {                   // one lane's bytes of one round
+struct DecodeGuBytes {                 // one lane's gate/up bytes of one round
   uint4 gq[2][2];                      // [gate, up][part]: nibbles of chunk c of neuron 8r + w
   uint4 gh[2];                         // [gate, up]: header of super-block c/4
-  uint4 dq[2];                         // down nibbles: super-block 2w + l/32, neurons 8r..8r+7,
+};
+struct DecodeDnBytes {                 // one lane's down bytes of one round
+  uint4 dq[2];                         // nibbles: super-block 2w + l/32, neurons 8r..8r+7,
                                        // outputs 8j..8j+3 and 8j+4..8j+7 (j = l%32)
-  uint4 dh;                            // down header: super-block 2w + (l%16)/8, neuron 8r + l%8
+  uint4 dh;                            // header: super-block 2w + (l%16)/8, neuron 8r + l%8
 };
 struct DecodeTable {                   // one wavefront's down coefficients of one round
   float D[2][8][8];                    // [super-block][group][neuron] d*sc*gate*h
@@ -1299,12 +1304,10 @@ struct DecodeLds {
   uint32_t consumed[4];                // wavefronts past their reads of slot s, over all pairs
 };
 
-// Round r of pair P for lane (wave, lane): gate and up rows of neuron
-// 8r + w (chunk c and the header of its super-block), the lane's down
-// nibbles and one down header. Super-blocks past the matrix are clamped to
-// its last one.
-__device__ __forceinline__ void load_round(const PairDesc& P, unsigned r, unsigned nch, unsigned nsb, int wave,
-                                           int lane, unsigned c, DecodeRound& R) {
+// Round r of pair P for lane (wave, lane), gate/up part: gate and up rows
+// of neuron 8r + w (chunk c and the header of its super-block).
+__device__ __forceinline__ void load_gu(const PairDesc& P, unsigned r, unsigned nch, int wave, unsigned c,
+                                        DecodeGuBytes& R) {
   const uint8_t* slice = reinterpret_cast<const uint8_t*>(P.slice);
   const uint32_t proj = P.proj, row = proj / kNeurons, n = 8 * r + (unsigned)wave;
 #pragma unroll
@@ -1314,7 +1317,12 @@ __device__ __forceinline__ void load_round(const PairDesc& P, unsigned r, unsign
     R.gq[k][1] = ldnt(rp + 16 * nch + 16 * c);
     R.gh[k] = ldnt(rp + 32 * nch + 16 * (c >> 2));
   }
-  const uint8_t* down = slice + 2 * (size_t)proj;
+}
+// Down part: the lane's down nibbles and one down header; super-blocks past
+// the matrix are clamped to its last one.
+__device__ __forceinline__ void load_dn(const PairDesc& P, unsigned r, unsigned nsb, int wave, int lane,
+                                        DecodeDnBytes& R) {
+  const uint8_t* down = reinterpret_cast<const uint8_t*>(P.slice) + 2 * (size_t)P.proj;
   const unsigned sb = min(2 * (unsigned)wave + ((unsigned)lane >> 5), nsb - 1), j = (unsigned)lane & 31;
   R.dq[0] = ldnt(down + 4608 * (size_t)sb + 1024 * r + 32 * j);
   R.dq[1] = ldnt(down + 4608 * (size_t)sb + 1024 * r + 32 * j + 16);
@@ -1340,7 +1348,7 @@ __device__ __forceinline__ float silu_mul_f32(float a, float u, uint32_t& bad) {
 // share each x value (read from LDS in two halves of 8 float4, so that only
 // half of the lane's x is in registers at once) and run as 16 independent
 // FMA chains; the two sums are reduced side by side.
-__device__ __forceinline__ float neuron_h(const DecodeRound& R, int c, bool active, const float4 (&xl)[16][64],
+__device__ __forceinline__ float neuron_h(const DecodeGuBytes& R, int c, bool active, const float4 (&xl)[16][64],
                                           float X0, float X1, uint32_t& bad) {
   LaneRaw rg, ru;
   rg.q[0] = R.gq[0][0];
@@ -1418,7 +1426,7 @@ __device__ __forceinline__ void publish_round(float gh, unsigned t, unsigned k, 
 
 // Down projection of round t (pair iteration k) from the round's down bytes
 // and the 8 published h: coefficients, then 8 outputs per lane.
-__device__ __forceinline__ void down_round(const DecodeRound& R, unsigned t, unsigned k, int wave, int lane,
+__device__ __forceinline__ void down_round(const DecodeDnBytes& R, unsigned t, unsigned k, int wave, int lane,
                                            unsigned nsb, DecodeLds& L, float (&y)[8], uint32_t& bad) {
   const unsigned s = t & 3;
   lds_wait(&L.published[s], kDecodeWaves * (k + 1), bad);
@@ -1502,8 +1510,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
     xv[k] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
   }
   unsigned p = blockIdx.x;   // the grid never exceeds the pair count
-  DecodeRound R0, R1, R2, R3;
-  load_round(pairs[p], 0, nch, nsb, wave, lane, c, R0);
+  DecodeGuBytes G0, G1, G2, G3;
+  DecodeDnBytes D0, D1, D2, D3;
+  load_gu(pairs[p], 0, nch, wave, c, G0);
   if (tid < 4) L.published[tid] = L.consumed[tid] = 0;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -1520,36 +1529,41 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
   }
   float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   uint32_t bad = 0;
-  // Round t: request round t+1 (the next pair's round 0 after round 3),
-  // compute h of round t, apply the down of round t-1. The scheduling
-  // barriers keep the loads where they are written.
+  // Round t: request the gate/up bytes of round t+1 (the next pair's round
+  // 0 after round 3) and the down bytes of round t, compute h of round t,
+  // apply the down of round t-1. The scheduling barriers keep the loads where
+  // they are written.
   for (unsigned k = 0;; ++k) {
     const PairDesc& P = pairs[p];
     const float gate = P.gate[0];
     const unsigned q = p + G, t = 4 * k;
     const bool more = q < np;
-    load_round(P, 1, nch, nsb, wave, lane, c, R1);
+    load_gu(P, 1, nch, wave, c, G1);
+    load_dn(P, 0, nsb, wave, lane, D0);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(gate * neuron_h(R0, (int)c, active, L.x, X0, X1, bad), t, k, wave, lane, L, bad);
-    if (k) down_round(R3, t - 1, k - 1, wave, lane, nsb, L, y, bad);
+    publish_round(gate * neuron_h(G0, (int)c, active, L.x, X0, X1, bad), t, k, wave, lane, L, bad);
+    if (k) down_round(D3, t - 1, k - 1, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
-    load_round(P, 2, nch, nsb, wave, lane, c, R2);
+    load_gu(P, 2, nch, wave, c, G2);
+    load_dn(P, 1, nsb, wave, lane, D1);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(gate * neuron_h(R1, (int)c, active, L.x, X0, X1, bad), t + 1, k, wave, lane, L, bad);
-    down_round(R0, t, k, wave, lane, nsb, L, y, bad);
+    publish_round(gate * neuron_h(G1, (int)c, active, L.x, X0, X1, bad), t + 1, k, wave, lane, L, bad);
+    down_round(D0, t, k, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
-    load_round(P, 3, nch, nsb, wave, lane, c, R3);
+    load_gu(P, 3, nch, wave, c, G3);
+    load_dn(P, 2, nsb, wave, lane, D2);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(gate * neuron_h(R2, (int)c, active, L.x, X0, X1, bad), t + 2, k, wave, lane, L, bad);
-    down_round(R1, t + 1, k, wave, lane, nsb, L, y, bad);
+    publish_round(gate * neuron_h(G2, (int)c, active, L.x, X0, X1, bad), t + 2, k, wave, lane, L, bad);
+    down_round(D1, t + 1, k, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
-    if (more) load_round(pairs[q], 0, nch, nsb, wave, lane, c, R0);
+    if (more) load_gu(pairs[q], 0, nch, wave, c, G0);
+    load_dn(P, 3, nsb, wave, lane, D3);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(gate * neuron_h(R3, (int)c, active, L.x, X0, X1, bad), t + 3, k, wave, lane, L, bad);
-    down_round(R2, t + 2, k, wave, lane, nsb, L, y, bad);
+    publish_round(gate * neuron_h(G3, (int)c, active, L.x, X0, X1, bad), t + 3, k, wave, lane, L, bad);
+    down_round(D2, t + 2, k, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
     if (!more) {
-      down_round(R3, t + 3, k, wave, lane, nsb, L, y, bad);
+      down_round(D3, t + 3, k, wave, lane, nsb, L, y, bad);
       break;
     }
     p = q;
