@@ -1274,13 +1274,35 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(const uint8_t* __restri
 // compiler's waits are exact. LDS holds x (read back per neuron), h, the
 // down headers and the down coefficients.
 
-// Non-temporal 16-byte load through a global-space pointer: a generic
-// pointer would make it a FLAT load, which also counts in lgkmcnt, so every
-// LDS wait would wait for the weight bytes in flight too.
-__device__ __forceinline__ uint4 ldnt(const uint8_t* p) {
-  const u32x4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)(p));
+// The weight loads are raw buffer loads with the non-temporal policy: the
+// pair's slice is a buffer resource in scalar registers (bounded by the
+// slice's bytes, so that an offset past it reads zeros), the per-lane part of
+// each offset is computed once, the per-round part is a scalar offset. No
+// 64-bit address arithmetic per load, and the loads count in vmcnt only.
+struct PairBuf {
+  __amdgpu_buffer_rsrc_t rsrc;         // the pair's slice
+  uint32_t proj, row;                  // bytes of the 32 gate rows (= up offset), of one row
+  float gate;                          // the token's expert weight
+};
+__device__ __forceinline__ PairBuf pair_buf(const PairDesc& P) {
+  PairBuf B;
+  B.proj = P.proj;
+  B.row = P.proj / kNeurons;
+  B.gate = P.gate[0];
+  B.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(P.slice), (short)0, (int)(3 * P.proj),
+                                             0x00020000);
+  return B;
+}
+__device__ __forceinline__ uint4 bld(const PairBuf& B, uint32_t voff, uint32_t soff) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(B.rsrc, (int)voff, (int)soff, 2);   // 2: nt
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+// Per-lane offsets of the loads, fixed for the kernel.
+struct LaneOffsets {
+  uint32_t q0, q1, gh;                 // gate/up row: parts 0 and 1 of chunk c, header of super-block c/4
+  uint32_t dq, dh;                     // down matrix: nibbles of super-block 2w + l/32, header of
+                                       // super-block 2w + (l%16)/8 and neuron l%8 (clamped super-blocks)
+};
 
 struct DecodeGuBytes {                 // one lane's gate/up bytes of one round
   uint4 gq[2][2];                      // [gate, up][part]: nibbles of chunk c of neuron 8r + w
@@ -1304,30 +1326,24 @@ struct DecodeLds {
   uint32_t consumed[4];                // wavefronts past their reads of slot s, over all pairs
 };
 
-// Round r of pair P for lane (wave, lane), gate/up part: gate and up rows
-// of neuron 8r + w (chunk c and the header of its super-block).
-__device__ __forceinline__ void load_gu(const PairDesc& P, unsigned r, unsigned nch, int wave, unsigned c,
+// Round r, gate/up part: gate and up rows of neuron 8r + w.
+__device__ __forceinline__ void load_gu(const PairBuf& B, unsigned r, int wave, const LaneOffsets& o,
                                         DecodeGuBytes& R) {
-  const uint8_t* slice = reinterpret_cast<const uint8_t*>(P.slice);
-  const uint32_t proj = P.proj, row = proj / kNeurons, n = 8 * r + (unsigned)wave;
+  const uint32_t n = 8 * r + (unsigned)wave;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
-    const uint8_t* rp = slice + (k ? proj : 0) + (size_t)n * row;
-    R.gq[k][0] = ldnt(rp + 16 * c);
-    R.gq[k][1] = ldnt(rp + 16 * nch + 16 * c);
-    R.gh[k] = ldnt(rp + 32 * nch + 16 * (c >> 2));
+    const uint32_t base = (k ? B.proj : 0) + n * B.row;
+    R.gq[k][0] = bld(B, o.q0, base);
+    R.gq[k][1] = bld(B, o.q1, base);
+    R.gh[k] = bld(B, o.gh, base);
   }
 }
-// Down part: the lane's down nibbles and one down header; super-blocks past
-// the matrix are clamped to its last one.
-__device__ __forceinline__ void load_dn(const PairDesc& P, unsigned r, unsigned nsb, int wave, int lane,
-                                        DecodeDnBytes& R) {
-  const uint8_t* down = reinterpret_cast<const uint8_t*>(P.slice) + 2 * (size_t)P.proj;
-  const unsigned sb = min(2 * (unsigned)wave + ((unsigned)lane >> 5), nsb - 1), j = (unsigned)lane & 31;
-  R.dq[0] = ldnt(down + 4608 * (size_t)sb + 1024 * r + 32 * j);
-  R.dq[1] = ldnt(down + 4608 * (size_t)sb + 1024 * r + 32 * j + 16);
-  const unsigned hs = min(2 * (unsigned)wave + (((unsigned)lane & 15) >> 3), nsb - 1);
-  R.dh = ldnt(down + 4608 * (size_t)hs + 4096 + 16 * (8 * r + ((unsigned)lane & 7)));
+// Round r, down part: the lane's nibbles of neurons 8r..8r+7 and one header.
+__device__ __forceinline__ void load_dn(const PairBuf& B, unsigned r, const LaneOffsets& o, DecodeDnBytes& R) {
+  const uint32_t base = 2 * B.proj;
+  R.dq[0] = bld(B, o.dq, base + 1024 * r);
+  R.dq[1] = bld(B, o.dq + 16, base + 1024 * r);
+  R.dh = bld(B, o.dh, base + 128 * r);
 }
 
 // SiLU(a)*u in fp32 with the stable sigmoid form; a, u or h outside fp32
@@ -1510,9 +1526,16 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
     xv[k] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
   }
   unsigned p = blockIdx.x;   // the grid never exceeds the pair count
+  LaneOffsets lo;
+  lo.q0 = 16 * c;
+  lo.q1 = 16 * nch + 16 * c;
+  lo.gh = 32 * nch + 16 * (c >> 2);
+  lo.dq = 4608 * min(2 * (unsigned)wave + ((unsigned)lane >> 5), nsb - 1) + 32 * ((unsigned)lane & 31);
+  lo.dh = 4608 * min(2 * (unsigned)wave + (((unsigned)lane & 15) >> 3), nsb - 1) + 4096 + 16 * ((unsigned)lane & 7);
+  PairBuf B = pair_buf(pairs[p]);
   DecodeGuBytes G0, G1, G2, G3;
   DecodeDnBytes D0, D1, D2, D3;
-  load_gu(pairs[p], 0, nch, wave, c, G0);
+  load_gu(B, 0, wave, lo, G0);
   if (tid < 4) L.published[tid] = L.consumed[tid] = 0;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -1534,32 +1557,31 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
   // apply the down of round t-1. The scheduling barriers keep the loads where
   // they are written.
   for (unsigned k = 0;; ++k) {
-    const PairDesc& P = pairs[p];
-    const float gate = P.gate[0];
     const unsigned q = p + G, t = 4 * k;
     const bool more = q < np;
-    load_gu(P, 1, nch, wave, c, G1);
-    load_dn(P, 0, nsb, wave, lane, D0);
+    load_gu(B, 1, wave, lo, G1);
+    load_dn(B, 0, lo, D0);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(gate * neuron_h(G0, (int)c, active, L.x, X0, X1, bad), t, k, wave, lane, L, bad);
+    publish_round(B.gate * neuron_h(G0, (int)c, active, L.x, X0, X1, bad), t, k, wave, lane, L, bad);
     if (k) down_round(D3, t - 1, k - 1, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
-    load_gu(P, 2, nch, wave, c, G2);
-    load_dn(P, 1, nsb, wave, lane, D1);
+    load_gu(B, 2, wave, lo, G2);
+    load_dn(B, 1, lo, D1);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(gate * neuron_h(G1, (int)c, active, L.x, X0, X1, bad), t + 1, k, wave, lane, L, bad);
+    publish_round(B.gate * neuron_h(G1, (int)c, active, L.x, X0, X1, bad), t + 1, k, wave, lane, L, bad);
     down_round(D0, t, k, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
-    load_gu(P, 3, nch, wave, c, G3);
-    load_dn(P, 2, nsb, wave, lane, D2);
+    load_gu(B, 3, wave, lo, G3);
+    load_dn(B, 2, lo, D2);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(gate * neuron_h(G2, (int)c, active, L.x, X0, X1, bad), t + 2, k, wave, lane, L, bad);
+    publish_round(B.gate * neuron_h(G2, (int)c, active, L.x, X0, X1, bad), t + 2, k, wave, lane, L, bad);
     down_round(D1, t + 1, k, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
-    if (more) load_gu(pairs[q], 0, nch, wave, c, G0);
-    load_dn(P, 3, nsb, wave, lane, D3);
+    const PairBuf Bn = pair_buf(pairs[more ? q : p]);
+    if (more) load_gu(Bn, 0, wave, lo, G0);
+    load_dn(B, 3, lo, D3);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(gate * neuron_h(G3, (int)c, active, L.x, X0, X1, bad), t + 3, k, wave, lane, L, bad);
+    publish_round(B.gate * neuron_h(G3, (int)c, active, L.x, X0, X1, bad), t + 3, k, wave, lane, L, bad);
     down_round(D2, t + 2, k, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
     if (!more) {
@@ -1567,6 +1589,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
       break;
     }
     p = q;
+    B = Bn;
   }
   if (bad) flag(status, bad);
   // Workgroup partial, position-major so that each store instruction covers
