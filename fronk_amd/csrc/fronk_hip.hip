@@ -85,9 +85,16 @@ struct PlanHeader {
 };
 static_assert(sizeof(PlanHeader) == 80, "header layout");
 
-// Which kernel a plan runs: the two-phase layer kernel, or the single-token
-// decode kernel for all-Q4_K units with the transposed down.
+// Which kernel a plan runs: the two-phase layer kernel, or the decode
+// kernel for all-Q4_K units with the transposed down (F32, routed experts
+// only), whose work list is (token, pair) units, token-major, each with its
+// own partial.
 enum : uint32_t { KIND_LAYER = 0, KIND_DECODE = 1 };
+// A decode plan's token table (at groups_off): token t's units.
+struct DecodeToken {
+  uint32_t first, count;
+};
+constexpr int kDecodeUnitsPerToken = 10 * kBlocks;
 
 struct Scratch {
   uint32_t* done;            // [2][kMaxPairs] phase-A wave completions per pair
@@ -95,7 +102,7 @@ struct Scratch {
   float* hbuf;               // [kMaxPairs][8][32]
   double* partial;           // [groups][burst][hidden]
   uint32_t* out;             // [2][out_words]: status, pad x3, y
-  float* wgpart;             // [kDecodeGridMax][hidden]: decode workgroup partials
+  float* wgpart;             // [kMaxPairs][hidden]: decode unit partials
   uint32_t* bar;             // [2]: decode workgroups past their partial store
   uint32_t out_words;
   uint32_t parity;
@@ -1283,14 +1290,21 @@ struct PairBuf {
   __amdgpu_buffer_rsrc_t rsrc;         // the pair's slice
   uint32_t proj, row;                  // bytes of the 32 gate rows (= up offset), of one row
   float gate;                          // the token's expert weight
+  uint32_t token;                      // the unit's token
 };
+// The fields pass through readfirstlane: they are uniform (one pair per
+// workgroup at a time), and the compiler must know it, or it would wrap every
+// buffer load in a loop over distinct resource values.
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ PairBuf pair_buf(const PairDesc& P) {
   PairBuf B;
-  B.proj = P.proj;
-  B.row = P.proj / kNeurons;
-  B.gate = P.gate[0];
-  B.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(P.slice), (short)0, (int)(3 * P.proj),
-                                             0x00020000);
+  const uint64_t slice = P.slice;
+  const uint64_t base = ((uint64_t)uniform((uint32_t)(slice >> 32)) << 32) | uniform((uint32_t)slice);
+  B.token = uniform(P.pad);
+  B.proj = uniform(P.proj);
+  B.row = B.proj / kNeurons;
+  B.gate = __uint_as_float(uniform(__float_as_uint(P.gate[0])));
+  B.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), (short)0, (int)(3 * B.proj), 0x00020000);
   return B;
 }
 __device__ __forceinline__ uint4 bld(const PairBuf& B, uint32_t voff, uint32_t soff) {
@@ -1318,7 +1332,7 @@ struct DecodeTable {                   // one wavefront's down coefficients of o
   float M[2][8][8];                    // dmin*mi*gate*h
 };
 struct DecodeLds {
-  float4 x[16][64];                    // [k][lane c] = x[64c + 4k .. 64c + 4k + 3]
+  float4 x[kMaxBurst][16][64];         // [token][k][lane c] = x[64c + 4k .. 64c + 4k + 3]
   uint4 dh[kDecodeWaves][16];          // [wave][super-block 2w + i/8, neuron 8r + i%8]
   DecodeTable table[kDecodeWaves];
   float h[4][8];                       // gate*h of round t's 8 neurons in slot t%4
@@ -1326,7 +1340,8 @@ struct DecodeLds {
   uint32_t consumed[4];                // wavefronts past their reads of slot s, over all pairs
 };
 
-// Round r, gate/up part: gate and up rows of neuron 8r + w.
+// Round r, gate/up part: gate and up rows of neuron 8r + w (kGuLoads loads).
+constexpr int kGuLoads = 6;
 __device__ __forceinline__ void load_gu(const PairBuf& B, unsigned r, int wave, const LaneOffsets& o,
                                         DecodeGuBytes& R) {
   const uint32_t n = 8 * r + (unsigned)wave;
@@ -1503,29 +1518,48 @@ __device__ __forceinline__ void down_round(const DecodeDnBytes& R, unsigned t, u
   }
 }
 
+// The unit's fp32 partial, position-major so that each store instruction
+// covers 1 KB: wavefront w, half h, lane l -> positions 4*(128w + 64h + l)..+3,
+// columns 256*sb + 8j + 4h..+3 (sb = 2w + l/32, j = l%32); y restarts at 0.
+// The kernel boundary makes the partials visible to decode_reduce.
+__device__ __forceinline__ void store_partial(const Scratch& S, unsigned unit, int wave, int lane, float (&y)[8]) {
+  float* mine = S.wgpart + (size_t)unit * kMaxHidden;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+    *reinterpret_cast<float4*>(mine + 4 * (128 * wave + 64 * hh + lane)) =
+        make_float4(y[4 * hh], y[4 * hh + 1], y[4 * hh + 2], y[4 * hh + 3]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = 0.f;
+}
+
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
   uint32_t* status = S.out + (size_t)S.parity * S.out_words;
   if (blockIdx.x == 0) clear_other_parity(S);
   const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + H.pairs_off);
   const unsigned hidden = H.hidden, nch = hidden / 64, nsb = hidden / 256, G = gridDim.x, np = H.npairs;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wavefront index through readfirstlane: the compiler then knows it is
+  // uniform, so offsets built from it stay in scalar registers.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool active = lane < (int)nch;
   const unsigned c = active ? (unsigned)lane : nch - 1;   // idle lanes re-read the last chunk
   __shared__ __align__(16) DecodeLds L;
 
-  // x first (the compiler then waits for x alone), then round 0; x goes to
-  // LDS as [k][lane] so that the per-neuron reads of a wavefront are
-  // contiguous.
-  const unsigned nx = hidden / 4;   // float4 of x
-  float4 xv[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const unsigned f = (unsigned)tid + kDecodeThreads * k;
-    const u32x4 v = gld<u32x4>(plan + H.x_off + 16 * (size_t)(f < nx ? f : 0));
-    xv[k] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+  // x of every token, copied to LDS as [token][k][lane] by the load units
+  // (lane c of copy k: x[64c + 4k .. +3]), so that the per-word reads of a
+  // wavefront are contiguous; then round 0 of the first unit, whose six
+  // loads are the only ones younger than the copies when they are waited for.
+  const unsigned T = H.burst;
+  {
+    const uint8_t* xg = plan + H.x_off;
+    for (unsigned i = (unsigned)wave; i < 16 * T; i += kDecodeWaves) {
+      const unsigned tok = i >> 4, k = i & 15;
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&L.x[tok][k][0]);
+      const uint8_t* g = xg + (size_t)tok * hidden * sizeof(float) + 256 * (size_t)c + 16 * k;
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+    }
   }
-  unsigned p = blockIdx.x;   // the grid never exceeds the pair count
+  unsigned p = blockIdx.x;   // the grid never exceeds the unit count
   LaneOffsets lo;
   lo.q0 = 16 * c;
   lo.q1 = 16 * nch + 16 * c;
@@ -1536,71 +1570,67 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
   DecodeGuBytes G0, G1, G2, G3;
   DecodeDnBytes D0, D1, D2, D3;
   load_gu(B, 0, wave, lo, G0);
+  static_assert(kGuLoads == 6, "the wait below counts round 0's loads");
+  asm volatile("s_waitcnt vmcnt(6)" ::: "memory");   // this wavefront's x copies
   if (tid < 4) L.published[tid] = L.consumed[tid] = 0;
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const unsigned f = (unsigned)tid + kDecodeThreads * k;
-    if (f < nx) L.x[f & 15][f >> 4] = xv[k];
-  }
-  __syncthreads();
-  float X0 = 0.f, X1 = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 a = L.x[i][c], b = L.x[8 + i][c];
-    X0 += (a.x + a.y) + (a.z + a.w);
-    X1 += (b.x + b.y) + (b.z + b.w);
-  }
+  __syncthreads();   // x is in LDS; the counters are zero
   float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   uint32_t bad = 0;
-  // Round t: request the gate/up bytes of round t+1 (the next pair's round
-  // 0 after round 3) and the down bytes of round t, compute h of round t,
-  // apply the down of round t-1. The scheduling barriers keep the loads where
-  // they are written.
+  unsigned prev = p;
+  // Unit k (a (token, pair) of the request), round t = 4k + r: request the
+  // gate/up bytes of round t+1 (the next unit's round 0 after round 3) and
+  // the down bytes of round t, compute h of round t, apply the down of round
+  // t-1; a unit's partial is stored after its last down. The scheduling
+  // barriers keep the loads where they are written.
   for (unsigned k = 0;; ++k) {
     const unsigned q = p + G, t = 4 * k;
     const bool more = q < np;
+    const float4(&xl)[16][64] = L.x[B.token];
+    float X0 = 0.f, X1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 a = xl[i][c], b = xl[8 + i][c];
+      X0 += (a.x + a.y) + (a.z + a.w);
+      X1 += (b.x + b.y) + (b.z + b.w);
+    }
     load_gu(B, 1, wave, lo, G1);
     load_dn(B, 0, lo, D0);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(B.gate * neuron_h(G0, (int)c, active, L.x, X0, X1, bad), t, k, wave, lane, L, bad);
-    if (k) down_round(D3, t - 1, k - 1, wave, lane, nsb, L, y, bad);
+    publish_round(B.gate * neuron_h(G0, (int)c, active, xl, X0, X1, bad), t, k, wave, lane, L, bad);
+    if (k) {
+      down_round(D3, t - 1, k - 1, wave, lane, nsb, L, y, bad);
+      store_partial(S, prev, wave, lane, y);
+    }
     __builtin_amdgcn_sched_barrier(0);
     load_gu(B, 2, wave, lo, G2);
     load_dn(B, 1, lo, D1);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(B.gate * neuron_h(G1, (int)c, active, L.x, X0, X1, bad), t + 1, k, wave, lane, L, bad);
+    publish_round(B.gate * neuron_h(G1, (int)c, active, xl, X0, X1, bad), t + 1, k, wave, lane, L, bad);
     down_round(D0, t, k, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
     load_gu(B, 3, wave, lo, G3);
     load_dn(B, 2, lo, D2);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(B.gate * neuron_h(G2, (int)c, active, L.x, X0, X1, bad), t + 2, k, wave, lane, L, bad);
+    publish_round(B.gate * neuron_h(G2, (int)c, active, xl, X0, X1, bad), t + 2, k, wave, lane, L, bad);
     down_round(D1, t + 1, k, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
     const PairBuf Bn = pair_buf(pairs[more ? q : p]);
     if (more) load_gu(Bn, 0, wave, lo, G0);
     load_dn(B, 3, lo, D3);
     __builtin_amdgcn_sched_barrier(0);
-    publish_round(B.gate * neuron_h(G3, (int)c, active, L.x, X0, X1, bad), t + 3, k, wave, lane, L, bad);
+    publish_round(B.gate * neuron_h(G3, (int)c, active, xl, X0, X1, bad), t + 3, k, wave, lane, L, bad);
     down_round(D2, t + 2, k, wave, lane, nsb, L, y, bad);
     __builtin_amdgcn_sched_barrier(0);
     if (!more) {
       down_round(D3, t + 3, k, wave, lane, nsb, L, y, bad);
+      store_partial(S, p, wave, lane, y);
       break;
     }
+    prev = p;
     p = q;
     B = Bn;
   }
   if (bad) flag(status, bad);
-  // Workgroup partial, position-major so that each store instruction covers
-  // 1 KB: wavefront w, half h, lane l -> positions 4*(128w + 64h + l)..+3,
-  // columns 256*sb + 8j + 4h..+3 (sb = 2w + l/32, j = l%32). The kernel
-  // boundary makes the partials visible to decode_reduce.
-  float* mine = S.wgpart + (size_t)blockIdx.x * kMaxHidden;
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh)
-    *reinterpret_cast<float4*>(mine + 4 * (128 * wave + 64 * hh + lane)) =
-        make_float4(y[4 * hh], y[4 * hh + 1], y[4 * hh + 2], y[4 * hh + 3]);
 }
 
 // Position p of a decode partial -> output column (see above).
@@ -1609,18 +1639,19 @@ __device__ __forceinline__ unsigned decode_column(unsigned p) {
   return 256 * (2 * w + (l >> 5)) + 8 * (l & 31) + 4 * hh + cc;
 }
 
-// Sum of the G decode partials, 16 positions per workgroup: thread (ps, q)
-// adds partials ps, ps+128 of positions 16*blockIdx + 4q..4q+3 in fp64,
-// then a fixed binary tree over the 128 ps; narrowing with the reference's
-// overflow rule (backends/ref.c:95) and the status word of decode_kernel.
+// Sum of a token's unit partials, 16 positions per workgroup (token =
+// blockIdx.y, units [first, first + count) of the plan's token table):
+// thread (ps, q) adds units ps, ps+128 of positions 16*blockIdx.x + 4q..4q+3
+// in fp64, then a fixed binary tree over the 128 ps; narrowing with the
+// reference's overflow rule (backends/ref.c:95) and the status word of
+// decode_kernel. A token's result depends only on its own units, in order.
 constexpr int kReduceThreads = 512;
 constexpr int kReducePositions = 16;
-static_assert(kDecodeGridMax <= 2 * (kReduceThreads / (kReducePositions / 4)), "two partials per reduce lane");
-__global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* __restrict__ plan, Scratch S,
-                                                                unsigned G) {
+__global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
+  const DecodeToken tk = reinterpret_cast<const DecodeToken*>(plan + H.groups_off)[blockIdx.y];
   uint32_t* status = S.out + (size_t)S.parity * S.out_words;
-  float* yout = reinterpret_cast<float*>(status + 4);
+  float* yout = reinterpret_cast<float*>(status + 4) + (size_t)blockIdx.y * H.hidden;
   constexpr unsigned kLanes = kReduceThreads / (kReducePositions / 4);   // partial lanes
   const unsigned tid = threadIdx.x, q = tid & 3, ps = tid >> 2;
   const unsigned p0 = kReducePositions * blockIdx.x + 4 * q;
@@ -1629,8 +1660,8 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const unsigned g = ps + kLanes * k;
-    r[k] = g < G ? *reinterpret_cast<const float4*>(S.wgpart + (size_t)g * kMaxHidden + p0)
-                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    r[k] = g < tk.count ? *reinterpret_cast<const float4*>(S.wgpart + (size_t)(tk.first + g) * kMaxHidden + p0)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -1661,6 +1692,7 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
     }
   }
 }
+static_assert(kDecodeUnitsPerToken <= 2 * (kReduceThreads / (kReducePositions / 4)), "two partials per reduce lane");
 
 // ------------------------------------------------------- load re-tiling
 //
@@ -2005,7 +2037,7 @@ struct Engine {
   size_t partial_bytes = 0;
   uint32_t* out = nullptr;        // [2][out_words]
   uint32_t out_words = 0;
-  float* wgpart = nullptr;        // [kDecodeGridMax][kMaxHidden]
+  float* wgpart = nullptr;        // [kMaxPairs][kMaxHidden]
   uint32_t* bar = nullptr;        // [2]
   uint8_t* plan_dev = nullptr;
   uint8_t* plan_host = nullptr;   // pinned
@@ -2141,19 +2173,53 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
                 kWaves * kCols * sizeof(double);
   H->lds = (uint32_t)(ldsA > ldsB ? ldsA : ldsB);
   if (H->lds > (uint32_t)kLdsLimit) return FR_HIP_UNSUPPORTED;
-  // Single token, F32, every pair Q4_K with the transposed down: the decode
-  // kernel, with ceil(tasks/256) tasks per workgroup spread over the fewest
-  // workgroups that keeps that count.
-  bool decode = T == 1 && r->mode == MODE_F32 && np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
-  for (uint32_t i = 0; decode && i < np; ++i) decode = pairs[i].gu == TQ4_K && pairs[i].dn == TQ4_KT;
+  // F32, routed experts only (no shared gate), every pair Q4_K with the
+  // transposed down: the decode kernel. Its work list is rebuilt as (token,
+  // pair) units, token-major, each token's experts in request order and
+  // blocks ascending (the single-token pair order), so that a token's units
+  // and their summation order do not depend on the rest of the burst.
+  bool decode = r->mode == MODE_F32 && np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
+  for (uint32_t i = 0; decode && i < np; ++i)
+    decode = pairs[i].gu == TQ4_K && pairs[i].dn == TQ4_KT;
+  for (int s2 = 0; decode && s2 < nu; ++s2) decode = ids[s2] != kShared;
   if (decode && !env_int("FRONK_HIP_NO_DECODE", 0)) {
-    // One workgroup per pair, one per CU at most (each uses most of a CU's
-    // LDS): the fewest workgroups that keep ceil(pairs / cap) pairs each.
+    uint32_t nunits = 0;
+    DecodeToken tok[kMaxBurst];
+    for (uint32_t t = 0; t < T; ++t) {
+      tok[t].first = nunits;
+      for (int e = 0; e < 10; ++e) {
+        const uint16_t id = r->expert[t * 10 + e];
+        for (int b = 0; b < kBlocks; ++b) {
+          if (!E.block[b]) continue;
+          const Layout& l = E.lay[b];
+          PairDesc& U = pairs[nunits++];
+          memset(&U, 0, sizeof(U));
+          U.slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer + (uint64_t)id * l.slice);
+          U.proj = (uint32_t)l.proj;
+          U.gu = (uint8_t)l.gu;
+          U.dn = (uint8_t)l.dn;
+          U.tmask = (uint8_t)(1u << t);
+          U.pad = (uint8_t)t;
+          U.gate[0] = r->gate[t * 11 + e];
+        }
+      }
+      tok[t].count = nunits - tok[t].first;
+    }
+    H->npairs = nunits;
+    H->ngroups = T;
+    H->groups_off = H->pairs_off + nunits * sizeof(PairDesc);
+    memcpy(out + H->groups_off, tok, T * sizeof(DecodeToken));
+    H->x_off = (uint32_t)((H->groups_off + T * sizeof(DecodeToken) + 255) & ~255u);
+    memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
+    H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
+    // One workgroup per unit, one per CU at most (the fewest workgroups that
+    // keep ceil(units / cap) units each).
     const uint32_t cap = E.cus < (unsigned)kDecodeGridMax ? E.cus : (unsigned)kDecodeGridMax;
-    const uint32_t ppw = (np + cap - 1) / cap;
+    const uint32_t ppw = (nunits + cap - 1) / cap;
     H->kind = KIND_DECODE;
     H->tpw = ppw;
-    H->grid = (np + ppw - 1) / ppw;
+    H->grid = (nunits + ppw - 1) / ppw;
+    np = nunits;
   } else {
     H->kind = KIND_LAYER;
     H->tpw = 0;
@@ -2171,7 +2237,8 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
 
 int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream) {
   if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
-  if (H.kind == KIND_DECODE && (grid > (unsigned)kDecodeGridMax || H.burst != 1)) return FR_HIP_INVALID;
+  if (H.kind == KIND_DECODE && (grid > (unsigned)kDecodeGridMax || grid > H.npairs || H.ngroups != H.burst))
+    return FR_HIP_INVALID;
   Scratch S;
   S.done = E.done;
   S.fin = E.fin;
@@ -2189,8 +2256,8 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
   if (H.kind == KIND_DECODE) {
     hipLaunchKernelGGL(decode_kernel, g, dim3(kDecodeThreads), 0, stream, dev_plan, S);
     if (te && hipEventRecord(te[1], stream) != hipSuccess) return FR_HIP_IO;
-    hipLaunchKernelGGL(decode_reduce, dim3(kMaxHidden / kReducePositions), dim3(kReduceThreads), 0, stream, dev_plan,
-                       S, grid);
+    hipLaunchKernelGGL(decode_reduce, dim3(kMaxHidden / kReducePositions, H.burst), dim3(kReduceThreads), 0, stream,
+                       dev_plan, S);
   } else switch (H.mode) {
     case MODE_F32:
       if (one) hipLaunchKernelGGL((layer_kernel<MODE_F32, 1>), g, blk, H.lds, stream, dev_plan, S);
@@ -2267,7 +2334,7 @@ int fr_hip_open(int device) {
   CK(hipMalloc(&E.partial, E.partial_bytes));
   E.out_words = 4 + kMaxBurst * kMaxHidden;
   CK(hipMalloc(&E.out, 2 * (size_t)E.out_words * sizeof(uint32_t)));
-  CK(hipMalloc(&E.wgpart, (size_t)kDecodeGridMax * kMaxHidden * sizeof(float)));
+  CK(hipMalloc(&E.wgpart, (size_t)kMaxPairs * kMaxHidden * sizeof(float)));
   CK(hipMalloc(&E.bar, 2 * sizeof(uint32_t)));
   CK(hipMemset(E.bar, 0, 2 * sizeof(uint32_t)));
   CK(hipMemset(E.done, 0, 2 * kMaxPairs * sizeof(uint32_t)));

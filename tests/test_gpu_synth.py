@@ -150,3 +150,43 @@ def test_decode_kernel_and_layer_kernel_agree_with_oracle(eng, hidden, monkeypat
     finally:
         for b in range(20):
             eng.release(b)
+
+
+@pytest.mark.parametrize("burst", [2, 4, 8])
+def test_decode_burst_rows_equal_single_token_runs(eng, burst):
+    """Bursts of all-Q4_K routed requests also run on the decode kernel: each
+    (token, pair) is a unit with its own partial, and a token's units are
+    summed in the single-token order. Every row must match the oracle and be
+    bit-identical to the same token run alone (the batching property of
+    src/native.c:94-117, which the reference checks with memcmp)."""
+    hidden, seed = 4096, 777
+    lay = oracle.layout(hidden, fa.FMT_Q4KT)
+    rng = np.random.default_rng(burst)
+    for b in range(20):
+        assert eng.synthetic(b, hidden, fa.FMT_Q4KT, 1, seed) == fa.OK
+    try:
+        experts = zipf_routes(rng, burst)
+        gates = np.zeros((burst, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, burst)
+        x = rng.standard_normal((burst, hidden)).astype(np.float32)
+        kind, grid = plan_kind(eng, 0, experts, gates, x)
+        assert kind == 1 and 0 < grid <= 256, (kind, grid)
+        print(f"decode burst={burst} grid={grid}", flush=True)
+        rc, y = eng.run(0, experts, gates, x, fa.MODE_F32)
+        assert rc == fa.OK
+        units = []
+        for b in range(20):
+            u = sparse_unit(lay)
+            for e in set(int(v) for v in experts.ravel()):
+                slice_view(u, lay, 0, e)[:] = oracle.synth_slice(lay, seed, b, 0, e)
+            units.append(u)
+        rc, ref = oracle.ref_run(units, fa.FMT_Q4KT, False, oracle_request(0, experts, gates, x))
+        assert rc == 0
+        check_close(ref, y, fa.MODE_F32, ("burst", burst))
+        for t in range(burst):
+            rc, y1 = eng.run(0, experts[t:t + 1], gates[t:t + 1], x[t:t + 1], fa.MODE_F32)
+            assert rc == fa.OK
+            assert np.array_equal(y1[0].view(np.uint32), y[t].view(np.uint32)), f"token {t} differs from its T=1 run"
+    finally:
+        for b in range(20):
+            eng.release(b)
