@@ -248,6 +248,17 @@ __device__ __forceinline__ uint32_t nib_hi(uint32_t v) {
   asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(v >> 4));
   return r;
 }
+// Bytes 2h and 2h+1 of v, each holding a nibble value q in 0..15, as two
+// floats q * 2^-9 in one conversion: an FP8 E4M3 byte below 16 is q * 2^-9
+// exactly (subnormal below 8, exponent 1 from 8 to 15, spacing 2^-9 in both).
+// Callers fold the 2^9 into a scale; a power of two commutes with rounding,
+// so the products and sums are those of the unscaled nibbles.
+constexpr float kFp8Nibble = 512.f;   // 2^9
+template <bool H>
+__device__ __forceinline__ float2 nib_pair(uint32_t v) {
+  const auto r = __builtin_amdgcn_cvt_pk_f32_fp8((int)v, H);
+  return make_float2(r[0], r[1]);
+}
 
 // Weight and plan addresses arrive as 64-bit integers, so the compiler sees
 // generic pointers and would emit FLAT loads; a FLAT load also counts against
@@ -1409,18 +1420,23 @@ __device__ __forceinline__ float neuron_h(const DecodeGuBytes& R, int c, bool ac
       const uint32_t glo = nib_lo(vg), ghi = nib_hi(vg), ulo = nib_lo(vu), uhi = nib_hi(vu);
       const float xav[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w};
       const float xbv[4] = {xb[i].x, xb[i].y, xb[i].z, xb[i].w};
+      // Nibbles as q * 2^-9 (nib_pair), two per conversion.
+      const float2 gl[2] = {nib_pair<false>(glo), nib_pair<true>(glo)}, gh[2] = {nib_pair<false>(ghi), nib_pair<true>(ghi)};
+      const float2 ul[2] = {nib_pair<false>(ulo), nib_pair<true>(ulo)}, uh[2] = {nib_pair<false>(uhi), nib_pair<true>(uhi)};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        ga[k] = fmaf(ub(glo, k), xav[k], ga[k]);
-        gb[k] = fmaf(ub(ghi, k), xbv[k], gb[k]);
-        ua[k] = fmaf(ub(ulo, k), xav[k], ua[k]);
-        ub_[k] = fmaf(ub(uhi, k), xbv[k], ub_[k]);
+        const float qgl = k & 1 ? gl[k >> 1].y : gl[k >> 1].x, qgh = k & 1 ? gh[k >> 1].y : gh[k >> 1].x;
+        const float qul = k & 1 ? ul[k >> 1].y : ul[k >> 1].x, quh = k & 1 ? uh[k >> 1].y : uh[k >> 1].x;
+        ga[k] = fmaf(qgl, xav[k], ga[k]);
+        gb[k] = fmaf(qgh, xbv[k], gb[k]);
+        ua[k] = fmaf(qul, xav[k], ua[k]);
+        ub_[k] = fmaf(quh, xbv[k], ub_[k]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-  const float g0 = (ga[0] + ga[1]) + (ga[2] + ga[3]), g1 = (gb[0] + gb[1]) + (gb[2] + gb[3]);
-  const float u0 = (ua[0] + ua[1]) + (ua[2] + ua[3]), u1 = (ub_[0] + ub_[1]) + (ub_[2] + ub_[3]);
+  const float g0 = ((ga[0] + ga[1]) + (ga[2] + ga[3])) * kFp8Nibble, g1 = ((gb[0] + gb[1]) + (gb[2] + gb[3])) * kFp8Nibble;
+  const float u0 = ((ua[0] + ua[1]) + (ua[2] + ua[3])) * kFp8Nibble, u1 = ((ub_[0] + ub_[1]) + (ub_[2] + ub_[3])) * kFp8Nibble;
   float a = (gs[0] * g0 - gm[0] * X0) + (gs[1] * g1 - gm[1] * X1);
   float u = (us[0] * u0 - um[0] * X0) + (us[1] * u1 - um[1] * X1);
   a = row_sum(active ? a : 0.f);
@@ -1476,7 +1492,7 @@ __device__ __forceinline__ void down_round(const DecodeDnBytes& R, unsigned t, u
       hdr_dm(hdr, tg, Dv[q], Mv[q], ok);
       if (tvalid && !ok) bad |= kErrScale;
       const float gh = hs[n0 + q];
-      Dv[q] *= gh;
+      Dv[q] *= gh * kFp8Nibble;   // the nibbles below are q * 2^-9
       Mv[q] *= gh;
     }
     *reinterpret_cast<float2*>(&T.D[ts][tg][n0]) = make_float2(Dv[0], Dv[1]);
@@ -1502,15 +1518,16 @@ __device__ __forceinline__ void down_round(const DecodeDnBytes& R, unsigned t, u
         // nibbles columns 0 and 2, high nibbles columns 1 and 3.
         const uint32_t v = word(dq, wd);
         const uint32_t lo = nib_lo(v), hi = nib_hi(v);
+        const float2 la = nib_pair<false>(lo), lb = nib_pair<true>(lo), ha = nib_pair<false>(hi), hb = nib_pair<true>(hi);
         const float ca = coef[2 * wd], cb = coef[2 * wd + 1];
-        s4[0] = fmaf(ub(lo, 0), ca, s4[0]);
-        s4[1] = fmaf(ub(hi, 0), ca, s4[1]);
-        s4[2] = fmaf(ub(lo, 1), ca, s4[2]);
-        s4[3] = fmaf(ub(hi, 1), ca, s4[3]);
-        s4[0] = fmaf(ub(lo, 2), cb, s4[0]);
-        s4[1] = fmaf(ub(hi, 2), cb, s4[1]);
-        s4[2] = fmaf(ub(lo, 3), cb, s4[2]);
-        s4[3] = fmaf(ub(hi, 3), cb, s4[3]);
+        s4[0] = fmaf(la.x, ca, s4[0]);
+        s4[1] = fmaf(ha.x, ca, s4[1]);
+        s4[2] = fmaf(la.y, ca, s4[2]);
+        s4[3] = fmaf(ha.y, ca, s4[3]);
+        s4[0] = fmaf(lb.x, cb, s4[0]);
+        s4[1] = fmaf(hb.x, cb, s4[1]);
+        s4[2] = fmaf(lb.y, cb, s4[2]);
+        s4[3] = fmaf(hb.y, cb, s4[3]);
       }
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) y[4 * half + cc] += s4[cc];
@@ -1640,51 +1657,59 @@ __device__ __forceinline__ unsigned decode_column(unsigned p) {
 }
 
 // Sum of a token's unit partials, 16 positions per workgroup (token =
-// blockIdx.y, units [first, first + count) of the plan's token table):
-// thread (ps, q) adds units ps, ps+128 of positions 16*blockIdx.x + 4q..4q+3
-// in fp64, then a fixed binary tree over the 128 ps; narrowing with the
-// reference's overflow rule (backends/ref.c:95) and the status word of
-// decode_kernel. A token's result depends only on its own units, in order.
-constexpr int kReduceThreads = 512;
+// blockIdx.y, units [first, first + count) of the plan's token table), in
+// fp64 and a fixed order: lane (q, ps) of wavefront w, ps = 16w + l/4, adds
+// units ps, ps+64, ps+128, ps+192 of positions 16*blockIdx.x + 4q..4q+3 in
+// that order (its four loads are in flight together), a butterfly over the
+// 16 ps of each wavefront combines them, and wavefront 0 adds the four
+// wavefronts' sums in order. Narrowing follows the reference's overflow rule
+// (backends/ref.c:95); the status word is decode_kernel's. A token's result
+// depends only on its own units, in order.
+constexpr int kReduceThreads = 256;
 constexpr int kReducePositions = 16;
+constexpr unsigned kReduceLanes = kReduceThreads / (kReducePositions / 4);   // 64 partial lanes
+constexpr unsigned kReduceDepth = 4;                                          // units per partial lane
+__device__ __forceinline__ double xor_d(double v, int m) {
+  const int lo = __shfl_xor((int)(uint32_t)__double_as_longlong(v), m);
+  const int hi = __shfl_xor((int)(uint32_t)((uint64_t)__double_as_longlong(v) >> 32), m);
+  return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
 __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
   const DecodeToken tk = reinterpret_cast<const DecodeToken*>(plan + H.groups_off)[blockIdx.y];
   uint32_t* status = S.out + (size_t)S.parity * S.out_words;
   float* yout = reinterpret_cast<float*>(status + 4) + (size_t)blockIdx.y * H.hidden;
-  constexpr unsigned kLanes = kReduceThreads / (kReducePositions / 4);   // partial lanes
-  const unsigned tid = threadIdx.x, q = tid & 3, ps = tid >> 2;
+  const unsigned tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane & 3;
+  const unsigned ps = 16 * wave + (lane >> 2);
   const unsigned p0 = kReducePositions * blockIdx.x + 4 * q;
-  double v[4] = {0.0, 0.0, 0.0, 0.0};
-  float4 r[2];
+  float4 r[kReduceDepth];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const unsigned g = ps + kLanes * k;
+  for (unsigned k = 0; k < kReduceDepth; ++k) {
+    const unsigned g = ps + kReduceLanes * k;
     r[k] = g < tk.count ? *reinterpret_cast<const float4*>(S.wgpart + (size_t)(tk.first + g) * kMaxHidden + p0)
                         : make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  double v[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
+  for (unsigned k = 0; k < kReduceDepth; ++k) {
     v[0] += (double)r[k].x;
     v[1] += (double)r[k].y;
     v[2] += (double)r[k].z;
     v[3] += (double)r[k].w;
   }
-  __shared__ double red[kLanes][kReducePositions + 1];
 #pragma unroll
-  for (int cc = 0; cc < 4; ++cc) red[ps][4 * q + cc] = v[cc];
+  for (int m = 4; m < 64; m <<= 1)
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) v[cc] += xor_d(v[cc], m);
+  __shared__ double red[kReduceThreads / 64][kReducePositions];
+  if (lane < 4)
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) red[wave][4 * q + cc] = v[cc];
   __syncthreads();
-#pragma unroll
-  for (unsigned stride = kLanes / 2; stride > 0; stride >>= 1) {
-    if (ps < stride)
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc) red[ps][4 * q + cc] += red[ps + stride][4 * q + cc];
-    __syncthreads();
-  }
   if (tid < kReducePositions) {
+    const double t = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
     const unsigned col = decode_column(kReducePositions * blockIdx.x + tid);
     if (col < H.hidden) {
-      const double t = red[0][tid];
       float f = 0.f;
       if (!isfinite(t) || fabs(t) > (double)FLT_MAX) flag(status, kErrRange);
       else f = (float)t;
@@ -1692,7 +1717,8 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
     }
   }
 }
-static_assert(kDecodeUnitsPerToken <= 2 * (kReduceThreads / (kReducePositions / 4)), "two partials per reduce lane");
+static_assert(kDecodeUnitsPerToken <= kReduceDepth * kReduceLanes, "units per token within the reduce's lanes");
+static_assert(kReduceThreads == 256, "the final sum adds four wavefronts");
 
 // ------------------------------------------------------- load re-tiling
 //
