@@ -59,7 +59,10 @@ constexpr uint32_t kErrScale = 1;     // referenced non-finite scale
 constexpr uint32_t kErrRange = 2;     // a, u, h or y outside fp32
 constexpr uint32_t kErrTimeout = 4;   // dependency wait exceeded its bound
 
-enum : uint8_t { TQ4_0 = 2, TQ8_0 = 8, TQ4_K = 12, TMXFP4 = 39, TQ4_KT = 140 };
+enum : uint8_t { TQ4_0 = 2, TQ8_0 = 8, TQ4_K = 12, TMXFP4 = 39, TQ4_KT = 140, TQ4_KM = 141 };
+// TQ4_KM: the routed Q4_K gate/up rows of a pair in matrix-core tiles (see
+// the re-tiled layouts); it decodes as TQ4_K once loaded.
+template <int GU> constexpr int kAs = GU == TQ4_KM ? TQ4_K : GU;
 enum { MODE_F32 = 0, MODE_F64 = 1, MODE_Q8 = 2 };
 
 struct PairDesc {            // one (expert, block) slice of the request
@@ -328,6 +331,16 @@ __device__ __forceinline__ void q8_regs64(float4* x4) {
 //  Q4_0 : [2 parts][nch][16 B] nibbles, then [nch][2 x fp16] scales.
 // Lane c reads its 64 columns with 16-byte loads; 64 lanes read contiguous
 // 1 KB runs. Same byte count as the native row (the permutation is lossless).
+//
+// Q4_K gate/up of the transposed-down format (TQ4_KM), the 64 rows of a pair
+// together: row-block rb (0..3) holds rows i = 0..7 gate and 8..15 up of
+// neurons 8rb + i%8. Per super-block sb: [4 rb][16 rows][16 B] headers
+// (1 KB), then [4 rb][2 parts][64 lanes][16 B] nibbles (8 KB). Lane
+// l = 16kg + i of part p holds sub-block 4p + kg of row i: its 32 values in
+// 4 words, word u having positions 8u..8u+3 in the low nibbles of its bytes
+// and 8u+4..8u+7 in the high nibbles. Lane l of part p is then the int8 A
+// operand of two 16x16x64 matrix products (row i, k = 16kg..16kg+15) once
+// each word is split into its low and high nibbles.
 
 // Decode the lane's 64 columns of a gate/up row exactly as the reference
 // decodes each weight (src/native.c:13-31, src/q4.c:29-31). Used by the
@@ -357,6 +370,35 @@ __device__ __forceinline__ void load_raw(const uint8_t* row, int nch, int c, Lan
     r.q[1] = ld16(row + 16 * nch + 16 * c);
     r.h.x = gld<uint32_t>(row + 32 * nch + 4 * c);
   }
+}
+
+// Row (k = 0 gate, 1 up; neuron n) of a TQ4_KM pair, lane chunk c, in the
+// TQ4_K lane form of load_raw: the two 16-byte sub-block runs of chunk c are
+// merged back into the reference's 32-byte chunk (byte i: low nibble position
+// i of the first sub-block, high nibble position i of the second).
+__device__ __forceinline__ void load_km(const uint8_t* slice, int k, unsigned n, int c, LaneRaw& r) {
+  const unsigned sb = (unsigned)c >> 2, rb = n >> 3, i = 8 * k + (n & 7), s0 = 2 * ((unsigned)c & 3);
+  const uint8_t* blk = slice + 9216 * sb;
+  r.h = ld16(blk + 16 * (16 * rb + i));
+  const uint8_t* nib = blk + 1024 + 2048 * rb + 1024 * (s0 >> 2) + 16 * i;
+  const uint4 a = ld16(nib + 16 * 16 * (s0 & 3)), b = ld16(nib + 16 * 16 * ((s0 & 3) + 1));
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+  uint32_t o[8];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    o[2 * u] = (aw[u] & 0x0f0f0f0fu) | ((bw[u] & 0x0f0f0f0fu) << 4);
+    o[2 * u + 1] = ((aw[u] >> 4) & 0x0f0f0f0fu) | (bw[u] & 0xf0f0f0f0u);
+  }
+  r.q[0] = make_uint4(o[0], o[1], o[2], o[3]);
+  r.q[1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// Gate (k = 0) or up row of neuron n of a pair for lane chunk c.
+template <int GU>
+__device__ __forceinline__ void load_gu_row(uint64_t slice, uint32_t proj, int k, unsigned n, int nch, int c,
+                                            LaneRaw& r) {
+  if (GU == TQ4_KM) load_km(reinterpret_cast<const uint8_t*>(slice), k, n, c, r);
+  else load_raw<GU>(reinterpret_cast<const uint8_t*>(slice) + (k ? proj : 0) + (size_t)n * (proj / kNeurons), nch, c, r);
 }
 
 // Scale factors of the raw row for the fp32 path; false on a bad scale.
@@ -593,14 +635,12 @@ __device__ __forceinline__ uint32_t phase_a_single(const PlanHeader& H, const Sc
   const int lane = threadIdx.x & 63;
   const bool active = lane < (int)nch;
   const int c = active ? lane : 0;
-  const uint32_t row_bytes = proj / kNeurons;
   LaneRaw raw[2 * kWaveNeurons];
 #pragma unroll
   for (int k = 0; k < kWaveNeurons; ++k)
 #pragma unroll
     for (int r = 0; r < 2; ++r)
-      load_raw<GU>(reinterpret_cast<const uint8_t*>(slice) + (r ? proj : 0) + (size_t)(n0 + k) * row_bytes, nch, c,
-                   raw[2 * k + r]);
+      load_gu_row<GU>(slice, proj, r, n0 + k, nch, c, raw[2 * k + r]);
   float4 x[16];
   {
     const float4* xs = reinterpret_cast<const float4*>(xg + 64 * c);
@@ -609,7 +649,7 @@ __device__ __forceinline__ uint32_t phase_a_single(const PlanHeader& H, const Sc
   }
   if (MODE == MODE_Q8) q8_regs64(x);  // the lane chunk is one 64-group
   float X0 = 0.f, X1 = 0.f;
-  if (MODE == MODE_F32 && (GU == TQ4_K || GU == TQ4_0)) {
+  if (MODE == MODE_F32 && (kAs<GU> == TQ4_K || GU == TQ4_0)) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       X0 += (x[i].x + x[i].y) + (x[i].z + x[i].w);
@@ -625,13 +665,13 @@ __device__ __forceinline__ uint32_t phase_a_single(const PlanHeader& H, const Sc
       const LaneRaw& rr = raw[2 * k + r];
       if (MODE == MODE_F32) {
         float sc[2], mn[2];
-        bool ok = raw_scales<GU>(rr, c, sc, mn);
+        bool ok = raw_scales<kAs<GU>>(rr, c, sc, mn);
         if (active && !ok) bad |= kErrScale;
-        float part = lane_dot_f32<GU>(rr, sc, mn, x, X0, X1);
+        float part = lane_dot_f32<kAs<GU>>(rr, sc, mn, x, X0, X1);
         au[r] = wave_total(active ? part : 0.f);
       } else {
         float w[64];
-        bool ok = decode_raw<GU>(rr, c, w);
+        bool ok = decode_raw<kAs<GU>>(rr, c, w);
         if (active && !ok) bad |= kErrScale;
         double acc = 0.0;
 #pragma unroll
@@ -660,13 +700,12 @@ __device__ __forceinline__ uint32_t phase_a_tile(const PlanHeader& H, const Scra
   const int lane = threadIdx.x & 63;
   const bool active = lane < (int)nch;
   const int c = active ? lane : 0;
-  const uint32_t row_bytes = proj / kNeurons;
   uint32_t bad = 0;
   float X0[BT], X1[BT];
 #pragma unroll
   for (int t = 0; t < BT; ++t) {
     X0[t] = X1[t] = 0.f;
-    if (MODE == MODE_F32 && (GU == TQ4_K || GU == TQ4_0) && t < (int)tc) {
+    if (MODE == MODE_F32 && (kAs<GU> == TQ4_K || GU == TQ4_0) && t < (int)tc) {
       const float4* x = reinterpret_cast<const float4*>(lds + t * hidden + 64 * c);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -681,8 +720,7 @@ __device__ __forceinline__ uint32_t phase_a_tile(const PlanHeader& H, const Scra
   for (int k = 0; k < kWaveNeurons; ++k)
 #pragma unroll
     for (int r = 0; r < 2; ++r)
-      load_raw<GU>(reinterpret_cast<const uint8_t*>(slice) + (r ? proj : 0) + (size_t)(n0 + k) * row_bytes, nch, c,
-                   raw[2 * k + r]);
+      load_gu_row<GU>(slice, proj, r, n0 + k, nch, c, raw[2 * k + r]);
 #pragma unroll
   for (int k = 0; k < kWaveNeurons; ++k) {
     float au[2][BT];
@@ -691,18 +729,18 @@ __device__ __forceinline__ uint32_t phase_a_tile(const PlanHeader& H, const Scra
       const LaneRaw& rr = raw[2 * k + r];
       if (MODE == MODE_F32) {
         float sc[2], mn[2];
-        bool ok = raw_scales<GU>(rr, c, sc, mn);
+        bool ok = raw_scales<kAs<GU>>(rr, c, sc, mn);
         if (active && !ok) bad |= kErrScale;
 #pragma unroll
         for (int t = 0; t < BT; ++t) {
           float part = 0.f;
           if (active && t < (int)tc)
-            part = lane_dot_f32<GU>(rr, sc, mn, reinterpret_cast<const float4*>(lds + t * hidden + 64 * c), X0[t], X1[t]);
+            part = lane_dot_f32<kAs<GU>>(rr, sc, mn, reinterpret_cast<const float4*>(lds + t * hidden + 64 * c), X0[t], X1[t]);
           au[r][t] = wave_total(part);
         }
       } else {
         float w[64];
-        bool ok = decode_raw<GU>(rr, c, w);
+        bool ok = decode_raw<kAs<GU>>(rr, c, w);
         if (active && !ok) bad |= kErrScale;
 #pragma unroll
         for (int t = 0; t < BT; ++t) {
@@ -743,6 +781,7 @@ __device__ void phase_a(const PlanHeader& H, const uint8_t* plan, const Scratch&
   if (BT == 1) {
     switch (gu) {
       case TQ4_K: bad = phase_a_single<MODE, TQ4_K>(H, S, p, n0, slice, proj, xg); break;
+      case TQ4_KM: bad = phase_a_single<MODE, TQ4_KM>(H, S, p, n0, slice, proj, xg); break;
       case TQ8_0: bad = phase_a_single<MODE, TQ8_0>(H, S, p, n0, slice, proj, xg); break;
       case TMXFP4: bad = phase_a_single<MODE, TMXFP4>(H, S, p, n0, slice, proj, xg); break;
       default: bad = phase_a_single<MODE, TQ4_0>(H, S, p, n0, slice, proj, xg); break;
@@ -763,6 +802,7 @@ __device__ void phase_a(const PlanHeader& H, const uint8_t* plan, const Scratch&
       }
       switch (gu) {
         case TQ4_K: bad |= phase_a_tile<MODE, BT, TQ4_K>(H, S, p, n0, slice, proj, tmask, t0, tc, lds); break;
+        case TQ4_KM: bad |= phase_a_tile<MODE, BT, TQ4_KM>(H, S, p, n0, slice, proj, tmask, t0, tc, lds); break;
         case TQ8_0: bad |= phase_a_tile<MODE, BT, TQ8_0>(H, S, p, n0, slice, proj, tmask, t0, tc, lds); break;
         case TMXFP4: bad |= phase_a_tile<MODE, BT, TMXFP4>(H, S, p, n0, slice, proj, tmask, t0, tc, lds); break;
         default: bad |= phase_a_tile<MODE, BT, TQ4_0>(H, S, p, n0, slice, proj, tmask, t0, tc, lds); break;
@@ -1267,39 +1307,49 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(const uint8_t* __restri
 
 // ------------------------------------------------------------ decode kernel
 //
-// Single token, every pair routed Q4_K with the transposed Q4_K down (the
-// down rows are per neuron): one workgroup of 8 wavefronts per (expert,
-// block) pair (pairs b, b+G, ...), so that no h crosses workgroups. A pair is
-// processed in 4 rounds of 8 neurons. In round t, wavefront w computes gate
-// and up of neuron 8(t%4) + w in fp32 (this kernel serves the F32 mode only),
-// h = SiLU(a)*u in fp32 (backends/ref.c:82-83), and publishes gate*h in LDS
-// with a counter; it then applies the down projection of round t-1's 8
-// neurons, whose h the other wavefronts published a round earlier, to
-// super-blocks 2w and 2w+1 (outputs 512w..512w+511), accumulating an fp32
-// partial over all outputs in registers. No barrier separates the rounds:
-// a wavefront waits only for a counter, which is normally complete. A second
-// small kernel on the same stream, decode_reduce, sums the workgroup partials
-// in workgroup order: the kernel boundary is the global barrier and makes the
-// partials visible across XCDs, which in-kernel coherent stores, counters and
-// polling would do at about 2 us per hop.
+// F32 mode, every pair routed Q4_K (TQ4_KM tiles) with the transposed Q4_K
+// down: one workgroup of 8 wavefronts per unit, a (token, pair) of the
+// request (units b, b+G, ...), so that no h crosses workgroups.
 //
-// Every lane loads exactly the bytes it uses into registers, with the
-// non-temporal policy: a round's gate/up bytes one round ahead of its h, its
-// down bytes together with the next round's gate/up bytes, one round ahead of
-// its down projection. Only x and round 0's gate/up bytes are requested
-// before the first h, so that they arrive early. The rounds of a pair are
-// unrolled, so each round's bytes have registers of their own and the
-// compiler's waits are exact. LDS holds x (read back per neuron), h, the
-// down headers and the down coefficients.
+// Gate and up run on the matrix cores, exactly in integers. Each value of x
+// is written as four signed 8-bit digits over a power of two per 32-value
+// sub-block, x = 2^e (2^24 d0 + 2^16 d1 + 2^8 d2 + d3) with |x| 2^-e < 2^30
+// (31 bits relative to the sub-block's largest value, below fp32 rounding:
+// a staging error is the same for every row, so it adds up coherently in y).
+// One 16x16x64 int8 product takes 16 rows (gate and up of 8 neurons), 16
+// values of each of 4 sub-blocks as k, and 16 columns (sub-block, digit); columns whose
+// sub-block is not that of the k range are zero, so that after the two
+// products of a group C[row][(s, d)] is the exact integer dot of row and
+// digit d over sub-block s. Each lane then scales its 4 values by
+// d*sc (fp32, as the reference forms it, src/native.c:14-19) times 2^e
+// times the digit's weight and adds them to its row sums; the min term is
+// dmin*m times the fp32 sum of the sub-block's x. Wavefront w owns
+// super-blocks 2w and 2w+1 of every row.
+//
+// A unit is processed in 4 rounds, one row-block (8 neurons) each: the
+// round's row sums meet in LDS behind a barrier, and every wavefront forms
+// the round's 8 h = SiLU(a)*u in fp32 (backends/ref.c:82-83) itself. The
+// down projection is the fp32 one, one round late: each wavefront builds
+// d*sc*gate*h and dmin*m*gate*h of the round's neurons for its two
+// super-blocks of outputs (512w..512w+511) and accumulates 8 outputs per
+// lane. A second small kernel on the same stream, decode_reduce, sums the
+// unit partials in unit order: the kernel boundary is the global barrier and
+// makes the partials visible across XCDs.
+//
+// Every lane loads the bytes it uses into registers with the non-temporal
+// policy, one round ahead: round r+1's gate/up and down bytes during round r
+// (the next unit's headers and first round during round 3). One round in
+// flight (about 55 KB per workgroup) streams at the measured ceiling; two
+// rounds in flight stream more slowly.
 
-// The weight loads are raw buffer loads with the non-temporal policy: the
-// pair's slice is a buffer resource in scalar registers (bounded by the
-// slice's bytes, so that an offset past it reads zeros), the per-lane part of
-// each offset is computed once, the per-round part is a scalar offset. No
-// 64-bit address arithmetic per load, and the loads count in vmcnt only.
+// The weight loads are raw buffer loads: the pair's slice is a buffer
+// resource in scalar registers (bounded by the slice's bytes, so that an
+// offset past it reads zeros), the per-lane part of each offset is computed
+// once, the per-load part is a scalar offset. No 64-bit address arithmetic
+// per load, and the loads count in vmcnt only.
 struct PairBuf {
   __amdgpu_buffer_rsrc_t rsrc;         // the pair's slice
-  uint32_t proj, row;                  // bytes of the 32 gate rows (= up offset), of one row
+  uint32_t proj;                       // bytes of the 32 gate rows (= up offset)
   float gate;                          // the token's expert weight
   uint32_t token;                      // the unit's token
 };
@@ -1307,32 +1357,41 @@ struct PairBuf {
 // workgroup at a time), and the compiler must know it, or it would wrap every
 // buffer load in a loop over distinct resource values.
 __device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ PairBuf pair_buf(const PairDesc& P) {
+// Plan reads through the constant address space: the plan is read-only
+// while the kernel runs, so they become scalar loads, which count in the
+// scalar counter. A vector load of a descriptor would make its wait also
+// wait for every weight load issued before it.
+__device__ __forceinline__ uint32_t plan_read(const uint32_t* p) {
+  return *(const __attribute__((address_space(4))) uint32_t*)p;
+}
+template <class T>
+__device__ __forceinline__ uint32_t plan_field(const T* base, size_t offset) {
+  return plan_read(reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(base) + offset));
+}
+// The descriptor's words are read whole (the token is the top byte of the
+// word of its four byte fields): scalar loads have no byte form.
+// With `live` false the resource has no records: its loads return zeros
+// without a memory access (the requests past a workgroup's last unit).
+__device__ __forceinline__ PairBuf pair_buf(const PairDesc* P, bool live = true) {
+  static_assert(offsetof(PairDesc, gu) == 12 && offsetof(PairDesc, pad) == 15, "descriptor word 3");
   PairBuf B;
-  const uint64_t slice = P.slice;
-  const uint64_t base = ((uint64_t)uniform((uint32_t)(slice >> 32)) << 32) | uniform((uint32_t)slice);
-  B.token = uniform(P.pad);
-  B.proj = uniform(P.proj);
-  B.row = B.proj / kNeurons;
-  B.gate = __uint_as_float(uniform(__float_as_uint(P.gate[0])));
-  B.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), (short)0, (int)(3 * B.proj), 0x00020000);
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(P);
+  const uint64_t base = ((uint64_t)uniform(plan_read(w + 1)) << 32) | uniform(plan_read(w));
+  B.token = uniform(plan_read(w + 3)) >> 24;
+  B.proj = uniform(plan_read(w + 2));
+  B.gate = __uint_as_float(uniform(plan_read(reinterpret_cast<const uint32_t*>(P->gate))));
+  B.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), (short)0, live ? (int)(3 * B.proj) : 0,
+                                              0x00020000);
   return B;
 }
 __device__ __forceinline__ uint4 bld(const PairBuf& B, uint32_t voff, uint32_t soff) {
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(B.rsrc, (int)voff, (int)soff, 2);   // 2: nt
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
-// Per-lane offsets of the loads, fixed for the kernel.
-struct LaneOffsets {
-  uint32_t q0, q1, gh;                 // gate/up row: parts 0 and 1 of chunk c, header of super-block c/4
-  uint32_t dq, dh;                     // down matrix: nibbles of super-block 2w + l/32, header of
-                                       // super-block 2w + (l%16)/8 and neuron l%8 (clamped super-blocks)
-};
 
-struct DecodeGuBytes {                 // one lane's gate/up bytes of one round
-  uint4 gq[2][2];                      // [gate, up][part]: nibbles of chunk c of neuron 8r + w
-  uint4 gh[2];                         // [gate, up]: header of super-block c/4
-};
+constexpr int kSubBlocks = kMaxHidden / 32;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
 struct DecodeDnBytes {                 // one lane's down bytes of one round
   uint4 dq[2];                         // nibbles: super-block 2w + l/32, neurons 8r..8r+7,
                                        // outputs 8j..8j+3 and 8j+4..8j+7 (j = l%32)
@@ -1343,33 +1402,150 @@ struct DecodeTable {                   // one wavefront's down coefficients of o
   float M[2][8][8];                    // dmin*mi*gate*h
 };
 struct DecodeLds {
-  float4 x[kMaxBurst][16][64];         // [token][k][lane c] = x[64c + 4k .. 64c + 4k + 3]
-  uint4 dh[kDecodeWaves][16];          // [wave][super-block 2w + i/8, neuron 8r + i%8]
+  int8_t xd[2][4][kSubBlocks][32];           // [unit parity][digit][sub-block][value]: x of the unit's token
+  float xf[2][kSubBlocks];                   // 2^e of each sub-block
+  float xs[2][kSubBlocks];                   // fp32 sum of each sub-block's values
+  float dsc[kDecodeWaves][16][64];           // [wave][sub-block of its super-blocks][row] d*sc
+  float rowp[2][kDecodeWaves][64];           // [unit parity][wave][row] scaled integer dots
+  float minp[2][kDecodeWaves][64];           // [unit parity][wave][row] min terms
+  float h[kDecodeWaves][8];                  // gate*h of the round (each wavefront's own copy)
+  uint4 dh[kDecodeWaves][16];                // [wave][super-block 2w + i/8, neuron 8r + i%8]
   DecodeTable table[kDecodeWaves];
-  float h[4][8];                       // gate*h of round t's 8 neurons in slot t%4
-  uint32_t published[4];               // h values written to slot s, over all pairs
-  uint32_t consumed[4];                // wavefronts past their reads of slot s, over all pairs
 };
+static_assert(sizeof(DecodeLds) <= 160 * 1024, "decode LDS");
 
-// Round r, gate/up part: gate and up rows of neuron 8r + w (kGuLoads loads).
-constexpr int kGuLoads = 6;
-__device__ __forceinline__ void load_gu(const PairBuf& B, unsigned r, int wave, const LaneOffsets& o,
-                                        DecodeGuBytes& R) {
-  const uint32_t n = 8 * r + (unsigned)wave;
+// Round (row-block) rb of the unit's gate/up nibbles for this wavefront's
+// super-blocks 2w, 2w+1: [super-block][part], lane l's 16 bytes.
+struct DecodeNib {
+  uint4 q[2][2];
+};
+// sb0, sb1 are clamped to the matrix by the caller; every load is issued,
+// so that the compiler's waits count all of them.
+__device__ __forceinline__ void load_nib(const PairBuf& B, unsigned rb, unsigned sb0, unsigned sb1, int lane,
+                                         DecodeNib& N) {
+  const uint32_t v = 16 * (uint32_t)lane;
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const uint32_t base = (k ? B.proj : 0) + n * B.row;
-    R.gq[k][0] = bld(B, o.q0, base);
-    R.gq[k][1] = bld(B, o.q1, base);
-    R.gh[k] = bld(B, o.gh, base);
+  for (int sbl = 0; sbl < 2; ++sbl)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) N.q[sbl][p] = bld(B, v, 9216 * (sbl ? sb1 : sb0) + 1024 + 2048 * rb + 1024 * p);
+}
+// Headers of super-block sb: lane l holds row l (row-block l/16, row l%16).
+__device__ __forceinline__ uint4 load_hdr(const PairBuf& B, unsigned sb, int lane) {
+  return bld(B, 16 * (uint32_t)lane, 9216 * sb);
+}
+// Round r of the down matrix: the lane's nibbles of neurons 8r..8r+7 and one
+// header (dq: 4608 * super-block + 32 * (l%32); dh: + 4096 + 16 * (l%8)).
+__device__ __forceinline__ void load_dn(const PairBuf& B, unsigned r, uint32_t dq, uint32_t dh, DecodeDnBytes& R) {
+  const uint32_t base = 2 * B.proj;
+  R.dq[0] = bld(B, dq, base + 1024 * r);
+  R.dq[1] = bld(B, dq + 16, base + 1024 * r);
+  R.dh = bld(B, dh, base + 128 * r);
+}
+
+// x of a token into digits in slot `slot` (thread: sub-block tid/4, values
+// 8*(tid%4)..+7, from v). The four threads of a sub-block agree on its
+// largest magnitude and sum through butterflies within their quad.
+__device__ __forceinline__ void stage_x(const float4 (&v4)[2], unsigned slot, unsigned nsub, bool routed,
+                                        DecodeLds& L, uint32_t& bad) {
+  const unsigned tid = threadIdx.x, s = tid >> 2, q = tid & 3;
+  const float v[8] = {v4[0].x, v4[0].y, v4[0].z, v4[0].w, v4[1].x, v4[1].y, v4[1].z, v4[1].w};
+  float m = 0.f;
+  uint32_t fin = 1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    m = fmaxf(m, fabsf(v[i]));
+    fin &= isfinite(v[i]) ? 1u : 0u;
+  }
+  float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  m = fmaxf(m, __shfl_xor(m, 1));
+  m = fmaxf(m, __shfl_xor(m, 2));
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  fin &= (uint32_t)__shfl_xor((int)fin, 1);
+  fin &= (uint32_t)__shfl_xor((int)fin, 2);
+  if (!fin && routed && s < nsub) bad |= kErrRange;   // a non-finite x makes every a of the token non-finite
+  int E = 0;
+  if (m > 0.f) (void)frexpf(m, &E);                  // m < 2^E
+  const int e = max(E - 30, -149);
+  uint32_t w[4][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}, {0u, 0u}};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int X = fin ? (int)rintf(ldexpf(v[i], -e)) : 0;   // |X| <= 2^30
+    const int d3 = ((X + 128) & 255) - 128, X1 = (X - d3) >> 8;
+    const int d2 = ((X1 + 128) & 255) - 128, X2 = (X1 - d2) >> 8;
+    const int d1 = ((X2 + 128) & 255) - 128, d0 = (X2 - d1) >> 8;   // |d0| <= 65
+    w[0][i >> 2] |= (uint32_t)(d0 & 255) << (8 * (i & 3));
+    w[1][i >> 2] |= (uint32_t)(d1 & 255) << (8 * (i & 3));
+    w[2][i >> 2] |= (uint32_t)(d2 & 255) << (8 * (i & 3));
+    w[3][i >> 2] |= (uint32_t)(d3 & 255) << (8 * (i & 3));
+  }
+  if (s < nsub) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) *reinterpret_cast<uint2*>(&L.xd[slot][d][s][8 * q]) = make_uint2(w[d][0], w[d][1]);
+    if (q == 0) {
+      L.xf[slot][s] = ldexpf(1.f, e);
+      L.xs[slot][s] = sum;
+    }
   }
 }
-// Round r, down part: the lane's nibbles of neurons 8r..8r+7 and one header.
-__device__ __forceinline__ void load_dn(const PairBuf& B, unsigned r, const LaneOffsets& o, DecodeDnBytes& R) {
-  const uint32_t base = 2 * B.proj;
-  R.dq[0] = bld(B, o.dq, base + 1024 * r);
-  R.dq[1] = bld(B, o.dq + 16, base + 1024 * r);
-  R.dh = bld(B, o.dh, base + 128 * r);
+
+// Headers of super-block sb (sbl = sb - 2w) into this wavefront's d*sc
+// table; returns the row's min term over the super-block.
+__device__ __forceinline__ float header_pass(const uint4& h, unsigned sb, unsigned sbl, unsigned t, int wave, int lane,
+                                             DecodeLds& L, uint32_t& bad) {
+  if (half_bad(h.x) || half_bad(h.x >> 16)) bad |= kErrScale;
+  const float d = half_to_float(h.x & 0xffff), dm = half_to_float(h.x >> 16);
+  float mins = 0.f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    uint32_t sc, mi;
+    q4k_scale_min(h.y, h.z, h.w, (uint32_t)g, sc, mi);
+    L.dsc[wave][8 * sbl + g][lane] = d * (float)sc;
+    mins += (dm * (float)mi) * L.xs[t][8 * sb + g];   // t: the x slot
+  }
+  return mins;
+}
+
+// The x operands of super-block sb (x slot t): lane (kg = l/16, column
+// j = l%16 = 4 * sub-block + digit) holds digit j%4 of values 16hh..16hh+15
+// of sub-block 4G + kg for product m = 2G + hh when its column's sub-block
+// is kg, zero otherwise; fx[G] = 2^e * digit weight of its column's sub-block.
+__device__ __forceinline__ void x_operands(unsigned t, unsigned sb, int lane, const DecodeLds& L, i32x4 (&b)[4],
+                                           float (&fx)[2]) {
+  const unsigned kg = (unsigned)lane >> 4, j = (unsigned)lane & 15, js = j >> 2, jd = j & 3;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const unsigned G = (unsigned)m >> 1, hh = (unsigned)m & 1;
+    const i32x4 z = {0, 0, 0, 0};
+    b[m] = js == kg ? *reinterpret_cast<const i32x4*>(&L.xd[t][jd][8 * sb + 4 * G + kg][16 * hh]) : z;
+  }
+  const float wd = jd == 0 ? 16777216.f : jd == 1 ? 65536.f : jd == 2 ? 256.f : 1.f;
+#pragma unroll
+  for (int G = 0; G < 2; ++G) fx[G] = L.xf[t][8 * sb + 4 * G + js] * wd;
+}
+
+// Row-block rb of super-block 2w + sbl: two products per group of four
+// sub-blocks, then each lane's four values scaled into acc (rows 4kg..4kg+3).
+__device__ __forceinline__ void rb_products(const uint4 (&q)[2], const i32x4 (&b)[4], const float (&fx)[2],
+                                            unsigned sbl, unsigned rb, int wave, int lane, const DecodeLds& L,
+                                            float (&acc)[4]) {
+  const unsigned kg = (unsigned)lane >> 4, js = ((unsigned)lane & 15) >> 2;
+#pragma unroll
+  for (int G = 0; G < 2; ++G) {
+    const uint4 w = q[G];
+    i32x4 c = {0, 0, 0, 0};
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const uint32_t w0 = hh ? w.z : w.x, w1 = hh ? w.w : w.y;
+      const i32x4 a = {(int)nib_lo(w0), (int)nib_hi(w0), (int)nib_lo(w1), (int)nib_hi(w1)};
+      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[2 * G + hh], c, 0, 0, 0);
+    }
+    const float4 ds = *reinterpret_cast<const float4*>(&L.dsc[wave][8 * sbl + 4 * G + js][16 * rb + 4 * kg]);
+    acc[0] = fmaf((float)c[0], ds.x * fx[G], acc[0]);
+    acc[1] = fmaf((float)c[1], ds.y * fx[G], acc[1]);
+    acc[2] = fmaf((float)c[2], ds.z * fx[G], acc[2]);
+    acc[3] = fmaf((float)c[3], ds.w * fx[G], acc[3]);
+  }
 }
 
 // SiLU(a)*u in fp32 with the stable sigmoid form; a, u or h outside fp32
@@ -1386,98 +1562,10 @@ __device__ __forceinline__ float silu_mul_f32(float a, float u, uint32_t& bad) {
   return h;
 }
 
-// h of the round's neuron from its gate and up rows. The gate and up dots
-// share each x value (read from LDS in two halves of 8 float4, so that only
-// half of the lane's x is in registers at once) and run as 16 independent
-// FMA chains; the two sums are reduced side by side.
-__device__ __forceinline__ float neuron_h(const DecodeGuBytes& R, int c, bool active, const float4 (&xl)[16][64],
-                                          float X0, float X1, uint32_t& bad) {
-  LaneRaw rg, ru;
-  rg.q[0] = R.gq[0][0];
-  rg.q[1] = R.gq[0][1];
-  rg.h = R.gh[0];
-  ru.q[0] = R.gq[1][0];
-  ru.q[1] = R.gq[1][1];
-  ru.h = R.gh[1];
-  float gs[2], gm[2], us[2], um[2];
-  const bool ok = raw_scales<TQ4_K>(rg, c, gs, gm) & raw_scales<TQ4_K>(ru, c, us, um);
-  if (active && !ok) bad |= kErrScale;
-  // Byte i of the 32-byte chunk: column i (low nibble, group A), 32+i (high, group B).
-  float ga[4] = {0.f, 0.f, 0.f, 0.f}, gb[4] = {0.f, 0.f, 0.f, 0.f};
-  float ua[4] = {0.f, 0.f, 0.f, 0.f}, ub_[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int hlf = 0; hlf < 2; ++hlf) {
-    float4 xa[4], xb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      xa[i] = xl[4 * hlf + i][c];
-      xb[i] = xl[8 + 4 * hlf + i][c];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int wi = 4 * hlf + i;
-      const uint32_t vg = word(rg.q[wi >> 2], wi & 3), vu = word(ru.q[wi >> 2], wi & 3);
-      const uint32_t glo = nib_lo(vg), ghi = nib_hi(vg), ulo = nib_lo(vu), uhi = nib_hi(vu);
-      const float xav[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w};
-      const float xbv[4] = {xb[i].x, xb[i].y, xb[i].z, xb[i].w};
-      // Nibbles as q * 2^-9 (nib_pair), two per conversion.
-      const float2 gl[2] = {nib_pair<false>(glo), nib_pair<true>(glo)}, gh[2] = {nib_pair<false>(ghi), nib_pair<true>(ghi)};
-      const float2 ul[2] = {nib_pair<false>(ulo), nib_pair<true>(ulo)}, uh[2] = {nib_pair<false>(uhi), nib_pair<true>(uhi)};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float qgl = k & 1 ? gl[k >> 1].y : gl[k >> 1].x, qgh = k & 1 ? gh[k >> 1].y : gh[k >> 1].x;
-        const float qul = k & 1 ? ul[k >> 1].y : ul[k >> 1].x, quh = k & 1 ? uh[k >> 1].y : uh[k >> 1].x;
-        ga[k] = fmaf(qgl, xav[k], ga[k]);
-        gb[k] = fmaf(qgh, xbv[k], gb[k]);
-        ua[k] = fmaf(qul, xav[k], ua[k]);
-        ub_[k] = fmaf(quh, xbv[k], ub_[k]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  const float g0 = ((ga[0] + ga[1]) + (ga[2] + ga[3])) * kFp8Nibble, g1 = ((gb[0] + gb[1]) + (gb[2] + gb[3])) * kFp8Nibble;
-  const float u0 = ((ua[0] + ua[1]) + (ua[2] + ua[3])) * kFp8Nibble, u1 = ((ub_[0] + ub_[1]) + (ub_[2] + ub_[3])) * kFp8Nibble;
-  float a = (gs[0] * g0 - gm[0] * X0) + (gs[1] * g1 - gm[1] * X1);
-  float u = (us[0] * u0 - um[0] * X0) + (us[1] * u1 - um[1] * X1);
-  a = row_sum(active ? a : 0.f);
-  u = row_sum(active ? u : 0.f);
-  a = (readlane_f(a, 0) + readlane_f(a, 16)) + (readlane_f(a, 32) + readlane_f(a, 48));
-  u = (readlane_f(u, 0) + readlane_f(u, 16)) + (readlane_f(u, 32) + readlane_f(u, 48));
-  return silu_mul_f32(a, u, bad);
-}
-
-// Bounded wait (wave-uniform) until LDS counter *p reaches `target`; a wait
-// past the bound sets the timeout bit and returns, so every wave exits.
-__device__ __forceinline__ void lds_wait(const uint32_t* p, uint32_t target, uint32_t& bad) {
-  uint32_t spins = 0;
-  while (__hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
-    if (++spins > kSpinLimit) {
-      bad |= kErrTimeout;
-      return;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-
-// Publish gate*h of round t (pair iteration k) in slot t%4.
-__device__ __forceinline__ void publish_round(float gh, unsigned t, unsigned k, int wave, int lane, DecodeLds& L,
-                                              uint32_t& bad) {
-  const unsigned s = t & 3;
-  // The slot's previous use (pair iteration k-1) is read by every wavefront.
-  if (k) lds_wait(&L.consumed[s], kDecodeWaves * k, bad);
-  if (lane == 0) {
-    L.h[s][wave] = gh;
-    __hip_atomic_fetch_add(&L.published[s], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-}
-
-// Down projection of round t (pair iteration k) from the round's down bytes
-// and the 8 published h: coefficients, then 8 outputs per lane.
-__device__ __forceinline__ void down_round(const DecodeDnBytes& R, unsigned t, unsigned k, int wave, int lane,
-                                           unsigned nsb, DecodeLds& L, float (&y)[8], uint32_t& bad) {
-  const unsigned s = t & 3;
-  lds_wait(&L.published[s], kDecodeWaves * (k + 1), bad);
-  const float* hs = L.h[s];
+// Down projection of round r (neurons 8r..8r+7, gate*h in hs[0..7]) from the
+// round's down bytes: coefficients, then 8 outputs per lane.
+__device__ __forceinline__ void down_round(const DecodeDnBytes& R, const float* hs, int wave, int lane, unsigned nsb,
+                                           DecodeLds& L, float (&y)[8], uint32_t& bad) {
   if (lane < 16) L.dh[wave][lane] = R.dh;
   DecodeTable& T = L.table[wave];
   {
@@ -1498,8 +1586,6 @@ __device__ __forceinline__ void down_round(const DecodeDnBytes& R, unsigned t, u
     *reinterpret_cast<float2*>(&T.D[ts][tg][n0]) = make_float2(Dv[0], Dv[1]);
     *reinterpret_cast<float2*>(&T.M[ts][tg][n0]) = make_float2(Mv[0], Mv[1]);
   }
-  // This wavefront is past its reads of the slot's h.
-  if (lane == 0) __hip_atomic_fetch_add(&L.consumed[s], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   __builtin_amdgcn_wave_barrier();
   const unsigned sbl = (unsigned)lane >> 5, j = (unsigned)lane & 31, g = j >> 2;   // 8 outputs
   if (2 * (unsigned)wave + sbl < nsb) {
@@ -1533,6 +1619,7 @@ __device__ __forceinline__ void down_round(const DecodeDnBytes& R, unsigned t, u
       for (int cc = 0; cc < 4; ++cc) y[4 * half + cc] += s4[cc];
     }
   }
+  __builtin_amdgcn_wave_barrier();   // the table and headers are read before the next round writes them
 }
 
 // The unit's fp32 partial, position-major so that each store instruction
@@ -1550,100 +1637,133 @@ __device__ __forceinline__ void store_partial(const Scratch& S, unsigned unit, i
 }
 
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* __restrict__ plan, Scratch S) {
-  const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
+  const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
   uint32_t* status = S.out + (size_t)S.parity * S.out_words;
   if (blockIdx.x == 0) clear_other_parity(S);
-  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + H.pairs_off);
-  const unsigned hidden = H.hidden, nch = hidden / 64, nsb = hidden / 256, G = gridDim.x, np = H.npairs;
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
+  const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden)), nsb = hidden / 256, nsub = hidden / 32;
+  const unsigned G = gridDim.x, np = plan_field(PH, offsetof(PlanHeader, npairs));
   // The wavefront index through readfirstlane: the compiler then knows it is
   // uniform, so offsets built from it stay in scalar registers.
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool active = lane < (int)nch;
-  const unsigned c = active ? (unsigned)lane : nch - 1;   // idle lanes re-read the last chunk
   __shared__ __align__(16) DecodeLds L;
-
-  // x of every token, copied to LDS as [token][k][lane] by the load units
-  // (lane c of copy k: x[64c + 4k .. +3]), so that the per-word reads of a
-  // wavefront are contiguous; then round 0 of the first unit, whose six
-  // loads are the only ones younger than the copies when they are waited for.
-  const unsigned T = H.burst;
-  {
-    const uint8_t* xg = plan + H.x_off;
-    for (unsigned i = (unsigned)wave; i < 16 * T; i += kDecodeWaves) {
-      const unsigned tok = i >> 4, k = i & 15;
-      const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&L.x[tok][k][0]);
-      const uint8_t* g = xg + (size_t)tok * hidden * sizeof(float) + 256 * (size_t)c + 16 * k;
-      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
-    }
-  }
-  unsigned p = blockIdx.x;   // the grid never exceeds the unit count
-  LaneOffsets lo;
-  lo.q0 = 16 * c;
-  lo.q1 = 16 * nch + 16 * c;
-  lo.gh = 32 * nch + 16 * (c >> 2);
-  lo.dq = 4608 * min(2 * (unsigned)wave + ((unsigned)lane >> 5), nsb - 1) + 32 * ((unsigned)lane & 31);
-  lo.dh = 4608 * min(2 * (unsigned)wave + (((unsigned)lane & 15) >> 3), nsb - 1) + 4096 + 16 * ((unsigned)lane & 7);
-  PairBuf B = pair_buf(pairs[p]);
-  DecodeGuBytes G0, G1, G2, G3;
-  DecodeDnBytes D0, D1, D2, D3;
-  load_gu(B, 0, wave, lo, G0);
-  static_assert(kGuLoads == 6, "the wait below counts round 0's loads");
-  asm volatile("s_waitcnt vmcnt(6)" ::: "memory");   // this wavefront's x copies
-  if (tid < 4) L.published[tid] = L.consumed[tid] = 0;
-  __syncthreads();   // x is in LDS; the counters are zero
-  float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const float* xg = reinterpret_cast<const float*>(plan + plan_field(PH, offsetof(PlanHeader, x_off)));
+  const unsigned xs0 = 32 * ((unsigned)tid >> 2) + 8 * ((unsigned)tid & 3);   // this thread's 8 values of a token
+  const bool xin = ((unsigned)tid >> 2) < nsub;
+  const unsigned sb0 = 2 * (unsigned)wave, sb1 = sb0 + 1;
+  const bool has0 = sb0 < nsb, has1 = sb1 < nsb;
+  const unsigned lb0 = min(sb0, nsb - 1), lb1 = min(sb1, nsb - 1);   // super-blocks loaded (clamped)
+  // Down-matrix offsets of this lane (super-blocks clamped to the matrix).
+  const uint32_t dq_off = 4608 * min(2 * (unsigned)wave + ((unsigned)lane >> 5), nsb - 1) + 32 * ((unsigned)lane & 31);
+  const uint32_t dh_off =
+      4608 * min(2 * (unsigned)wave + (((unsigned)lane & 15) >> 3), nsb - 1) + 4096 + 16 * ((unsigned)lane & 7);
   uint32_t bad = 0;
-  unsigned prev = p;
-  // Unit k (a (token, pair) of the request), round t = 4k + r: request the
-  // gate/up bytes of round t+1 (the next unit's round 0 after round 3) and
-  // the down bytes of round t, compute h of round t, apply the down of round
-  // t-1; a unit's partial is stored after its last down. The scheduling
-  // barriers keep the loads where they are written.
+
+  // The first unit's x is requested first, then its round 0, so that waiting
+  // for x does not wait for the weights. x is staged per unit (the units of
+  // a burst are token-major): the next unit's x is requested with its first
+  // bytes and staged into the other slot after this unit.
+  unsigned p = blockIdx.x;   // the grid never exceeds the unit count
+  PairBuf B = pair_buf(pairs + p);
+  float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  if (xin) {
+    const float* xt = xg + (size_t)B.token * hidden + xs0;
+    xv[0] = *reinterpret_cast<const float4*>(xt);
+    xv[1] = *reinterpret_cast<const float4*>(xt + 4);
+  }
+  uint4 h0 = make_uint4(0u, 0u, 0u, 0u), h1 = h0;
+  DecodeNib N[4];                      // [round]: round r+1's bytes are in flight during round r
+  DecodeDnBytes D[4];                  // a round's down bytes are used one round later (lagged down)
+  h0 = load_hdr(B, lb0, lane);
+  h1 = load_hdr(B, lb1, lane);
+  load_nib(B, 0, lb0, lb1, lane, N[0]);
+  load_dn(B, 0, dq_off, dh_off, D[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  stage_x(xv, 0, nsub, true, L, bad);
+  __syncthreads();   // x is in LDS
+
+  float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const unsigned kg = (unsigned)lane >> 4, jcol = (unsigned)lane & 15;
+  // Unit k: round rb = 0..3 requests round rb+1's bytes (the next unit's
+  // headers and round 0 after round 3), applies the down projection of round
+  // rb-1 (its bytes and h are at hand), forms row-block rb's gate/up sums,
+  // meets the other wavefronts at the barrier and forms the round's 8 h;
+  // round 3's down follows the loop. Doing the lagged down first gives the
+  // round's gate/up bytes that much longer to arrive. The scheduling
+  // barriers keep the loads where they are written. Round 1's bytes are
+  // requested before the header pass, whose wait on the headers would
+  // otherwise delay them.
   for (unsigned k = 0;; ++k) {
-    const unsigned q = p + G, t = 4 * k;
+    const unsigned q = p + G, par = k & 1, t = par;   // t: this unit's x slot
     const bool more = q < np;
-    const float4(&xl)[16][64] = L.x[B.token];
-    float X0 = 0.f, X1 = 0.f;
+    const PairBuf Bn = pair_buf(pairs + (more ? q : p), more);
+    load_nib(B, 1, lb0, lb1, lane, N[1]);
+    load_dn(B, 1, dq_off, dh_off, D[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 b0[4], b1[4];
+    float fx0[2], fx1[2];
+    x_operands(t, sb0, lane, L, b0, fx0);
+    x_operands(t, sb1, lane, L, b1, fx1);
+    {
+      float mp = 0.f;
+      if (has0) mp += header_pass(h0, sb0, 0, t, wave, lane, L, bad);
+      if (has1) mp += header_pass(h1, sb1, 1, t, wave, lane, L, bad);
+      L.minp[par][wave][lane] = mp;
+    }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 a = xl[i][c], b = xl[8 + i][c];
-      X0 += (a.x + a.y) + (a.z + a.w);
-      X1 += (b.x + b.y) + (b.z + b.w);
+    for (int rb = 0; rb < 4; ++rb) {
+      const DecodeNib& Nc = N[rb];
+      __builtin_amdgcn_sched_barrier(0);
+      if (rb == 1 || rb == 2) {
+        load_nib(B, rb + 1, lb0, lb1, lane, N[rb + 1]);
+        load_dn(B, rb + 1, dq_off, dh_off, D[rb + 1]);
+      } else if (rb == 3) {   // the next unit (zeros without a memory access after the last)
+        if (xin) {
+          const float* xt = xg + (size_t)Bn.token * hidden + xs0;
+          xv[0] = *reinterpret_cast<const float4*>(xt);
+          xv[1] = *reinterpret_cast<const float4*>(xt + 4);
+        }
+        h0 = load_hdr(Bn, lb0, lane);
+        h1 = load_hdr(Bn, lb1, lane);
+        load_nib(Bn, 0, lb0, lb1, lane, N[0]);
+        load_dn(Bn, 0, dq_off, dh_off, D[0]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (rb) down_round(D[rb - 1], L.h[wave], wave, lane, nsb, L, y, bad);
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      if (has0) rb_products(Nc.q[0], b0, fx0, 0, rb, wave, lane, L, acc);
+      if (has1) rb_products(Nc.q[1], b1, fx1, 1, rb, wave, lane, L, acc);
+      {
+        float4 v4;
+        v4.x = row_sum(acc[0]);
+        v4.y = row_sum(acc[1]);
+        v4.z = row_sum(acc[2]);
+        v4.w = row_sum(acc[3]);
+        if (jcol == 0) *reinterpret_cast<float4*>(&L.rowp[par][wave][16 * rb + 4 * kg]) = v4;
+      }
+      __syncthreads();   // every wavefront's sums of row-block rb are in LDS
+      // h of neurons 8rb..8rb+7 (gate row 16rb + i, up row 16rb + 8 + i);
+      // every wavefront forms its own copy.
+      if (lane < 8) {
+        const unsigned rg = 16 * rb + (unsigned)lane, ru = rg + 8;
+        float a = 0.f, u = 0.f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+          a += L.rowp[par][w][rg] - L.minp[par][w][rg];
+          u += L.rowp[par][w][ru] - L.minp[par][w][ru];
+        }
+        uint32_t hb = 0;
+        const float gh = B.gate * silu_mul_f32(a, u, hb);
+        if (wave == 0) bad |= hb;
+        L.h[wave][lane] = gh;
+      }
+      __builtin_amdgcn_wave_barrier();
     }
-    load_gu(B, 1, wave, lo, G1);
-    load_dn(B, 0, lo, D0);
-    __builtin_amdgcn_sched_barrier(0);
-    publish_round(B.gate * neuron_h(G0, (int)c, active, xl, X0, X1, bad), t, k, wave, lane, L, bad);
-    if (k) {
-      down_round(D3, t - 1, k - 1, wave, lane, nsb, L, y, bad);
-      store_partial(S, prev, wave, lane, y);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    load_gu(B, 2, wave, lo, G2);
-    load_dn(B, 1, lo, D1);
-    __builtin_amdgcn_sched_barrier(0);
-    publish_round(B.gate * neuron_h(G1, (int)c, active, xl, X0, X1, bad), t + 1, k, wave, lane, L, bad);
-    down_round(D0, t, k, wave, lane, nsb, L, y, bad);
-    __builtin_amdgcn_sched_barrier(0);
-    load_gu(B, 3, wave, lo, G3);
-    load_dn(B, 2, lo, D2);
-    __builtin_amdgcn_sched_barrier(0);
-    publish_round(B.gate * neuron_h(G2, (int)c, active, xl, X0, X1, bad), t + 2, k, wave, lane, L, bad);
-    down_round(D1, t + 1, k, wave, lane, nsb, L, y, bad);
-    __builtin_amdgcn_sched_barrier(0);
-    const PairBuf Bn = pair_buf(pairs[more ? q : p]);
-    if (more) load_gu(Bn, 0, wave, lo, G0);
-    load_dn(B, 3, lo, D3);
-    __builtin_amdgcn_sched_barrier(0);
-    publish_round(B.gate * neuron_h(G3, (int)c, active, xl, X0, X1, bad), t + 3, k, wave, lane, L, bad);
-    down_round(D2, t + 2, k, wave, lane, nsb, L, y, bad);
-    __builtin_amdgcn_sched_barrier(0);
-    if (!more) {
-      down_round(D3, t + 3, k, wave, lane, nsb, L, y, bad);
-      store_partial(S, p, wave, lane, y);
-      break;
-    }
-    prev = p;
+    down_round(D[3], L.h[wave], wave, lane, nsb, L, y, bad);
+    store_partial(S, p, wave, lane, y);
+    if (!more) break;
+    stage_x(xv, par ^ 1, nsub, true, L, bad);
+    __syncthreads();   // the next unit's x is in LDS
     p = q;
     B = Bn;
   }
@@ -1806,10 +1926,32 @@ __device__ __forceinline__ uint8_t q4kt_byte(const Src& src, uint32_t base, uint
   return (uint8_t)(q4kt_nibble(src, base, row_bytes, n, j) | (q4kt_nibble(src, base, row_bytes, n, j + 1) << 4));
 }
 
+// Byte o of the TQ4_KM gate/up tiles of a pair (layout above) from the
+// reference rows: gate rows at 0, up rows at proj, row n at n * 144 * nsb,
+// super-block sb at 144 * sb with its 128 nibble bytes from offset 16
+// (element j of a super-block: byte 32 * (j / 64) + j % 32, high nibble when
+// j % 64 >= 32).
+template <class Src>
+__device__ __forceinline__ uint8_t km_byte(const Src& src, uint32_t hidden, uint32_t proj, uint32_t o) {
+  const uint32_t row_bytes = 144 * (hidden / 256), sb = o / 9216, r = o % 9216;
+  if (r < 1024) {
+    const uint32_t rb = r / 256, i = (r / 16) % 16;
+    return src[(i >> 3) * proj + (8 * rb + (i & 7)) * row_bytes + 144 * sb + r % 16];
+  }
+  const uint32_t q = r - 1024, rb = q / 2048, p = (q / 1024) & 1, lane = (q / 16) & 63, byte = q & 15;
+  const uint32_t i = lane & 15, kg = lane >> 4, u = byte >> 2, b = byte & 3;
+  const uint32_t base = (i >> 3) * proj + (8 * rb + (i & 7)) * row_bytes + 144 * sb + 16;
+  const uint32_t j0 = 32 * (4 * p + kg) + 8 * u + b, j1 = j0 + 4;   // positions of the low and high nibble
+  const uint32_t n0 = (src[base + 32 * (j0 / 64) + j0 % 32] >> (4 * ((j0 % 64) / 32))) & 15u;
+  const uint32_t n1 = (src[base + 32 * (j1 / 64) + j1 % 32] >> (4 * ((j1 % 64) / 32))) & 15u;
+  return (uint8_t)(n0 | (n1 << 4));
+}
+
 // Byte o of a re-tiled slice whose reference-layout bytes are src[0..).
 template <class Src>
 __device__ uint8_t retile_byte(const SliceShape& s, const Src& src, uint32_t o) {
   const uint32_t nch = s.hidden / 64;
+  if (o < 2 * s.proj && s.gu == TQ4_KM) return km_byte(src, s.hidden, s.proj, o);
   if (o < 2 * s.proj) {
     uint32_t row_bytes = s.proj / kNeurons, rbase = (o / row_bytes) * row_bytes;
     return src[rbase + gu_source((uint8_t)s.gu, nch, o - rbase)];
@@ -1925,7 +2067,7 @@ __global__ void synth_kernel(uint8_t* __restrict__ dst, SliceShape routed, Slice
   const SliceShape& s = sh ? shared : routed;
   SynthSrc src;
   src.key = synth_key(seed, block, layer, e);
-  src.gu = s.gu;
+  src.gu = s.gu == TQ4_KM ? TQ4_K : s.gu;
   src.dn = s.dn == TQ4_KT ? TQ4_K : s.dn;
   src.proj = s.proj;
   src.gu_row = s.proj / kNeurons;
@@ -2000,7 +2142,8 @@ struct Layout {
 
 uint64_t row_bytes(uint32_t type, uint32_t n) {
   switch (type) {
-    case TQ4_K: return (uint64_t)n / 256 * 144;
+    case TQ4_K:
+    case TQ4_KM: return (uint64_t)n / 256 * 144;
     case TMXFP4: return (uint64_t)n / 32 * 17;
     case TQ8_0: return (uint64_t)n / 32 * 34;
     case TQ4_0: return (uint64_t)n / 32 * 18;
@@ -2016,7 +2159,7 @@ bool layout_of(uint32_t hidden, uint32_t format, Layout& l) {
   switch (format) {
     case FR_HIP_FMT_LEGACY: l.gu = TQ4_0; l.dn = TQ4_0; break;
     case FR_HIP_FMT_NATIVE: l.gu = TQ4_K; l.dn = TMXFP4; break;
-    case FR_HIP_FMT_Q4KT: l.gu = TQ4_K; l.dn = TQ4_KT; break;
+    case FR_HIP_FMT_Q4KT: l.gu = TQ4_KM; l.dn = TQ4_KT; break;
     case FR_HIP_FMT_Q8: l.gu = TQ8_0; l.dn = TQ8_0; break;
     case FR_HIP_FMT_MXFP4: l.gu = TMXFP4; l.dn = TMXFP4; break;
     default: return false;
@@ -2206,7 +2349,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   // and their summation order do not depend on the rest of the burst.
   bool decode = r->mode == MODE_F32 && np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
   for (uint32_t i = 0; decode && i < np; ++i)
-    decode = pairs[i].gu == TQ4_K && pairs[i].dn == TQ4_KT;
+    decode = pairs[i].gu == TQ4_KM && pairs[i].dn == TQ4_KT;
   for (int s2 = 0; decode && s2 < nu; ++s2) decode = ids[s2] != kShared;
   if (decode && !env_int("FRONK_HIP_NO_DECODE", 0)) {
     uint32_t nunits = 0;
