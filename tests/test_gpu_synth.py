@@ -52,6 +52,55 @@ def test_device_generator_matches_oracle_bytes(eng, fmt):
         assert eng.release(7) == fa.OK
 
 
+def km_tiles(ref, hidden):
+    """The matrix-core tiles of a Q4KT slice's gate/up rows, restated from the
+    layout description: ref holds the 32 gate and 32 up rows in the reference
+    layout (row = nsb super-blocks of [d, dmin, 12 scale bytes, 128 nibble
+    bytes]; element j of a super-block is byte 32*(j//64) + j%32, high nibble
+    when j%64 >= 32). Per super-block: [4 row-blocks][16 rows][16 B] headers,
+    then [4 row-blocks][2 parts][64 lanes][16 B] nibbles; row i < 8 of
+    row-block rb is gate row 8rb+i, row i >= 8 is up row 8rb+i-8; lane
+    16kg+i of part p holds sub-block 4p+kg of row i as 4 words, word u with
+    positions 8u..8u+3 in the low nibbles and 8u+4..8u+7 in the high ones."""
+    nsb = hidden // 256
+    rows = ref[:64 * 144 * nsb].reshape(64, nsb, 144)
+    j = np.arange(256)
+    q = (rows[:, :, 16 + 32 * (j // 64) + j % 32] >> (4 * ((j % 64) // 32))) & 15   # [row][sb][256]
+    out = np.zeros(9216 * nsb, np.uint8)
+    u, b = np.meshgrid(np.arange(4), np.arange(4), indexing="ij")
+    for sb in range(nsb):
+        blk = out[9216 * sb:9216 * (sb + 1)]
+        for rb in range(4):
+            for i in range(16):
+                r = 8 * rb + i if i < 8 else 32 + 8 * rb + i - 8
+                blk[16 * (16 * rb + i):16 * (16 * rb + i) + 16] = rows[r, sb, :16]
+                for p in range(2):
+                    for kg in range(4):
+                        v = q[r, sb, 32 * (4 * p + kg):32 * (4 * p + kg) + 32]
+                        base = 1024 + 2048 * rb + 1024 * p + 16 * (16 * kg + i)
+                        blk[base:base + 16] = (v[8 * u + b] | (v[8 * u + 4 + b] << 4)).reshape(16)
+    return out
+
+
+def test_q4kt_gate_up_tiles_match_layout(eng):
+    """The re-tiler's matrix-core tiles of the Q4KT gate/up rows, byte for
+    byte, against the layout restated above, on random slice bytes."""
+    lay = oracle.layout(H, fa.FMT_Q4KT)
+    rng = np.random.default_rng(77)
+    assert eng.reserve(7, H, fa.FMT_Q4KT) == fa.OK
+    try:
+        unit = sparse_unit(lay)
+        for layer, e in [(0, 5), (3, 400)]:
+            view = slice_view(unit, lay, layer, e)
+            view[:] = rng.integers(0, 256, view.size, dtype=np.uint8)
+            assert eng.refresh(7, unit, layer, e) == fa.OK
+            got = eng.read(7, oracle.slice_offset(lay, layer, e), 2 * lay.proj)
+            want = km_tiles(view, H)
+            assert np.array_equal(got, want), (layer, e, int(np.argmax(got != want)))
+    finally:
+        assert eng.release(7) == fa.OK
+
+
 def test_absent_layer_is_state(eng):
     assert eng.synthetic(2, H, fa.FMT_Q4KT, 1, 1) == fa.OK
     try:
