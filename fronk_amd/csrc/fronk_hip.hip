@@ -1336,8 +1336,10 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(const uint8_t* __restri
 // unit partials in unit order: the kernel boundary is the global barrier and
 // makes the partials visible across XCDs.
 //
-// Every lane loads the bytes it uses into registers with the non-temporal
-// policy, one round ahead: round r+1's gate/up and down bytes during round r
+// Every lane loads the bytes it uses into registers with the default cache
+// policy (measured faster here than the non-temporal one, and it lets the
+// units of one pair that follow each other in a workgroup's chunk find its
+// bytes cached), one round ahead: round r+1's gate/up and down bytes during round r
 // (the next unit's headers and first round during round 3). One round in
 // flight (about 55 KB per workgroup) streams at the measured ceiling; two
 // rounds in flight stream more slowly.
@@ -1385,7 +1387,7 @@ __device__ __forceinline__ PairBuf pair_buf(const PairDesc* P, bool live = true)
   return B;
 }
 __device__ __forceinline__ uint4 bld(const PairBuf& B, uint32_t voff, uint32_t soff) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(B.rsrc, (int)voff, (int)soff, 2);   // 2: nt
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(B.rsrc, (int)voff, (int)soff, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
@@ -1642,7 +1644,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
   if (blockIdx.x == 0) clear_other_parity(S);
   const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
   const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden)), nsb = hidden / 256, nsub = hidden / 32;
-  const unsigned G = gridDim.x, np = plan_field(PH, offsetof(PlanHeader, npairs));
+  const unsigned np = plan_field(PH, offsetof(PlanHeader, npairs)), tpw = plan_field(PH, offsetof(PlanHeader, tpw));
+  const unsigned burst = plan_field(PH, offsetof(PlanHeader, burst));
+  // Token-major partial index of each unit of the work list (after the token table).
+  const uint32_t* upart = reinterpret_cast<const uint32_t*>(plan + plan_field(PH, offsetof(PlanHeader, groups_off)) +
+                                                          burst * sizeof(DecodeToken));
   // The wavefront index through readfirstlane: the compiler then knows it is
   // uniform, so offsets built from it stay in scalar registers.
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1663,7 +1669,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
   // for x does not wait for the weights. x is staged per unit (the units of
   // a burst are token-major): the next unit's x is requested with its first
   // bytes and staged into the other slot after this unit.
-  unsigned p = blockIdx.x;   // the grid never exceeds the unit count
+  unsigned p = blockIdx.x * tpw;   // this workgroup's chunk: units [p, min(p + tpw, np))
+  const unsigned pend = min(p + tpw, np);
   PairBuf B = pair_buf(pairs + p);
   float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
   if (xin) {
@@ -1694,8 +1701,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
   // requested before the header pass, whose wait on the headers would
   // otherwise delay them.
   for (unsigned k = 0;; ++k) {
-    const unsigned q = p + G, par = k & 1, t = par;   // t: this unit's x slot
-    const bool more = q < np;
+    const unsigned q = p + 1, par = k & 1, t = par;   // t: this unit's x slot
+    const bool more = q < pend;
     const PairBuf Bn = pair_buf(pairs + (more ? q : p), more);
     load_nib(B, 1, lb0, lb1, lane, N[1]);
     load_dn(B, 1, dq_off, dh_off, D[1]);
@@ -1760,7 +1767,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
       __builtin_amdgcn_wave_barrier();
     }
     down_round(D[3], L.h[wave], wave, lane, nsb, L, y, bad);
-    store_partial(S, p, wave, lane, y);
+    store_partial(S, plan_read(upart + p), wave, lane, y);
     if (!more) break;
     stage_x(xv, par ^ 1, nsub, true, L, bad);
     __syncthreads();   // the next unit's x is in LDS
@@ -2352,37 +2359,54 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     decode = pairs[i].gu == TQ4_KM && pairs[i].dn == TQ4_KT;
   for (int s2 = 0; decode && s2 < nu; ++s2) decode = ids[s2] != kShared;
   if (decode && !env_int("FRONK_HIP_NO_DECODE", 0)) {
-    uint32_t nunits = 0;
+    // Units are (token, pair). Their partials are numbered token-major in the
+    // reference's order (token, routed expert in request order, ascending
+    // block), which the reduction follows; the work list is pair-major, so
+    // that the units of one pair are consecutive in one workgroup's chunk and
+    // its bytes are read again while they are still cached.
     DecodeToken tok[kMaxBurst];
+    uint32_t nunits = 0;
     for (uint32_t t = 0; t < T; ++t) {
       tok[t].first = nunits;
-      for (int e = 0; e < 10; ++e) {
-        const uint16_t id = r->expert[t * 10 + e];
-        for (int b = 0; b < kBlocks; ++b) {
-          if (!E.block[b]) continue;
-          const Layout& l = E.lay[b];
-          PairDesc& U = pairs[nunits++];
+      tok[t].count = 10u * (uint32_t)nloaded;
+      nunits += tok[t].count;
+    }
+    uint32_t* upart = reinterpret_cast<uint32_t*>(out + H->pairs_off + nunits * sizeof(PairDesc) +
+                                                  T * sizeof(DecodeToken));
+    uint32_t w = 0;
+    for (int s2 = 0; s2 < nu; ++s2) {
+      int brank = 0;
+      for (int b = 0; b < kBlocks; ++b) {
+        if (!E.block[b]) continue;
+        const Layout& l = E.lay[b];
+        for (uint32_t t = 0; t < T; ++t) {
+          if (!(masks[s2] >> t & 1u)) continue;
+          int e = 0;
+          while (r->expert[t * 10 + e] != ids[s2]) ++e;   // the expert's place in the token's list
+          PairDesc& U = pairs[w];
           memset(&U, 0, sizeof(U));
-          U.slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer + (uint64_t)id * l.slice);
+          U.slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer + (uint64_t)ids[s2] * l.slice);
           U.proj = (uint32_t)l.proj;
           U.gu = (uint8_t)l.gu;
           U.dn = (uint8_t)l.dn;
           U.tmask = (uint8_t)(1u << t);
           U.pad = (uint8_t)t;
           U.gate[0] = r->gate[t * 11 + e];
+          upart[w++] = tok[t].first + (uint32_t)e * (uint32_t)nloaded + (uint32_t)brank;
         }
+        ++brank;
       }
-      tok[t].count = nunits - tok[t].first;
     }
+    if (w != nunits) return FR_HIP_INVALID;   // every token routes 10 distinct experts
     H->npairs = nunits;
     H->ngroups = T;
     H->groups_off = H->pairs_off + nunits * sizeof(PairDesc);
     memcpy(out + H->groups_off, tok, T * sizeof(DecodeToken));
-    H->x_off = (uint32_t)((H->groups_off + T * sizeof(DecodeToken) + 255) & ~255u);
+    H->x_off = (uint32_t)((H->groups_off + T * sizeof(DecodeToken) + nunits * sizeof(uint32_t) + 255) & ~255u);
     memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
     H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
-    // One workgroup per unit, one per CU at most (the fewest workgroups that
-    // keep ceil(units / cap) units each).
+    // One workgroup per CU at most, each taking a contiguous chunk of
+    // ceil(units / cap) units of the work list.
     const uint32_t cap = E.cus < (unsigned)kDecodeGridMax ? E.cus : (unsigned)kDecodeGridMax;
     const uint32_t ppw = (nunits + cap - 1) / cap;
     H->kind = KIND_DECODE;
