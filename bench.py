@@ -15,6 +15,8 @@ stdout: exactly one JSON line. Everything else goes to stderr.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload q4k]
                   [--cpu-seconds S] [--no-cpu]
+  python bench.py --workload prefill   a step is one 48-layer chunk of 512
+                                        tokens through fr_hip_run_batch
   python bench.py --copy-kernel BYTES   plain device copy, for scaling the
                                         FETCH_SIZE/WRITE_SIZE counters
 """
@@ -166,12 +168,173 @@ def cpu_baseline(fa, eng, fmt, reqs, budget_s):
     }
 
 
+PREFILL_LAYERS = 48
+PREFILL_TOKENS = 512
+MFMA_F32_PEAK_TFLOPS = 157.3
+PREFILL_TEXT = ("Resident node prefill: 48 layers x 512 experts x 640 intermediate x hidden 4096, all Q4_K "
+                "(down transposed, 108.7 GB in HBM); a chunk of 512 tokens, top-10 of 512 uniform per token per "
+                "layer, through fr_hip_run_batch (fp32 matrix cores)")
+
+
+def prefill_requests(rng, layers, tokens):
+    reqs = []
+    for layer in range(layers):
+        experts = np.argsort(rng.random((tokens, 512)), axis=1)[:, :10].astype(np.uint16)
+        reqs.append((layer, experts, softmax_gates(rng, tokens),
+                     rng.standard_normal((tokens, HIDDEN)).astype(np.float32)))
+    return reqs
+
+
+def prefill_cpu_baseline(fa, y0, req, budget_s):
+    """Bursts of 8 tokens of the chunk's layer 0 (the reference client's cut,
+    client/fronk_client.h:41-42) through the oracle's scalar restatement of
+    ref (backends/ref.c:57-98), one host thread; bytes are each burst's unique
+    experts x 20 slices. The chunk's GPU rows are compared with it."""
+    import oracle
+    from fixtures import host_units, oracle_request
+    lay = oracle.layout(HIDDEN, fa.FMT_Q4KT)
+    layer, experts, gates, x = req
+    done, seconds, wbytes, worst = 0, 0.0, 0, [0.0, 0.0]
+    for t0 in range(0, experts.shape[0], 8):
+        sl = slice(t0, t0 + 8)
+        units = host_units(lay, SEED, layer, experts[sl])
+        t1 = time.perf_counter()
+        rc, ref = oracle.ref_run(units, fa.FMT_Q4KT, False, oracle_request(layer, experts[sl], gates[sl], x[sl]))
+        seconds += time.perf_counter() - t1
+        if rc != 0:
+            raise RuntimeError(f"oracle ref_run failed with {rc}")
+        for t in range(ref.shape[0]):
+            rc, err = oracle.compare(ref[t], y0[t0 + t])
+            worst = [max(worst[0], err[0]), max(worst[1], err[1])]
+        wbytes += len(set(experts[sl].ravel().tolist())) * SLICES * lay.slice
+        done += ref.shape[0]
+        del units
+        if seconds >= budget_s:
+            break
+    return {
+        "value": wbytes / seconds / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"{done} tokens of layer 0 in bursts of 8 through the oracle's scalar restatement of ref "
+                  f"(backends/ref.c:57-98), 1 thread, {seconds:.1f} s",
+        "tokens_per_s": done / seconds,
+        "gpu_vs_oracle": {"rel_l2_max": worst[0], "normalized_max": worst[1], "tokens": done},
+    }
+
+
+def bench_prefill(args):
+    import torch
+    import fronk_amd as fa
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    steps = args.steps if args.steps is not None else 3
+    warmup = args.warmup if args.warmup is not None else 1
+    lib = fa.lib()
+    eng = fa.Engine(0)
+    t0 = time.perf_counter()
+    for b in range(SLICES):
+        fa.check(eng.synthetic(b, HIDDEN, fa.FMT_Q4KT, PREFILL_LAYERS, SEED), "fr_hip_synthetic")
+    log(f"resident: {SLICES} blocks x {PREFILL_LAYERS} layers generated in {time.perf_counter() - t0:.1f} s")
+    reqs = prefill_requests(np.random.default_rng(SEED + 5), PREFILL_LAYERS, PREFILL_TOKENS)
+    slice_bytes = slice_sizes(fa, fa.FMT_Q4KT)[0]
+    cap = lib.fr_hip_batch_plan_bytes(PREFILL_TOKENS, HIDDEN)
+    stride = (cap + 255) // 256 * 256
+    host = np.zeros((PREFILL_LAYERS, stride), np.uint8)
+    wts = np.zeros(PREFILL_LAYERS)
+    for i, (layer, experts, gates, x) in enumerate(reqs):
+        plan = eng.batch_plan(layer, experts, gates, x)
+        host[i, :plan.size] = plan
+        wts[i] = len(set(experts.ravel().tolist())) * SLICES * slice_bytes
+    dev = torch.from_numpy(host).to("cuda")
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    hptr, dptr, sptr = host.ctypes.data, dev.data_ptr(), C.c_void_p(stream.cuda_stream)
+
+    def chunk():
+        for i in range(PREFILL_LAYERS):
+            rc = lib.fr_hip_batch_launch(C.c_void_p(hptr + i * stride), C.c_void_p(dptr + i * stride), sptr)
+            if rc != fa.OK:
+                raise RuntimeError(f"fr_hip_batch_launch failed with {rc}")
+
+    for _ in range(warmup):
+        chunk()
+    stream.synchronize()
+    log(f"warm: {warmup} chunks")
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for _ in range(steps):
+            chunk()
+        ev1.record(stream)
+    stream.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    chunk_ms = ev0.elapsed_time(ev1) / steps
+    log(f"timed: {steps} chunks, {chunk_ms:.3f} ms per chunk")
+    status = C.c_uint(0)
+    fa.check(lib.fr_hip_batch_output(sptr, None, 0, C.byref(status)), "fr_hip_batch_output")
+    if status.value:
+        raise RuntimeError(f"prefill kernels reported status {status.value}")
+
+    # Split per launch: prefill_gate_up + prefill_down ("main") and the whole
+    # launch, from events on the launch stream over one more chunk.
+    fa.check(lib.fr_hip_timing(PREFILL_LAYERS), "fr_hip_timing")
+    chunk()
+    main_ms, total_ms, counted = C.c_double(), C.c_double(), C.c_uint()
+    fa.check(lib.fr_hip_timing_read(C.byref(main_ms), C.byref(total_ms), C.byref(counted)), "fr_hip_timing_read")
+
+    alg = wts.sum() + PREFILL_LAYERS * 8.0 * PREFILL_TOKENS * HIDDEN   # weights once per unique expert, x and y
+    achieved = alg / (chunk_ms * 1e-3) / 1e9
+    flops = PREFILL_LAYERS * 2.0 * PREFILL_TOKENS * 10 * SLICES * 3 * 32 * HIDDEN   # useful multiply-adds x 2
+    tflops = flops / (chunk_ms * 1e-3) / 1e12
+
+    cpu = None
+    if not args.no_cpu:
+        layer, experts, gates, x = reqs[0]
+        rc, y0 = eng.run_batch(layer, experts, gates, x)
+        fa.check(rc, "fr_hip_run_batch")
+        cpu = prefill_cpu_baseline(fa, y0, reqs[0], args.cpu_seconds)
+    for b in range(SLICES):
+        eng.release(b)
+    out = {
+        "metric": METRIC,
+        "value": round(wts.sum() * steps / wall / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall * 1e3 / steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded device generator; Q4_K d/dmin fp16 U[1e-3,1e-2], x ~ N(0,1))",
+        "config": {"workload": PREFILL_TEXT, "hidden": HIDDEN, "experts": 512, "active_experts": 10,
+                   "slices": SLICES, "tokens": PREFILL_TOKENS, "layers": PREFILL_LAYERS, "format": "Q4KT",
+                   "mode": "f32"},
+        "hbm_frac": round(wts.sum() * steps / wall / 1e9 / HBM_PEAK_GBS, 4),
+        "tokens_per_s_per_layer": round(PREFILL_TOKENS / (chunk_ms * 1e-3 / PREFILL_LAYERS), 1),
+        "chunk_ms": round(chunk_ms, 4),
+        "layer_us": round(chunk_ms * 1e3 / PREFILL_LAYERS, 2),
+        "kernel_split_us": {"gate_up+down": round(main_ms.value * 1e3 / counted.value, 2),
+                            "launch": round(total_ms.value * 1e3 / counted.value, 2),
+                            "note": "per layer launch, events on the launch stream, one extra chunk"},
+        "weight_bytes_per_chunk": float(wts.sum()),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "prefill_gate_up + prefill_down + prefill_reduce"},
+        "mfma": {"achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s (fp32 matrix)",
+                 "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", default="q4k", choices=sorted(WORKLOADS))
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="q4k", choices=sorted(WORKLOADS) + ["prefill"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--run-calls", type=int, default=200)
@@ -184,6 +347,13 @@ def main():
     if args.copy_kernel:
         copy_kernel(args.copy_kernel)
         return
+    if args.workload == "prefill":
+        bench_prefill(args)
+        return
+    if args.steps is None:
+        args.steps = 1000
+    if args.warmup is None:
+        args.warmup = 200
 
     import torch
     import fronk_amd as fa

@@ -26,6 +26,12 @@ class Request(C.Structure):
                 ("x", C.POINTER(C.c_float))]
 
 
+class Batch(C.Structure):
+    _fields_ = [("layer", C.c_uint), ("tokens", C.c_uint), ("hidden", C.c_uint), ("mode", C.c_uint),
+                ("expert", C.POINTER(C.c_uint16)), ("gate", C.POINTER(C.c_float)),
+                ("x", C.POINTER(C.c_float))]
+
+
 class Sample(C.Structure):
     _fields_ = [("runs", C.c_uint64), ("weight_bytes", C.c_uint64), ("hot_allocations", C.c_uint64),
                 ("blocks", C.c_uint), ("unique_experts", C.c_uint), ("pairs", C.c_uint), ("grid", C.c_uint),
@@ -50,6 +56,11 @@ SIGNATURES = {
     "fr_hip_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "fr_hip_last_output": (C.c_int, [C.c_void_p, C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_uint)]),
     "fr_hip_sample_get": (C.c_int, [C.POINTER(Sample)]),
+    "fr_hip_run_batch": (C.c_int, [C.POINTER(Batch), C.POINTER(C.c_float)]),
+    "fr_hip_batch_plan_bytes": (C.c_size_t, [C.c_uint, C.c_uint]),
+    "fr_hip_batch_plan": (C.c_int, [C.POINTER(Batch), C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "fr_hip_batch_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "fr_hip_batch_output": (C.c_int, [C.c_void_p, C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_uint)]),
     "fr_hip_timing": (C.c_int, [C.c_uint]),
     "fr_hip_timing_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_uint)]),
     "fr_hip_debug_dequant": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
@@ -98,6 +109,16 @@ def make_request(layer, experts, gates, x, mode=MODE_F32):
     burst, hidden = x.shape
     req = Request(layer, burst, hidden, mode, experts.ctypes.data_as(C.POINTER(C.c_uint16)),
                   fptr(gates), fptr(x))
+    return req, (experts, gates, x)
+
+
+def make_batch(layer, experts, gates, x, mode=MODE_F32):
+    """Build a Batch over numpy arrays; returns (batch, keepalive)."""
+    experts = np.ascontiguousarray(experts, np.uint16).reshape(-1, 10)
+    gates = np.ascontiguousarray(gates, np.float32).reshape(-1, 11)
+    x = np.ascontiguousarray(x, np.float32)
+    tokens, hidden = x.shape
+    req = Batch(layer, tokens, hidden, mode, experts.ctypes.data_as(C.POINTER(C.c_uint16)), fptr(gates), fptr(x))
     return req, (experts, gates, x)
 
 
@@ -158,6 +179,22 @@ class Engine:
         rc = lib().fr_hip_plan(C.byref(req), buf.ctypes.data, cap, C.byref(used), C.byref(grid))
         check(rc, "fr_hip_plan")
         return buf[:used.value].copy(), grid.value
+
+    def run_batch(self, layer, experts, gates, x, mode=MODE_F32):
+        """fr_hip_run_batch: a prefill chunk of any number of tokens."""
+        req, keep = make_batch(layer, experts, gates, x, mode)
+        y = np.zeros((req.tokens, req.hidden), np.float32)
+        rc = lib().fr_hip_run_batch(C.byref(req), fptr(y))
+        return rc, y
+
+    def batch_plan(self, layer, experts, gates, x, mode=MODE_F32):
+        req, keep = make_batch(layer, experts, gates, x, mode)
+        cap = lib().fr_hip_batch_plan_bytes(req.tokens, req.hidden)
+        buf = np.zeros(cap, np.uint8)
+        used = C.c_size_t()
+        rc = lib().fr_hip_batch_plan(C.byref(req), buf.ctypes.data, cap, C.byref(used))
+        check(rc, "fr_hip_batch_plan")
+        return buf[:used.value].copy()
 
     def sample(self):
         s = Sample()

@@ -30,6 +30,7 @@
 #include <string.h>
 
 #include <cmath>
+#include <vector>
 
 #include "fronk_hip.h"
 
@@ -2087,6 +2088,265 @@ __global__ void synth_kernel(uint8_t* __restrict__ dst, SliceShape routed, Slice
   }
 }
 
+// ------------------------------------------------------------ prefill path
+// A prefill chunk: T tokens of one layer (T up to kMaxBatchTokens), each with
+// its own top-10 routing, all owned slices Q4_K with the transposed down, F32.
+// The reference serves it as run() calls of at most 8 tokens
+// (client/fronk_client.h:41-42, src/backend.h:21); the result of token t is
+// that of run() on token t alone (backends/ref.c:57-98). Here the tokens are
+// grouped by routed expert, so that each expert's weights are read once for
+// all of its tokens and the work is a contraction:
+//   prefill_gate_up  (tile, slice): a, u of up to 16 tokens over one slice's
+//                    32 neurons on fp32 matrix cores, then gate*SiLU(a)*u;
+//   prefill_down     (tile, 1024 outputs): the expert's down matrix over all
+//                    owned slices applied to the tile's h on fp32 matrix
+//                    cores, one fp32 partial per (token, expert);
+//   prefill_reduce   (token, 1024 outputs): the token's 10 expert partials
+//                    summed in its routing order in fp64, then narrowed with
+//                    the reference's rule (backends/ref.c:37-40, 95).
+// v_mfma_f32_16x16x4_f32 (A: lane l holds A[l%16][l/16]; B: B[l/16][l%16];
+// C: lane l holds C[4(l/16)+r][l%16]) takes one fp32 value per lane and
+// operand, so each lane dequantizes exactly the weight it contributes; the
+// Q4_K-T down, stored along the outputs, needs no transposition.
+constexpr int kTileTokens = 16;          // tokens of one expert tile (the MFMA N)
+constexpr int kBatchThreads = 512;
+constexpr int kMaxBatchTokens = 4096;
+constexpr int kDownCols = 1024;          // outputs of one prefill_down workgroup
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct BatchTile {                       // one routed expert and up to 16 of its tokens
+  uint32_t expert, ntok, slot0, pad;
+};
+struct BatchSlot {                       // one (token, expert) of the chunk
+  uint32_t token;
+  float gate;
+};
+struct BatchHeader {
+  uint32_t hidden, tokens, nslots, ntiles;
+  uint32_t nblk, layer, tiles_off, slots_off;
+  uint32_t tokslot_off, x_off, total, experts;
+  uint64_t slice_bytes, proj;
+  uint64_t base[kBlocks];                // owned slices in ascending block order: the layer's base
+};
+static_assert(sizeof(BatchHeader) == 224, "batch header layout");
+struct BatchScratch {
+  float* h;                              // [nslots][nblk * 32] gate * h
+  float* part;                           // [nslots][hidden] per-(token, expert) partials
+  float* y;                              // [tokens][hidden]
+  uint32_t* status;
+};
+
+struct GateUpLds {
+  float x[2][32][8][kTileTokens];        // [buffer][position][sub-block][token]: one super-block of x
+  f32x4 c[kDecodeWaves][64];             // each wavefront's C fragment
+};
+
+// Workgroup (tile, slice): wavefront w takes row-block w%4 (gate rows of
+// neurons 8rb..8rb+7, then their up rows) and part w/4 (sub-blocks 0-3 or 4-7
+// of every super-block) of the TQ4_KM tiles; lane 16kg + i holds sub-block
+// 4p + kg of row i, which is exactly its A operand (row i, k = kg) for the 32
+// positions of the sub-block. x moves through LDS one super-block at a time,
+// double-buffered, the next one loaded while the current one is used.
+__global__ __launch_bounds__(kBatchThreads) void prefill_gate_up(const uint8_t* __restrict__ plan,
+                                                                 BatchScratch S) {
+  const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
+  const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[blockIdx.x];
+  const BatchSlot* slots = reinterpret_cast<const BatchSlot*>(plan + H.slots_off) + T.slot0;
+  const float* xg = reinterpret_cast<const float*>(plan + H.x_off);
+  const unsigned hidden = H.hidden, nsb = hidden / 256, nblk = H.nblk, brank = blockIdx.y;
+  const uint8_t* slice = reinterpret_cast<const uint8_t*>(H.base[brank] + (uint64_t)T.expert * H.slice_bytes);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const unsigned rb = (unsigned)wave & 3, p = (unsigned)wave >> 2, kg = (unsigned)lane >> 4,
+                 col = (unsigned)lane & 15;
+  __shared__ __align__(16) GateUpLds L;
+  // x staging: thread -> token xn, positions 8*xq..8*xq+7 of the super-block.
+  const unsigned xn = (unsigned)tid >> 5, xq = (unsigned)tid & 31;
+  const bool xlive = xn < T.ntok;
+  const float* xrow = xg + (size_t)(xlive ? slots[xn].token : 0) * hidden + 8 * xq;
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 xr[2] = {z4, z4};
+  auto load_x = [&](unsigned s) {
+    if (xlive) {
+      xr[0] = *reinterpret_cast<const float4*>(xrow + 256 * (size_t)s);
+      xr[1] = *reinterpret_cast<const float4*>(xrow + 256 * (size_t)s + 4);
+    }
+  };
+  auto store_x = [&](unsigned buf) {
+    const float v[8] = {xr[0].x, xr[0].y, xr[0].z, xr[0].w, xr[1].x, xr[1].y, xr[1].z, xr[1].w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) L.x[buf][8 * (xq & 3) + j][xq >> 2][xn] = v[j];
+  };
+  const uint8_t* wq = slice + 1024 + 2048 * rb + 1024 * p + 16 * (unsigned)lane;   // + 9216 s
+  const uint8_t* wh = slice + 256 * rb + 16 * col;
+  uint32_t bad = 0;
+  load_x(0);
+  uint4 q = ld16(wq), hd = ld16(wh);
+  store_x(0);
+  __syncthreads();
+  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  for (unsigned s = 0; s < nsb; ++s) {
+    const unsigned buf = s & 1;
+    const uint4 qc = q, hc = hd;
+    if (s + 1 < nsb) {
+      load_x(s + 1);
+      q = ld16(wq + 9216 * (size_t)(s + 1));
+      hd = ld16(wh + 9216 * (size_t)(s + 1));
+    }
+    uint32_t sc, mi;
+    q4k_scale_min(hc.y, hc.z, hc.w, 4 * p + kg, sc, mi);
+    if (half_bad(hc.x) || half_bad(hc.x >> 16)) bad |= kErrScale;
+    const float D = half_to_float(hc.x & 0xffff) * (float)sc * kFp8Nibble;   // nibbles arrive as q * 2^-9
+    const float M = half_to_float(hc.x >> 16) * (float)mi;
+    const float* xb = &L.x[buf][0][4 * p + kg][col];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      // Word u: low nibbles = positions 8u..8u+3, high nibbles 8u+4..8u+7.
+      const uint32_t w = word(qc, u), lo = nib_lo(w), hi = nib_hi(w);
+      const float2 l0 = nib_pair<false>(lo), l1 = nib_pair<true>(lo), h0 = nib_pair<false>(hi),
+                   h1 = nib_pair<true>(hi);
+      const float a[8] = {l0.x, l0.y, l1.x, l1.y, h0.x, h0.y, h1.x, h1.y};
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(fmaf(a[j], D, -M), xb[(8 * u + j) * 8 * kTileTokens], c, 0, 0, 0);
+    }
+    if (s + 1 < nsb) store_x(buf ^ 1);
+    __syncthreads();
+  }
+  L.c[wave][lane] = c;
+  __syncthreads();
+  // Thread -> (row-block, neuron i, token n): a = gate row i, u = up row 8+i,
+  // each the sum of the two parts in a fixed order.
+  {
+    const unsigned trb = (unsigned)tid >> 7, i = ((unsigned)tid >> 4) & 7, n = (unsigned)tid & 15;
+    const float* c0 = reinterpret_cast<const float*>(&L.c[trb][0]);
+    const float* c1 = reinterpret_cast<const float*>(&L.c[trb + 4][0]);
+    const unsigned ga = 4 * (16 * (i >> 2) + n) + (i & 3), ua = 4 * (16 * (2 + (i >> 2)) + n) + (i & 3);
+    const float a = c0[ga] + c1[ga], u = c0[ua] + c1[ua];
+    if (n < T.ntok) {
+      uint32_t hb = 0;
+      const float h = slots[n].gate * silu_mul_f32(a, u, hb);
+      bad |= hb;
+      S.h[(size_t)(T.slot0 + n) * (nblk * kNeurons) + kNeurons * brank + 8 * trb + i] = h;
+    }
+  }
+  if (bad) flag(S.status, bad);
+}
+
+struct DownLds {
+  float h[kBlocks][4][kTileTokens][8];   // [slice][round q][token][neuron 8q + i of the slice]
+};
+
+// Workgroup (tile, 1024 outputs): wavefront w takes the 128 outputs
+// 256 sb + 128 hb .. +127 (sb = 4 blockIdx.y + w/2, hb = w%2). Lane (m, q)
+// loads, per owned slice, the 16-byte Q4_K-T units 32hb + m and 32hb + 16 + m
+// of round q (neurons 8q..8q+7; outputs 4 per unit) and the 8 neuron headers
+// of the round; the MFMA (unit u, neuron i, output c4) has k = q (neuron
+// 8q + i), m -> output 128hb + 64u + 4m + c4 and n = token.
+__global__ __launch_bounds__(kBatchThreads) void prefill_down(const uint8_t* __restrict__ plan, BatchScratch S) {
+  const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
+  const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[blockIdx.x];
+  const unsigned hidden = H.hidden, nsb = hidden / 256, nblk = H.nblk;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __shared__ __align__(16) DownLds L;
+  const unsigned nh = nblk * kNeurons;
+  for (unsigned k = (unsigned)tid; k < nblk * 4 * kTileTokens * 8; k += kBatchThreads) {
+    const unsigned i = k & 7, n = (k >> 3) & 15, rq = k >> 7;   // rq = 4 * slice + round
+    L.h[rq >> 2][rq & 3][n][i] = n < T.ntok ? S.h[(size_t)(T.slot0 + n) * nh + 8 * rq + i] : 0.f;
+  }
+  __syncthreads();
+  const unsigned sb = 4 * blockIdx.y + ((unsigned)wave >> 1), hb = (unsigned)wave & 1;
+  if (sb >= nsb) return;
+  const unsigned m = (unsigned)lane & 15, q = (unsigned)lane >> 4, n = m;
+  const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * H.proj + 4608 * (uint64_t)sb;
+  const uint32_t u0 = 1024 * q + 16 * (32 * hb + m), u1 = u0 + 16 * 16, hoff = 4096 + 128 * q;
+  const uint32_t g0 = 4 * hb + m / 8, g1 = g0 + 2;   // sub-blocks of the two units' outputs
+  uint32_t bad = 0;
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) acc[u][c4] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint4 U[2], hd[8];
+  auto load = [&](unsigned R) {
+    const uint8_t* d = reinterpret_cast<const uint8_t*>(H.base[R] + eoff);
+    U[0] = ld16(d + u0);
+    U[1] = ld16(d + u1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hd[i] = ld16(d + hoff + 16 * i);
+  };
+  load(0);
+  for (unsigned R = 0; R < nblk; ++R) {
+    const uint4 Uc[2] = {U[0], U[1]};
+    float D[2][8], M[2][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      bool ok0, ok1;
+      hdr_dm(hd[i], g0, D[0][i], M[0][i], ok0);
+      hdr_dm(hd[i], g1, D[1][i], M[1][i], ok1);
+      if (!ok0) bad |= kErrScale;
+      D[0][i] *= kFp8Nibble;
+      D[1][i] *= kFp8Nibble;
+    }
+    if (R + 1 < nblk) load(R + 1);
+    const float4 hv0 = *reinterpret_cast<const float4*>(&L.h[R][q][n][0]);
+    const float4 hv1 = *reinterpret_cast<const float4*>(&L.h[R][q][n][4]);
+    const float hv[8] = {hv0.x, hv0.y, hv0.z, hv0.w, hv1.x, hv1.y, hv1.z, hv1.w};
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        // Dword i/2: neurons 8q+2(i/2) (bytes 0,1) and 8q+2(i/2)+1 (bytes 2,3);
+        // low nibbles outputs 0 and 2, high nibbles outputs 1 and 3.
+        const uint32_t w = word(Uc[u], i >> 1), lo = nib_lo(w), hi = nib_hi(w);
+        const float2 lv = (i & 1) ? nib_pair<true>(lo) : nib_pair<false>(lo);
+        const float2 hv2 = (i & 1) ? nib_pair<true>(hi) : nib_pair<false>(hi);
+        const float a[4] = {lv.x, hv2.x, lv.y, hv2.y};
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4)
+          acc[u][c4] = __builtin_amdgcn_mfma_f32_16x16x4f32(fmaf(a[c4], D[u][i], -M[u][i]), hv[i], acc[u][c4], 0,
+                                                            0, 0);
+      }
+  }
+  // Lane l holds rows 4(l/16) + r (outputs 128hb + 64u + 4(4(l/16) + r) + c4)
+  // of token l%16.
+  if (n < T.ntok) {
+    float* dst = S.part + (size_t)(T.slot0 + n) * hidden + 256 * sb + 128 * hb;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<float4*>(dst + 64 * u + 4 * (4 * q + r)) =
+            make_float4(acc[u][0][r], acc[u][1][r], acc[u][2][r], acc[u][3][r]);
+  }
+  if (bad) flag(S.status, bad);
+}
+
+// Token t's outputs 1024 by..+1023: its 10 expert partials in routing order,
+// summed in fp64, narrowed to fp32 with the reference's overflow rule.
+__global__ __launch_bounds__(256) void prefill_reduce(const uint8_t* __restrict__ plan, BatchScratch S) {
+  const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
+  const unsigned t = blockIdx.x, hidden = H.hidden, c = kDownCols * blockIdx.y + 4 * threadIdx.x;
+  if (c >= hidden) return;
+  const uint32_t* ts = reinterpret_cast<const uint32_t*>(plan + H.tokslot_off) + 10 * (size_t)t;
+  double a[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int e = 0; e < 10; ++e) {
+    const float4 v = *reinterpret_cast<const float4*>(S.part + (size_t)ts[e] * hidden + c);
+    a[0] += v.x;
+    a[1] += v.y;
+    a[2] += v.z;
+    a[3] += v.w;
+  }
+  float y[4];
+  uint32_t bad = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (!isfinite(a[j]) || fabs(a[j]) > (double)FLT_MAX) bad = kErrRange;
+    y[j] = (float)a[j];
+  }
+  *reinterpret_cast<float4*>(S.y + (size_t)t * hidden + c) = make_float4(y[0], y[1], y[2], y[3]);
+  if (bad) flag(S.status, bad);
+}
+
 // Debug: decode re-tiled gate/up row(s) with the hot path's decoder.
 __global__ void debug_decode_rows(uint8_t type, const uint8_t* row, uint32_t n, float* out, uint32_t* status) {
   int c = threadIdx.x;
@@ -2230,6 +2490,17 @@ struct Engine {
   hipEvent_t* tev = nullptr;
   unsigned timed_cap = 0, timed = 0;
   bool timing = false;
+  // Prefill path: scratch (grown on demand), status word, plan buffers.
+  float* bh = nullptr;
+  float* bpart = nullptr;
+  float* by = nullptr;
+  size_t bh_bytes = 0, bpart_bytes = 0, by_bytes = 0;
+  uint32_t* bstatus = nullptr;
+  uint32_t* bstatus_host = nullptr;   // pinned
+  uint8_t* bplan_dev = nullptr;
+  uint8_t* bplan_host = nullptr;      // pinned
+  size_t bplan_cap = 0;
+  uint32_t batch_tokens = 0, batch_hidden = 0;
 };
 Engine E;
 bool g_open = false;
@@ -2490,6 +2761,170 @@ int fetch_output(hipStream_t s, size_t count, float* y, unsigned* status_out) {
   return FR_HIP_OK;
 }
 
+// ------------------------------------------------------------ prefill plan
+
+size_t batch_capacity(uint32_t tokens, uint32_t hidden) {
+  const size_t slots = (size_t)tokens * 10;
+  return sizeof(BatchHeader) + slots * (sizeof(BatchTile) + sizeof(BatchSlot) + sizeof(uint32_t)) + 4 * 256 +
+         (size_t)tokens * hidden * sizeof(float);
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Tokens grouped by routed expert (ascending id), each expert's tokens in
+// ascending order, cut into tiles of at most 16; tokslot[t][e] is the slot
+// of token t's e-th expert, the order in which its partials are summed.
+int build_batch(const fr_hip_batch* r, uint8_t* out, size_t cap, size_t* used) {
+  if (!r || !out || !used || !r->expert || !r->gate || !r->x) return FR_HIP_INVALID;
+  if (!r->tokens || r->tokens > (unsigned)kMaxBatchTokens || r->layer >= (unsigned)kLayers || r->mode > 2)
+    return FR_HIP_INVALID;
+  if (r->mode != MODE_F32) return FR_HIP_UNSUPPORTED;
+  const uint32_t T = r->tokens, hidden = r->hidden;
+  if (cap < batch_capacity(T, hidden)) return FR_HIP_INVALID;
+  BatchHeader* H = reinterpret_cast<BatchHeader*>(out);
+  memset(H, 0, sizeof(*H));
+  const Layout* l0 = nullptr;
+  for (int b = 0; b < kBlocks; ++b) {
+    if (!E.block[b]) continue;
+    const Layout& l = E.lay[b];
+    if (l.hidden != hidden) return FR_HIP_INVALID;
+    if (l.gu != TQ4_KM || l.dn != TQ4_KT) return FR_HIP_UNSUPPORTED;
+    if (r->layer >= E.layers[b]) return FR_HIP_STATE;
+    H->base[H->nblk++] = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer);
+    l0 = &l;
+  }
+  if (!l0) return FR_HIP_STATE;
+  std::vector<uint32_t> count(kRouted, 0), first(kRouted, 0), fill(kRouted, 0);
+  for (uint32_t t = 0; t < T; ++t) {
+    if (r->gate[t * 11 + 10] != 0.f) return FR_HIP_UNSUPPORTED;   // shared expert: run() serves it
+    for (int e = 0; e < 10; ++e) {
+      const uint16_t id = r->expert[t * 10 + e];
+      if (id >= kRouted) return FR_HIP_INVALID;
+      for (int f = 0; f < e; ++f)
+        if (r->expert[t * 10 + f] == id) return FR_HIP_INVALID;
+      ++count[id];
+    }
+  }
+  uint32_t nslots = 0, ntiles = 0, experts = 0;
+  for (int id = 0; id < kRouted; ++id) {
+    first[id] = nslots;
+    nslots += count[id];
+    ntiles += (count[id] + kTileTokens - 1) / kTileTokens;
+    experts += count[id] ? 1u : 0u;
+  }
+  H->hidden = hidden;
+  H->tokens = T;
+  H->nslots = nslots;
+  H->ntiles = ntiles;
+  H->layer = r->layer;
+  H->experts = experts;
+  H->slice_bytes = l0->slice;
+  H->proj = l0->proj;
+  H->tiles_off = (uint32_t)align256(sizeof(BatchHeader));
+  H->slots_off = (uint32_t)align256(H->tiles_off + (size_t)ntiles * sizeof(BatchTile));
+  H->tokslot_off = (uint32_t)align256(H->slots_off + (size_t)nslots * sizeof(BatchSlot));
+  H->x_off = (uint32_t)align256(H->tokslot_off + (size_t)T * 10 * sizeof(uint32_t));
+  H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
+  BatchTile* tiles = reinterpret_cast<BatchTile*>(out + H->tiles_off);
+  BatchSlot* slots = reinterpret_cast<BatchSlot*>(out + H->slots_off);
+  uint32_t* tokslot = reinterpret_cast<uint32_t*>(out + H->tokslot_off);
+  for (uint32_t t = 0; t < T; ++t)
+    for (int e = 0; e < 10; ++e) {
+      const uint16_t id = r->expert[t * 10 + e];
+      const uint32_t s = first[id] + fill[id]++;
+      slots[s].token = t;
+      slots[s].gate = r->gate[t * 11 + e];
+      tokslot[t * 10 + e] = s;
+    }
+  uint32_t k = 0;
+  for (int id = 0; id < kRouted; ++id)
+    for (uint32_t f = 0; f < count[id]; f += kTileTokens) {
+      BatchTile& B = tiles[k++];
+      B.expert = (uint32_t)id;
+      B.ntok = count[id] - f < (uint32_t)kTileTokens ? count[id] - f : (uint32_t)kTileTokens;
+      B.slot0 = first[id] + f;
+      B.pad = 0;
+    }
+  memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
+  *used = H->total;
+  E.sample.unique_experts = experts;
+  E.sample.pairs = ntiles * H->nblk;
+  E.sample.grid = ntiles;
+  E.sample.blocks = H->nblk;
+  E.sample.weight_bytes = (uint64_t)experts * H->nblk * l0->slice;
+  return FR_HIP_OK;
+}
+
+// Scratch of the prefill kernels, grown on demand (never inside a timed
+// region once warm: the sizes depend only on the token count).
+int batch_scratch(const BatchHeader& H) {
+  const size_t hb = (size_t)H.nslots * H.nblk * kNeurons * sizeof(float);
+  const size_t pb = (size_t)H.nslots * H.hidden * sizeof(float);
+  const size_t yb = (size_t)H.tokens * H.hidden * sizeof(float);
+  if (hb > E.bh_bytes) {
+    (void)hipFree(E.bh);
+    E.bh = nullptr;
+    E.bh_bytes = 0;
+    CK(hipMalloc(&E.bh, hb));
+    E.bh_bytes = hb;
+    ++E.sample.hot_allocations;
+  }
+  if (pb > E.bpart_bytes) {
+    (void)hipFree(E.bpart);
+    E.bpart = nullptr;
+    E.bpart_bytes = 0;
+    CK(hipMalloc(&E.bpart, pb));
+    E.bpart_bytes = pb;
+    ++E.sample.hot_allocations;
+  }
+  if (yb > E.by_bytes) {
+    (void)hipFree(E.by);
+    E.by = nullptr;
+    E.by_bytes = 0;
+    CK(hipMalloc(&E.by, yb));
+    E.by_bytes = yb;
+    ++E.sample.hot_allocations;
+  }
+  return FR_HIP_OK;
+}
+
+int batch_launch(const uint8_t* dev_plan, const BatchHeader& H, hipStream_t stream) {
+  if (!H.tokens || H.tokens > (unsigned)kMaxBatchTokens || !H.ntiles || !H.nblk || H.nblk > (unsigned)kBlocks ||
+      !H.hidden || H.hidden % 256 || H.hidden > (unsigned)kMaxHidden || H.nslots != 10 * H.tokens)
+    return FR_HIP_INVALID;
+  int rc = batch_scratch(H);
+  if (rc) return rc;
+  BatchScratch S;
+  S.h = E.bh;
+  S.part = E.bpart;
+  S.y = E.by;
+  S.status = E.bstatus;
+  hipEvent_t* te = E.timing && E.timed < E.timed_cap ? E.tev + 3 * E.timed++ : nullptr;
+  CK(hipMemsetAsync(E.bstatus, 0, sizeof(uint32_t), stream));
+  if (te) CK(hipEventRecord(te[0], stream));
+  const unsigned ncol = (H.hidden + kDownCols - 1) / kDownCols;
+  hipLaunchKernelGGL(prefill_gate_up, dim3(H.ntiles, H.nblk), dim3(kBatchThreads), 0, stream, dev_plan, S);
+  hipLaunchKernelGGL(prefill_down, dim3(H.ntiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S);
+  if (te) CK(hipEventRecord(te[1], stream));
+  hipLaunchKernelGGL(prefill_reduce, dim3(H.tokens, ncol), dim3(256), 0, stream, dev_plan, S);
+  if (te) CK(hipEventRecord(te[2], stream));
+  if (hipGetLastError() != hipSuccess) return FR_HIP_IO;
+  E.batch_tokens = H.tokens;
+  E.batch_hidden = H.hidden;
+  return FR_HIP_OK;
+}
+
+int batch_output(hipStream_t s, float* y, size_t count, unsigned* status_out) {
+  if (count > (size_t)E.batch_tokens * E.batch_hidden) return FR_HIP_INVALID;
+  uint32_t status = 0;
+  CK(hipMemcpyAsync(E.bstatus_host, E.bstatus, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  CK(hipStreamSynchronize(s));
+  status = *E.bstatus_host;
+  if (status_out) *status_out = status;
+  if (y && count && !status) CK(hipMemcpy(y, E.by, count * sizeof(float), hipMemcpyDeviceToHost));
+  return FR_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -2537,6 +2972,9 @@ int fr_hip_open(int device) {
   CK(hipMalloc(&E.plan_dev, E.plan_cap));
   CK(hipHostMalloc(reinterpret_cast<void**>(&E.plan_host), E.plan_cap, hipHostMallocDefault));
   CK(hipHostMalloc(reinterpret_cast<void**>(&E.out_host), (size_t)E.out_words * sizeof(uint32_t), hipHostMallocDefault));
+  CK(hipMalloc(&E.bstatus, sizeof(uint32_t)));
+  CK(hipMemset(E.bstatus, 0, sizeof(uint32_t)));
+  CK(hipHostMalloc(reinterpret_cast<void**>(&E.bstatus_host), sizeof(uint32_t), hipHostMallocDefault));
   CK(hipEventCreate(&E.ev0));
   CK(hipEventCreate(&E.ev1));
   CK(hipDeviceSynchronize());
@@ -2559,6 +2997,13 @@ int fr_hip_close(void) {
   (void)hipFree(E.bar);
   (void)hipFree(E.plan_dev);
   (void)hipFree(E.staging);
+  (void)hipFree(E.bh);
+  (void)hipFree(E.bpart);
+  (void)hipFree(E.by);
+  (void)hipFree(E.bstatus);
+  (void)hipFree(E.bplan_dev);
+  (void)hipHostFree(E.bplan_host);
+  (void)hipHostFree(E.bstatus_host);
   (void)hipHostFree(E.plan_host);
   (void)hipHostFree(E.out_host);
   (void)hipEventDestroy(E.ev0);
@@ -2750,6 +3195,63 @@ int fr_hip_run(const fr_hip_request* req, float* y) {
   if (status) return FR_HIP_NUMERIC;
   // y is written only on success: untouched on failure.
   memcpy(y, E.out_host + 4, count * sizeof(float));
+  return FR_HIP_OK;
+}
+
+size_t fr_hip_batch_plan_bytes(unsigned tokens, unsigned hidden) { return batch_capacity(tokens, hidden); }
+
+int fr_hip_batch_plan(const fr_hip_batch* req, void* plan, size_t cap, size_t* used) {
+  if (!g_open) return FR_HIP_STATE;
+  return build_batch(req, static_cast<uint8_t*>(plan), cap, used);
+}
+
+int fr_hip_batch_launch(const void* host_plan, const void* device_plan, void* stream) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!host_plan || !device_plan) return FR_HIP_INVALID;
+  CK(hipSetDevice(E.device));
+  return batch_launch(static_cast<const uint8_t*>(device_plan), *static_cast<const BatchHeader*>(host_plan),
+                      stream ? static_cast<hipStream_t>(stream) : E.stream);
+}
+
+int fr_hip_batch_output(void* stream, float* y, size_t count, unsigned* status) {
+  if (!g_open) return FR_HIP_STATE;
+  return batch_output(stream ? static_cast<hipStream_t>(stream) : E.stream, y, count, status);
+}
+
+int fr_hip_run_batch(const fr_hip_batch* req, float* y) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!req || !y) return FR_HIP_INVALID;
+  CK(hipSetDevice(E.device));
+  if (req->tokens > (unsigned)kMaxBatchTokens) return FR_HIP_INVALID;
+  const size_t need = batch_capacity(req->tokens, req->hidden);
+  if (need > E.bplan_cap) {
+    (void)hipFree(E.bplan_dev);
+    (void)hipHostFree(E.bplan_host);
+    E.bplan_dev = nullptr;
+    E.bplan_host = nullptr;
+    E.bplan_cap = 0;
+    CK(hipMalloc(&E.bplan_dev, need));
+    CK(hipHostMalloc(reinterpret_cast<void**>(&E.bplan_host), need, hipHostMallocDefault));
+    E.bplan_cap = need;
+  }
+  size_t used = 0;
+  int rc = build_batch(req, E.bplan_host, E.bplan_cap, &used);
+  if (rc) return rc;
+  const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(E.bplan_host);
+  CK(hipMemcpyAsync(E.bplan_dev, E.bplan_host, used, hipMemcpyHostToDevice, E.stream));
+  CK(hipEventRecord(E.ev0, E.stream));
+  rc = batch_launch(E.bplan_dev, H, E.stream);
+  if (rc) return rc;
+  CK(hipEventRecord(E.ev1, E.stream));
+  unsigned status = 0;
+  rc = batch_output(E.stream, nullptr, 0, &status);
+  if (rc) return rc;
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, E.ev0, E.ev1) == hipSuccess) E.sample.last_kernel_ns = ms * 1e6;
+  ++E.sample.runs;
+  if (status) return FR_HIP_NUMERIC;
+  // y is written only on success: untouched on failure.
+  CK(hipMemcpy(y, E.by, (size_t)H.tokens * H.hidden * sizeof(float), hipMemcpyDeviceToHost));
   return FR_HIP_OK;
 }
 

@@ -111,6 +111,34 @@ int fr_hip_last_output(void *stream, float *y, size_t count, unsigned *status);
 
 int fr_hip_sample_get(fr_hip_sample *out);
 
+/* Prefill chunk on matrix cores (config "resident node, 512-token prefill").
+ * The reference has no multi-token entry beyond run()'s burst of 8: its
+ * client cuts longer prompts into bursts (client/fronk_client.h:41-42) and
+ * every burst goes through run() (src/backend.h:63, backends/ref.c:57-98).
+ * This is fr_hip_run_batch, the extension the hot path's prefill needs: `tokens`
+ * tokens of one layer, each with its own routing, in one launch sequence that
+ * reads each routed expert's weights once for all of its tokens. Row t of y is
+ * run() of token t alone (same validation of ids, FR_NUMERIC rule), within
+ * the F32 tolerance. Supported: mode F32, every loaded block FR_HIP_FMT_Q4KT,
+ * routed experts only (gate[t][10] == 0; otherwise FR_HIP_UNSUPPORTED and the
+ * caller uses run()). tokens <= 4096. y receives tokens*hidden floats only on
+ * success. */
+typedef struct {
+    unsigned layer, tokens, hidden, mode;
+    const uint16_t *expert;  /* [tokens][10] distinct routed ids < 512 */
+    const float *gate;       /* [tokens][11], index 10 (shared) must be 0 */
+    const float *x;          /* [tokens][hidden] */
+} fr_hip_batch;
+int fr_hip_run_batch(const fr_hip_batch *req, float *y);
+/* Resident-input form of fr_hip_run_batch, like fr_hip_plan/fr_hip_launch:
+ * the plan (routing groups and x) is built on the host, copied by the caller
+ * to device memory it owns, and launched on `stream`; fr_hip_batch_output
+ * waits and reads the status word and y of the last batch launch. */
+size_t fr_hip_batch_plan_bytes(unsigned tokens, unsigned hidden);
+int fr_hip_batch_plan(const fr_hip_batch *req, void *plan, size_t cap, size_t *used);
+int fr_hip_batch_launch(const void *host_plan, const void *device_plan, void *stream);
+int fr_hip_batch_output(void *stream, float *y, size_t count, unsigned *status);
+
 /* Launch timing for measurement (no reference counterpart): after
  * fr_hip_timing(n), the next n launches record HIP events on their stream
  * before the main kernel, after it and after the launch's last kernel (a

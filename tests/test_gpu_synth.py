@@ -201,7 +201,7 @@ def test_decode_kernel_and_layer_kernel_agree_with_oracle(eng, hidden, monkeypat
             eng.release(b)
 
 
-@pytest.mark.parametrize("burst", [2, 4, 8])
+@pytest.mark.parametrize("burst", [2, 3, 4, 5, 8])
 def test_decode_burst_rows_equal_single_token_runs(eng, burst):
     """Bursts of all-Q4_K routed requests also run on the decode kernel: each
     (token, pair) is a unit with its own partial, and a token's units are
