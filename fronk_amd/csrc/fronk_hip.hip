@@ -2096,18 +2096,22 @@ __global__ void synth_kernel(uint8_t* __restrict__ dst, SliceShape routed, Slice
 // that of run() on token t alone (backends/ref.c:57-98). Here the tokens are
 // grouped by routed expert, so that each expert's weights are read once for
 // all of its tokens and the work is a contraction:
+//   prefill_digits   (token, super-block): x as exact int8 digits, once;
 //   prefill_gate_up  (tile, slice): a, u of up to 16 tokens over one slice's
-//                    32 neurons on fp32 matrix cores, then gate*SiLU(a)*u;
+//                    32 neurons on int8 matrix cores (exact integer dots),
+//                    then gate*SiLU(a)*u;
 //   prefill_down     (tile, 1024 outputs): the expert's down matrix over all
 //                    owned slices applied to the tile's h on fp32 matrix
 //                    cores, one fp32 partial per (token, expert);
 //   prefill_reduce   (token, 1024 outputs): the token's 10 expert partials
 //                    summed in its routing order in fp64, then narrowed with
 //                    the reference's rule (backends/ref.c:37-40, 95).
-// v_mfma_f32_16x16x4_f32 (A: lane l holds A[l%16][l/16]; B: B[l/16][l%16];
-// C: lane l holds C[4(l/16)+r][l%16]) takes one fp32 value per lane and
-// operand, so each lane dequantizes exactly the weight it contributes; the
-// Q4_K-T down, stored along the outputs, needs no transposition.
+// For the down, v_mfma_f32_16x16x4_f32 (A: lane l holds A[l%16][l/16]; B:
+// B[l/16][l%16]; C: lane l holds C[4(l/16)+r][l%16]) takes one fp32 value per
+// lane and operand, so each lane dequantizes exactly the weight it
+// contributes, and the Q4_K-T down, stored along the outputs, needs no
+// transposition. Its scales vary along both the neurons (the contraction) and
+// the outputs, which rules out folding them into integer operands.
 constexpr int kTileTokens = 16;          // tokens of one expert tile (the MFMA N)
 constexpr int kBatchThreads = 512;
 constexpr int kMaxBatchTokens = 4096;
@@ -2133,95 +2137,208 @@ struct BatchScratch {
   float* h;                              // [nslots][nblk * 32] gate * h
   float* part;                           // [nslots][hidden] per-(token, expert) partials
   float* y;                              // [tokens][hidden]
+  int8_t* dig;                           // [tokens][super-block][4 digits][256] x as integers
+  float* dscale;                         // [tokens][super-block] 2^e of the digits
+  float* dsum;                           // [tokens][super-block][8] sub-block sums of x
   uint32_t* status;
 };
 
+// x of the chunk as exact integers for the int8 matrix cores: per (token,
+// super-block), X = rint(x * 2^-e) with 2^e chosen so that |X| < 2^31 for the
+// super-block's largest magnitude, written as four signed base-256 digits
+// (X = ((d0*256 + d1)*256 + d2)*256 + d3, d1..d3 in [-128, 127]), plus 2^e
+// and the fp32 sum of each 32-value sub-block (for the min terms). The
+// digits keep 31 bits of the super-block's range, so the integer dots below
+// are those of x to within 2^-31 of its largest value.
+__global__ __launch_bounds__(256) void prefill_digits(const uint8_t* __restrict__ plan, BatchScratch S) {
+  const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
+  const unsigned t = blockIdx.x, sb = blockIdx.y, nsb = H.hidden / 256, v = threadIdx.x;
+  const float x = reinterpret_cast<const float*>(plan + H.x_off)[(size_t)t * H.hidden + 256 * sb + v];
+  __shared__ float red[4];
+  __shared__ uint32_t nonfinite;
+  if (v == 0) nonfinite = 0;
+  float m = fabsf(x);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float s = x;
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o, 64);   // the 32 values of a sub-block
+  __syncthreads();
+  if (!isfinite(x)) nonfinite = 1;
+  if ((v & 63) == 0) red[v >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const bool fin = nonfinite == 0;
+  int E = 0;
+  if (fin && m > 0.f) (void)frexpf(m, &E);                   // m < 2^E
+  const int e = max(E - 30, -149);
+  const int X = fin ? (int)rintf(ldexpf(x, -e)) : 0;          // |X| <= 2^30
+  const int d3 = ((X + 128) & 255) - 128, X1 = (X - d3) >> 8;
+  const int d2 = ((X1 + 128) & 255) - 128, X2 = (X1 - d2) >> 8;
+  const int d1 = ((X2 + 128) & 255) - 128, d0 = (X2 - d1) >> 8;
+  int8_t* dst = S.dig + ((size_t)t * nsb + sb) * 1024 + v;
+  dst[0] = (int8_t)d0;
+  dst[256] = (int8_t)d1;
+  dst[512] = (int8_t)d2;
+  dst[768] = (int8_t)d3;
+  if (v == 0) S.dscale[(size_t)t * nsb + sb] = ldexpf(1.f, e);
+  if ((v & 31) == 0) S.dsum[((size_t)t * nsb + sb) * 8 + v / 32] = s;
+  if (v == 0 && !fin) flag(S.status, kErrRange);   // a non-finite x makes the token's a and u non-finite
+}
+
+constexpr int kDigRow = 272;             // LDS bytes per (token, digit) row: 256 + 16 of padding
+
 struct GateUpLds {
-  float x[2][32][8][kTileTokens];        // [buffer][position][sub-block][token]: one super-block of x
-  f32x4 c[kDecodeWaves][64];             // each wavefront's C fragment
+  int8_t dig[2][kTileTokens * 4][kDigRow];   // [buffer][token * 4 + digit][position]
+  float scale[2][kTileTokens];               // 2^e of each token for the super-block
+  float xs[2][kTileTokens][8];               // sub-block sums
+  float main[kDecodeWaves][16][kTileTokens]; // [wave][row][token] integer-dot part
+  float mins[kDecodeWaves][16][kTileTokens]; // [wave][row][token] min part
 };
+
+// Bytes of v (each below 16) times s (below 8) in one packed 16-bit multiply:
+// every product is below 128, so no byte carries into the next.
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t v, uint32_t s) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 a = __builtin_bit_cast(u16x2, v), b = {(unsigned short)s, (unsigned short)s};
+  return __builtin_bit_cast(uint32_t, a * b);
+}
 
 // Workgroup (tile, slice): wavefront w takes row-block w%4 (gate rows of
 // neurons 8rb..8rb+7, then their up rows) and part w/4 (sub-blocks 0-3 or 4-7
 // of every super-block) of the TQ4_KM tiles; lane 16kg + i holds sub-block
-// 4p + kg of row i, which is exactly its A operand (row i, k = kg) for the 32
-// positions of the sub-block. x moves through LDS one super-block at a time,
-// double-buffered, the next one loaded while the current one is used.
-__global__ __launch_bounds__(kBatchThreads) void prefill_gate_up(const uint8_t* __restrict__ plan,
-                                                                 BatchScratch S) {
+// 4p + kg of row i. Per super-block the int8 matrix cores form, for row i and
+// column (token, digit), sum_k q_k * sc_k * X_k exactly: the 6-bit scale sc of
+// the lane's sub-block is folded into its A operand as sc = 8 sc_hi + sc_lo
+// (two operands q*sc_lo and q*sc_hi, both below 128), so the sum runs over the
+// whole super-block and is scaled once by d * 2^e * digit weight. The min
+// terms, sum_sub dmin * m_sub * sum(x_sub), take one fp32 MFMA per
+// super-block. The digits move through LDS one super-block at a time,
+// double-buffered.
+__global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_t* __restrict__ plan,
+                                                                    BatchScratch S) {
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
-  const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[blockIdx.x];
+  // Workgroups go round-robin over the 8 XCDs; each XCD takes a contiguous
+  // run of the (tile, slice) list, so that a tile's 20 slices read its x
+  // digits from one L2.
+  const unsigned nblk = H.nblk, per = gridDim.x / 8, b = blockIdx.x;
+  const unsigned j = b < 8 * per ? (b % 8) * per + b / 8 : b, brank = j % nblk;
+  const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[j / nblk];
   const BatchSlot* slots = reinterpret_cast<const BatchSlot*>(plan + H.slots_off) + T.slot0;
-  const float* xg = reinterpret_cast<const float*>(plan + H.x_off);
-  const unsigned hidden = H.hidden, nsb = hidden / 256, nblk = H.nblk, brank = blockIdx.y;
+  const unsigned hidden = H.hidden, nsb = hidden / 256;
   const uint8_t* slice = reinterpret_cast<const uint8_t*>(H.base[brank] + (uint64_t)T.expert * H.slice_bytes);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const unsigned rb = (unsigned)wave & 3, p = (unsigned)wave >> 2, kg = (unsigned)lane >> 4,
                  col = (unsigned)lane & 15;
   __shared__ __align__(16) GateUpLds L;
-  // x staging: thread -> token xn, positions 8*xq..8*xq+7 of the super-block.
-  const unsigned xn = (unsigned)tid >> 5, xq = (unsigned)tid & 31;
-  const bool xlive = xn < T.ntok;
-  const float* xrow = xg + (size_t)(xlive ? slots[xn].token : 0) * hidden + 8 * xq;
-  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 xr[2] = {z4, z4};
-  auto load_x = [&](unsigned s) {
-    if (xlive) {
-      xr[0] = *reinterpret_cast<const float4*>(xrow + 256 * (size_t)s);
-      xr[1] = *reinterpret_cast<const float4*>(xrow + 256 * (size_t)s + 4);
+  // Staging: thread -> token tl, 32-byte piece c of its 1 KB of digits.
+  const unsigned tl = (unsigned)tid >> 5, c = (unsigned)tid & 31;
+  const bool live = tl < T.ntok;
+  const size_t trow = (size_t)(live ? slots[tl].token : 0) * nsb;
+  const int8_t* dsrc = S.dig + trow * 1024 + 32 * c;
+  const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+  uint4 dr[2] = {z4, z4};
+  float sr = 0.f;
+  auto load_d = [&](unsigned s) {
+    if (live) {
+      dr[0] = *reinterpret_cast<const uint4*>(dsrc + 1024 * (size_t)s);
+      dr[1] = *reinterpret_cast<const uint4*>(dsrc + 1024 * (size_t)s + 16);
+      sr = c < 8 ? S.dsum[(trow + s) * 8 + c] : c == 8 ? S.dscale[trow + s] : 0.f;
     }
   };
-  auto store_x = [&](unsigned buf) {
-    const float v[8] = {xr[0].x, xr[0].y, xr[0].z, xr[0].w, xr[1].x, xr[1].y, xr[1].z, xr[1].w};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) L.x[buf][8 * (xq & 3) + j][xq >> 2][xn] = v[j];
+  auto store_d = [&](unsigned buf) {
+    int8_t* row = &L.dig[buf][4 * tl + c / 8][32 * (c % 8)];
+    *reinterpret_cast<uint4*>(row) = dr[0];
+    *reinterpret_cast<uint4*>(row + 16) = dr[1];
+    if (c < 8) L.xs[buf][tl][c] = sr;
+    else if (c == 8) L.scale[buf][tl] = sr;
   };
   const uint8_t* wq = slice + 1024 + 2048 * rb + 1024 * p + 16 * (unsigned)lane;   // + 9216 s
   const uint8_t* wh = slice + 256 * rb + 16 * col;
+  const float wdig[4] = {16777216.f, 65536.f, 256.f, 1.f};
   uint32_t bad = 0;
-  load_x(0);
+  load_d(0);
   uint4 q = ld16(wq), hd = ld16(wh);
-  store_x(0);
+  store_d(0);
   __syncthreads();
-  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  float acc[4][4];
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t4][r] = 0.f;
+  f32x4 cmin = {0.f, 0.f, 0.f, 0.f};
   for (unsigned s = 0; s < nsb; ++s) {
     const unsigned buf = s & 1;
     const uint4 qc = q, hc = hd;
     if (s + 1 < nsb) {
-      load_x(s + 1);
+      load_d(s + 1);
       q = ld16(wq + 9216 * (size_t)(s + 1));
       hd = ld16(wh + 9216 * (size_t)(s + 1));
     }
     uint32_t sc, mi;
     q4k_scale_min(hc.y, hc.z, hc.w, 4 * p + kg, sc, mi);
     if (half_bad(hc.x) || half_bad(hc.x >> 16)) bad |= kErrScale;
-    const float D = half_to_float(hc.x & 0xffff) * (float)sc * kFp8Nibble;   // nibbles arrive as q * 2^-9
-    const float M = half_to_float(hc.x >> 16) * (float)mi;
-    const float* xb = &L.x[buf][0][4 * p + kg][col];
+    const float d = half_to_float(hc.x & 0xffff);
+    // A operands: positions 16hh..16hh+15 of the lane's sub-block, times
+    // sc_lo and sc_hi.
+    i32x4 a_lo[2], a_hi[2];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      // Word u: low nibbles = positions 8u..8u+3, high nibbles 8u+4..8u+7.
-      const uint32_t w = word(qc, u), lo = nib_lo(w), hi = nib_hi(w);
-      const float2 l0 = nib_pair<false>(lo), l1 = nib_pair<true>(lo), h0 = nib_pair<false>(hi),
-                   h1 = nib_pair<true>(hi);
-      const float a[8] = {l0.x, l0.y, l1.x, l1.y, h0.x, h0.y, h1.x, h1.y};
+    for (int hh = 0; hh < 2; ++hh) {
+      const uint32_t w0 = hh ? qc.z : qc.x, w1 = hh ? qc.w : qc.y;
+      const uint32_t b[4] = {nib_lo(w0), nib_hi(w0), nib_lo(w1), nib_hi(w1)};
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        c = __builtin_amdgcn_mfma_f32_16x16x4f32(fmaf(a[j], D, -M), xb[(8 * u + j) * 8 * kTileTokens], c, 0, 0, 0);
+      for (int j = 0; j < 4; ++j) {
+        a_lo[hh][j] = (int)mul_bytes(b[j], sc & 7u);
+        a_hi[hh][j] = (int)mul_bytes(b[j], sc >> 3);
+      }
     }
-    if (s + 1 < nsb) store_x(buf ^ 1);
+    // d of the C rows 4(l/16)+r (lanes 0..15 hold rows 0..15).
+    float drow[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) drow[r] = __shfl(d, (int)(4 * kg) + r, 64);
+    const int8_t* db = &L.dig[buf][0][32 * (4 * p + kg)];
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) {
+      i32x4 c_lo = {0, 0, 0, 0}, c_hi = {0, 0, 0, 0};
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(db + (16 * t4 + col) * kDigRow + 16 * hh);
+        const i32x4 bb = {(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w};
+        c_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_lo[hh], bb, c_lo, 0, 0, 0);
+        c_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_hi[hh], bb, c_hi, 0, 0, 0);
+      }
+      // Column col = 4 * token + digit of this N-tile.
+      const float fx = L.scale[buf][4 * t4 + (col >> 2)] * wdig[col & 3];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t4][r] = fmaf((float)(c_lo[r] + 8 * c_hi[r]), drow[r] * fx, acc[t4][r]);
+    }
+    // Min terms: A = -dmin * m of the lane's (row, sub-block), B = the
+    // sub-block sum of token col.
+    cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-half_to_float(hc.x >> 16) * (float)mi, L.xs[buf][col][4 * p + kg],
+                                                cmin, 0, 0, 0);
+    if (s + 1 < nsb) store_d(buf ^ 1);
     __syncthreads();
   }
-  L.c[wave][lane] = c;
+  // Digits of a (row, token) are the 4 neighbouring columns: sum them.
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = acc[t4][r];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      if ((col & 3) == 0) L.main[wave][4 * kg + r][4 * t4 + (col >> 2)] = v;
+    }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) L.mins[wave][4 * kg + r][col] = cmin[r];
   __syncthreads();
   // Thread -> (row-block, neuron i, token n): a = gate row i, u = up row 8+i,
-  // each the sum of the two parts in a fixed order.
+  // each (integer part + min part) of part 0, then of part 1.
   {
     const unsigned trb = (unsigned)tid >> 7, i = ((unsigned)tid >> 4) & 7, n = (unsigned)tid & 15;
-    const float* c0 = reinterpret_cast<const float*>(&L.c[trb][0]);
-    const float* c1 = reinterpret_cast<const float*>(&L.c[trb + 4][0]);
-    const unsigned ga = 4 * (16 * (i >> 2) + n) + (i & 3), ua = 4 * (16 * (2 + (i >> 2)) + n) + (i & 3);
-    const float a = c0[ga] + c1[ga], u = c0[ua] + c1[ua];
+    const float a = (L.main[trb][i][n] + L.mins[trb][i][n]) + (L.main[trb + 4][i][n] + L.mins[trb + 4][i][n]);
+    const float u = (L.main[trb][8 + i][n] + L.mins[trb][8 + i][n]) +
+                    (L.main[trb + 4][8 + i][n] + L.mins[trb + 4][8 + i][n]);
     if (n < T.ntok) {
       uint32_t hb = 0;
       const float h = slots[n].gate * silu_mul_f32(a, u, hb);
@@ -2234,6 +2351,7 @@ __global__ __launch_bounds__(kBatchThreads) void prefill_gate_up(const uint8_t* 
 
 struct DownLds {
   float h[kBlocks][4][kTileTokens][8];   // [slice][round q][token][neuron 8q + i of the slice]
+  float2 tab[kDecodeWaves][2][4][8][4];  // [wave][slice parity][q][i][sub-block]: (d*sc*2^9, dmin*m)
 };
 
 // Workgroup (tile, 1024 outputs): wavefront w takes the 128 outputs
@@ -2242,7 +2360,7 @@ struct DownLds {
 // of round q (neurons 8q..8q+7; outputs 4 per unit) and the 8 neuron headers
 // of the round; the MFMA (unit u, neuron i, output c4) has k = q (neuron
 // 8q + i), m -> output 128hb + 64u + 4m + c4 and n = token.
-__global__ __launch_bounds__(kBatchThreads) void prefill_down(const uint8_t* __restrict__ plan, BatchScratch S) {
+__global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* __restrict__ plan, BatchScratch S) {
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
   const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[blockIdx.x];
   const unsigned hidden = H.hidden, nsb = hidden / 256, nblk = H.nblk;
@@ -2258,36 +2376,38 @@ __global__ __launch_bounds__(kBatchThreads) void prefill_down(const uint8_t* __r
   if (sb >= nsb) return;
   const unsigned m = (unsigned)lane & 15, q = (unsigned)lane >> 4, n = m;
   const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * H.proj + 4608 * (uint64_t)sb;
-  const uint32_t u0 = 1024 * q + 16 * (32 * hb + m), u1 = u0 + 16 * 16, hoff = 4096 + 128 * q;
-  const uint32_t g0 = 4 * hb + m / 8, g1 = g0 + 2;   // sub-blocks of the two units' outputs
+  const uint32_t u0 = 1024 * q + 16 * (32 * hb + m), u1 = u0 + 16 * 16;
+  // Header decoding: lane l reads neuron l%32's header and forms the scales
+  // of sub-blocks 4hb + 2(l/32) and +1 of the wavefront's outputs.
+  const unsigned hn = (unsigned)lane & 31, hg = 2 * ((unsigned)lane >> 5);
+  const uint32_t hoff = 4096 + 16 * hn;
   uint32_t bad = 0;
   f32x4 acc[2][4];
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) acc[u][c4] = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint4 U[2], hd[8];
+  uint4 U[2], hdr;
   auto load = [&](unsigned R) {
     const uint8_t* d = reinterpret_cast<const uint8_t*>(H.base[R] + eoff);
     U[0] = ld16(d + u0);
     U[1] = ld16(d + u1);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) hd[i] = ld16(d + hoff + 16 * i);
+    hdr = ld16(d + hoff);
   };
   load(0);
   for (unsigned R = 0; R < nblk; ++R) {
-    const uint4 Uc[2] = {U[0], U[1]};
-    float D[2][8], M[2][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      bool ok0, ok1;
-      hdr_dm(hd[i], g0, D[0][i], M[0][i], ok0);
-      hdr_dm(hd[i], g1, D[1][i], M[1][i], ok1);
-      if (!ok0) bad |= kErrScale;
-      D[0][i] *= kFp8Nibble;
-      D[1][i] *= kFp8Nibble;
-    }
+    const uint4 Uc[2] = {U[0], U[1]}, hc = hdr;
     if (R + 1 < nblk) load(R + 1);
+    float2* tab = &L.tab[wave][R & 1][0][0][0];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float D, M;
+      bool ok;
+      hdr_dm(hc, 4 * hb + hg + j, D, M, ok);
+      if (!ok) bad |= kErrScale;
+      tab[4 * hn + hg + j] = make_float2(D * kFp8Nibble, M);
+    }
+    __builtin_amdgcn_wave_barrier();
     const float4 hv0 = *reinterpret_cast<const float4*>(&L.h[R][q][n][0]);
     const float4 hv1 = *reinterpret_cast<const float4*>(&L.h[R][q][n][4]);
     const float hv[8] = {hv0.x, hv0.y, hv0.z, hv0.w, hv1.x, hv1.y, hv1.z, hv1.w};
@@ -2295,6 +2415,7 @@ __global__ __launch_bounds__(kBatchThreads) void prefill_down(const uint8_t* __r
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
+        const float2 dm = tab[4 * (8 * q + i) + 2 * u + m / 8];
         // Dword i/2: neurons 8q+2(i/2) (bytes 0,1) and 8q+2(i/2)+1 (bytes 2,3);
         // low nibbles outputs 0 and 2, high nibbles outputs 1 and 3.
         const uint32_t w = word(Uc[u], i >> 1), lo = nib_lo(w), hi = nib_hi(w);
@@ -2303,8 +2424,7 @@ __global__ __launch_bounds__(kBatchThreads) void prefill_down(const uint8_t* __r
         const float a[4] = {lv.x, hv2.x, lv.y, hv2.y};
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4)
-          acc[u][c4] = __builtin_amdgcn_mfma_f32_16x16x4f32(fmaf(a[c4], D[u][i], -M[u][i]), hv[i], acc[u][c4], 0,
-                                                            0, 0);
+          acc[u][c4] = __builtin_amdgcn_mfma_f32_16x16x4f32(fmaf(a[c4], dm.x, -dm.y), hv[i], acc[u][c4], 0, 0, 0);
       }
   }
   // Lane l holds rows 4(l/16) + r (outputs 128hb + 64u + 4(4(l/16) + r) + c4)
@@ -2494,7 +2614,8 @@ struct Engine {
   float* bh = nullptr;
   float* bpart = nullptr;
   float* by = nullptr;
-  size_t bh_bytes = 0, bpart_bytes = 0, by_bytes = 0;
+  uint8_t* bdig = nullptr;            // digits, then 2^e, then sub-block sums
+  size_t bh_bytes = 0, bpart_bytes = 0, by_bytes = 0, bdig_bytes = 0;
   uint32_t* bstatus = nullptr;
   uint32_t* bstatus_host = nullptr;   // pinned
   uint8_t* bplan_dev = nullptr;
@@ -2877,6 +2998,15 @@ int batch_scratch(const BatchHeader& H) {
     E.bpart_bytes = pb;
     ++E.sample.hot_allocations;
   }
+  const size_t db = (size_t)H.tokens * (H.hidden / 256) * (1024 + 9 * sizeof(float));
+  if (db > E.bdig_bytes) {
+    (void)hipFree(E.bdig);
+    E.bdig = nullptr;
+    E.bdig_bytes = 0;
+    CK(hipMalloc(&E.bdig, db));
+    E.bdig_bytes = db;
+    ++E.sample.hot_allocations;
+  }
   if (yb > E.by_bytes) {
     (void)hipFree(E.by);
     E.by = nullptr;
@@ -2898,12 +3028,17 @@ int batch_launch(const uint8_t* dev_plan, const BatchHeader& H, hipStream_t stre
   S.h = E.bh;
   S.part = E.bpart;
   S.y = E.by;
+  const size_t nd = (size_t)H.tokens * (H.hidden / 256);
+  S.dig = reinterpret_cast<int8_t*>(E.bdig);
+  S.dscale = reinterpret_cast<float*>(E.bdig + nd * 1024);
+  S.dsum = S.dscale + nd;
   S.status = E.bstatus;
   hipEvent_t* te = E.timing && E.timed < E.timed_cap ? E.tev + 3 * E.timed++ : nullptr;
   CK(hipMemsetAsync(E.bstatus, 0, sizeof(uint32_t), stream));
   if (te) CK(hipEventRecord(te[0], stream));
   const unsigned ncol = (H.hidden + kDownCols - 1) / kDownCols;
-  hipLaunchKernelGGL(prefill_gate_up, dim3(H.ntiles, H.nblk), dim3(kBatchThreads), 0, stream, dev_plan, S);
+  hipLaunchKernelGGL(prefill_digits, dim3(H.tokens, H.hidden / 256), dim3(256), 0, stream, dev_plan, S);
+  hipLaunchKernelGGL(prefill_gate_up, dim3(H.ntiles * H.nblk), dim3(kBatchThreads), 0, stream, dev_plan, S);
   hipLaunchKernelGGL(prefill_down, dim3(H.ntiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S);
   if (te) CK(hipEventRecord(te[1], stream));
   hipLaunchKernelGGL(prefill_reduce, dim3(H.tokens, ncol), dim3(256), 0, stream, dev_plan, S);
@@ -3000,6 +3135,7 @@ int fr_hip_close(void) {
   (void)hipFree(E.bh);
   (void)hipFree(E.bpart);
   (void)hipFree(E.by);
+  (void)hipFree(E.bdig);
   (void)hipFree(E.bstatus);
   (void)hipFree(E.bplan_dev);
   (void)hipHostFree(E.bplan_host);
