@@ -2256,6 +2256,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
   const uint8_t* wq = slice + 1024 + 2048 * rb + 1024 * p + 16 * (unsigned)lane;   // + 9216 s
   const uint8_t* wh = slice + 256 * rb + 16 * col;
   const float wdig[4] = {16777216.f, 65536.f, 256.f, 1.f};
+  const unsigned nt4 = (T.ntok + 3) / 4;   // N-tiles of 4 tokens in use
   uint32_t bad = 0;
   load_d(0);
   uint4 q = ld16(wq), hd = ld16(wh);
@@ -2299,6 +2300,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     const int8_t* db = &L.dig[buf][0][32 * (4 * p + kg)];
 #pragma unroll
     for (int t4 = 0; t4 < 4; ++t4) {
+      if ((unsigned)t4 >= nt4) break;   // N-tiles past the tile's tokens hold zeros only
       i32x4 c_lo = {0, 0, 0, 0}, c_hi = {0, 0, 0, 0};
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
@@ -2324,6 +2326,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
   for (int t4 = 0; t4 < 4; ++t4)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      if ((unsigned)t4 >= nt4) break;
       float v = acc[t4][r];
       v += __shfl_xor(v, 1, 64);
       v += __shfl_xor(v, 2, 64);
