@@ -287,6 +287,11 @@ def bench_prefill(args):
     flops = PREFILL_LAYERS * 2.0 * PREFILL_TOKENS * 10 * SLICES * 3 * 32 * HIDDEN   # useful multiply-adds x 2
     tflops = flops / (chunk_ms * 1e-3) / 1e12
 
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "prefill_traffic.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+
     cpu = None
     if not args.no_cpu:
         layer, experts, gates, x = reqs[0]
@@ -320,8 +325,9 @@ def bench_prefill(args):
                             "note": "per layer launch, events on the launch stream, one extra chunk"},
         "weight_bytes_per_chunk": float(wts.sum()),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "prefill_gate_up + prefill_down + prefill_reduce"},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_note": "HBM bytes per layer launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                     "kernel": "prefill_digits + prefill_gate_up + prefill_down + prefill_reduce per layer"},
         "mfma": {"achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s (fp32 matrix)",
                  "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4)},
         "cpu_baseline": cpu,
