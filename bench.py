@@ -335,6 +335,72 @@ def bench_prefill(args):
     print(json.dumps(out), flush=True)
 
 
+def avx2_reference_baseline(budget_s, workers=16):
+    """The reference's own AVX2 backend (backends/avx2.c, the fr_avx2 vtable),
+    compiled from its sources into oracle/_ref, run multi-threaded on the host
+    cores. The reference fixes H = 2560 (src/model.h:16), so the sample is the
+    same layer-share shape at that width in its native format (Q4_K gate/up,
+    MXFP4 down): 10 of 512 experts uniform, 20 owned slices, one token per
+    call; GB/s = routed slice bytes per call / time. None when oracle/_ref is
+    absent."""
+    import oracle
+    from fixtures import slice_view, sparse_unit
+    import vtable
+    if not os.path.exists(oracle.REF_PATH):
+        return None
+    ref = C.CDLL(oracle.REF_PATH, mode=C.RTLD_GLOBAL)
+    vt = vtable.Backend.in_dll(ref, "fr_avx2")
+    ref.fr_avx2_set_tuning(C.c_uint(SLICES), C.c_uint(1), C.c_uint(workers), C.c_uint(0))
+    if ref.fr_avx2_configure(C.c_uint(SLICES), C.c_uint(1)) != 0:
+        return None
+    H = vtable.HIDDEN
+    lay = oracle.layout(H, oracle.FMT_NATIVE)
+    rng = np.random.default_rng(SEED + 9)
+    calls = 48
+    routes = [rng.choice(512, 10, replace=False).astype(np.uint16) for _ in range(calls)]
+    used = sorted(set(int(e) for r in routes for e in r))
+    units = []
+    for b in range(SLICES):
+        u = sparse_unit(lay)
+        for e in used:
+            slice_view(u, lay, 0, e)[:] = oracle.synth_slice(lay, SEED, b, 0, e)
+        units.append(u)
+    for b in range(SLICES):
+        if vt.load(b, units[b].ctypes.data, lay.block) != 0:
+            raise RuntimeError("fr_avx2 load failed")
+    reqs = []
+    for r in routes:
+        q = vtable.Req()
+        q.layer, q.burst = 0, 1
+        for j in range(10):
+            q.expert[0][j] = int(r[j])
+        g = softmax_gates(rng, 1)[0]
+        for j in range(11):
+            q.gate[0][j] = float(g[j])
+        xs = rng.standard_normal(H).astype(np.float32)
+        C.memmove(q.x[0], xs.ctypes.data, 4 * H)
+        reqs.append(q)
+    part = vtable.Part()
+    for q in reqs[:4]:
+        if vt.run(C.byref(q), C.byref(part)) != 0:
+            raise RuntimeError("fr_avx2 run failed")
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        if vt.run(C.byref(reqs[n % calls]), C.byref(part)) != 0:
+            raise RuntimeError("fr_avx2 run failed")
+        n += 1
+    seconds = time.perf_counter() - t0
+    for b in range(SLICES):
+        vt.unload(b)
+    ref.fr_avx2_close()
+    return {"value": n * 10 * SLICES * lay.slice / seconds / 1e9, "unit": "GB/s", "cores": workers,
+            "kind": "reference",
+            "sample": f"{n} calls of a 10-of-512, 20-slice native layer share at H={H} (the reference's fixed "
+                      f"width; Q4_K gate/up, MXFP4 down) through backends/avx2.c built from the reference sources, "
+                      f"{workers} worker threads, {seconds:.1f} s",
+            "us_per_call": seconds / n * 1e6}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -458,10 +524,11 @@ def main():
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
 
-    cpu = None
+    cpu = avx2 = None
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "tests"))
         cpu = cpu_baseline(fa, eng, fmt, reqs[args.warmup:], args.cpu_seconds)
+        avx2 = avx2_reference_baseline(min(args.cpu_seconds, 6.0))
 
     for b in range(SLICES):
         eng.release(b)
@@ -496,6 +563,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": grid_kernels(lib, host[args.warmup])},
         "cpu_baseline": cpu,
+        "cpu_reference_avx2": avx2,
     }
     print(json.dumps(out), flush=True)
 
