@@ -2352,17 +2352,41 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
   if (bad) flag(S.status, bad);
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
 struct DownLds {
   float h[kBlocks][4][kTileTokens][8];   // [slice][round q][token][neuron 8q + i of the slice]
-  float2 tab[kDecodeWaves][2][4][8][4];  // [wave][slice parity][q][i][sub-block]: (d*sc*2^9, dmin*m)
+  // [wave][slice parity][18 q + 8 g + i]: (d*sc, dmin*m) of neuron 8q + i for
+  // the pass's sub-block g; the stride of 18 puts the four rounds of a read
+  // in different banks and keeps 16-byte reads aligned.
+  float2 tab[kDecodeWaves][2][4 * 18];
 };
 
+// v as three bf16 values whose sum is v exactly (8 + 8 + 8 significant bits,
+// each residual exact in fp32).
+__device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& b1, bf16x8& b2, bf16x8& b3) {
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    b1[j] = (__bf16)v[j];
+    r[j] = v[j] - (float)b1[j];
+    b2[j] = (__bf16)r[j];
+    r[j] -= (float)b2[j];
+    b3[j] = (__bf16)r[j];
+  }
+}
+
 // Workgroup (tile, 1024 outputs): wavefront w takes the 128 outputs
-// 256 sb + 128 hb .. +127 (sb = 4 blockIdx.y + w/2, hb = w%2). Lane (m, q)
-// loads, per owned slice, the 16-byte Q4_K-T units 32hb + m and 32hb + 16 + m
-// of round q (neurons 8q..8q+7; outputs 4 per unit) and the 8 neuron headers
-// of the round; the MFMA (unit u, neuron i, output c4) has k = q (neuron
-// 8q + i), m -> output 128hb + 64u + 4m + c4 and n = token.
+// 256 sb + 128 hb .. +127 (sb = 4 blockIdx.y + w/2, hb = w%2), in two passes
+// of 64. On v_mfma_f32_16x16x32_bf16 the contraction runs over the 32
+// neurons of a slice (lane group kq: neurons 8kq..8kq+7) with:
+//   A[output][neuron] = 16 + q, exact in bf16 (bits 0x4180 | q << 3), built
+//     from the Q4_K-T unit that holds the lane's output (4 outputs x 8
+//     neurons per 16-byte unit);
+//   B[neuron][token]  = h * d * sc of the output's sub-block, split into
+//     three bf16 parts that sum to it exactly (three MFMAs);
+// so C = sum (16 + q) h d sc, and the fp32 correction sum h (16 d sc + dmin m)
+// per (sub-block, token) leaves sum (d sc q - dmin m) h.
 __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* __restrict__ plan, BatchScratch S) {
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
   const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[blockIdx.x];
@@ -2377,69 +2401,104 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
   __syncthreads();
   const unsigned sb = 4 * blockIdx.y + ((unsigned)wave >> 1), hb = (unsigned)wave & 1;
   if (sb >= nsb) return;
-  const unsigned m = (unsigned)lane & 15, q = (unsigned)lane >> 4, n = m;
+  const unsigned m = (unsigned)lane & 15, kq = (unsigned)lane >> 4, n = m, c4 = m & 3;
   const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * H.proj + 4608 * (uint64_t)sb;
-  const uint32_t u0 = 1024 * q + 16 * (32 * hb + m), u1 = u0 + 16 * 16;
-  // Header decoding: lane l reads neuron l%32's header and forms the scales
-  // of sub-blocks 4hb + 2(l/32) and +1 of the wavefront's outputs.
-  const unsigned hn = (unsigned)lane & 31, hg = 2 * ((unsigned)lane >> 5);
+  // Header decoding: lane l forms the scales of neuron l%32 for the pass's
+  // sub-block l/32.
+  const unsigned hn = (unsigned)lane & 31, hgg = (unsigned)lane >> 5;
   const uint32_t hoff = 4096 + 16 * hn;
   uint32_t bad = 0;
-  f32x4 acc[2][4];
+  for (unsigned ph = 0; ph < 2; ++ph) {
+    // Unit of M-tile t (outputs 128hb + 64ph + 16t .. +15): lane m's output
+    // lies in unit 32hb + 16ph + 4t + m/4 of round kq, at column m%4.
+    const uint32_t ubase = 1024 * kq + 16 * (32 * hb + 16 * ph + (m >> 2));
+    struct DnBytes {
+      uint4 u[4], h;
+    };
+    auto load = [&](unsigned R) {
+      const uint8_t* d = reinterpret_cast<const uint8_t*>(H.base[min(R, nblk - 1)] + eoff);
+      DnBytes B;
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
+      for (int t = 0; t < 4; ++t) B.u[t] = ld16(d + ubase + 64 * t);
+      B.h = ld16(d + hoff);
+      return B;
+    };
+    f32x4 acc[4];
 #pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) acc[u][c4] = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint4 U[2], hdr;
-  auto load = [&](unsigned R) {
-    const uint8_t* d = reinterpret_cast<const uint8_t*>(H.base[R] + eoff);
-    U[0] = ld16(d + u0);
-    U[1] = ld16(d + u1);
-    hdr = ld16(d + hoff);
-  };
-  load(0);
-  for (unsigned R = 0; R < nblk; ++R) {
-    const uint4 Uc[2] = {U[0], U[1]}, hc = hdr;
-    if (R + 1 < nblk) load(R + 1);
-    float2* tab = &L.tab[wave][R & 1][0][0][0];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float D, M;
-      bool ok;
-      hdr_dm(hc, 4 * hb + hg + j, D, M, ok);
-      if (!ok) bad |= kErrScale;
-      tab[4 * hn + hg + j] = make_float2(D * kFp8Nibble, M);
-    }
-    __builtin_amdgcn_wave_barrier();
-    const float4 hv0 = *reinterpret_cast<const float4*>(&L.h[R][q][n][0]);
-    const float4 hv1 = *reinterpret_cast<const float4*>(&L.h[R][q][n][4]);
-    const float hv[8] = {hv0.x, hv0.y, hv0.z, hv0.w, hv1.x, hv1.y, hv1.z, hv1.w};
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float2 dm = tab[4 * (8 * q + i) + 2 * u + m / 8];
-        // Dword i/2: neurons 8q+2(i/2) (bytes 0,1) and 8q+2(i/2)+1 (bytes 2,3);
-        // low nibbles outputs 0 and 2, high nibbles outputs 1 and 3.
-        const uint32_t w = word(Uc[u], i >> 1), lo = nib_lo(w), hi = nib_hi(w);
-        const float2 lv = (i & 1) ? nib_pair<true>(lo) : nib_pair<false>(lo);
-        const float2 hv2 = (i & 1) ? nib_pair<true>(hi) : nib_pair<false>(hi);
-        const float a[4] = {lv.x, hv2.x, lv.y, hv2.y};
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4)
-          acc[u][c4] = __builtin_amdgcn_mfma_f32_16x16x4f32(fmaf(a[c4], dm.x, -dm.y), hv[i], acc[u][c4], 0, 0, 0);
+    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float corr[2] = {0.f, 0.f};
+    DnBytes nxt = load(0);
+    for (unsigned R = 0; R < nblk; ++R) {
+      const DnBytes cur = nxt;
+      nxt = load(R + 1);
+      float2* tab = &L.tab[wave][R & 1][0];
+      {
+        float D, M;
+        bool ok;
+        hdr_dm(cur.h, 4 * hb + 2 * ph + hgg, D, M, ok);
+        if (!ok) bad |= kErrScale;
+        tab[18 * (hn >> 3) + 8 * hgg + (hn & 7)] = make_float2(D, M);
       }
-  }
-  // Lane l holds rows 4(l/16) + r (outputs 128hb + 64u + 4(4(l/16) + r) + c4)
-  // of token l%16.
-  if (n < T.ntok) {
-    float* dst = S.part + (size_t)(T.slot0 + n) * hidden + 256 * sb + 128 * hb;
+      __builtin_amdgcn_wave_barrier();
+      const float4 hv0 = *reinterpret_cast<const float4*>(&L.h[R][kq][n][0]);
+      const float4 hv1 = *reinterpret_cast<const float4*>(&L.h[R][kq][n][4]);
+      const float hv[8] = {hv0.x, hv0.y, hv0.z, hv0.w, hv1.x, hv1.y, hv1.z, hv1.w};
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+      for (int gg = 0; gg < 2; ++gg) {
+        const float4* tp = reinterpret_cast<const float4*>(&tab[18 * kq + 8 * gg]);
+        float D[8], M[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<float4*>(dst + 64 * u + 4 * (4 * q + r)) =
-            make_float4(acc[u][0][r], acc[u][1][r], acc[u][2][r], acc[u][3][r]);
+        for (int j2 = 0; j2 < 4; ++j2) {
+          const float4 dm = tp[j2];
+          D[2 * j2] = dm.x;
+          M[2 * j2] = dm.y;
+          D[2 * j2 + 1] = dm.z;
+          M[2 * j2 + 1] = dm.w;
+        }
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          v[j] = hv[j] * D[j];
+          corr[gg] = fmaf(hv[j], fmaf(16.f, D[j], M[j]), corr[gg]);
+        }
+        bf16x8 b1, b2, b3;
+        split_bf16(v, b1, b2, b3);
+        bf16x8 a[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          // Dword w of the unit: neurons 8kq+2w (low half) and 8kq+2w+1 (high
+          // half), nibble c4 of each half -> bf16 16 + q in each half.
+          u32x4 aw;
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            aw[w] = 0x41804180u | (((word(cur.u[2 * gg + tt], w) >> (4 * c4)) & 0x000F000Fu) << 3);
+          a[tt] = __builtin_bit_cast(bf16x8, aw);
+        }
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[2 * gg + tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tt], b3, acc[2 * gg + tt], 0, 0, 0);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[2 * gg + tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tt], b2, acc[2 * gg + tt], 0, 0, 0);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[2 * gg + tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tt], b1, acc[2 * gg + tt], 0, 0, 0);
+      }
+    }
+    // The correction of token n over all 32 neurons: sum the four rounds.
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      corr[gg] += __shfl_xor(corr[gg], 16, 64);
+      corr[gg] += __shfl_xor(corr[gg], 32, 64);
+    }
+    // Lane l holds rows 4(l/16) + r (outputs 128hb + 64ph + 16t + 4(l/16) + r)
+    // of token l%16.
+    if (n < T.ntok) {
+      float* dst = S.part + (size_t)(T.slot0 + n) * hidden + 256 * sb + 128 * hb + 64 * ph + 4 * kq;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float c = corr[t >> 1];
+        *reinterpret_cast<float4*>(dst + 16 * t) =
+            make_float4(acc[t][0] - c, acc[t][1] - c, acc[t][2] - c, acc[t][3] - c);
+      }
+    }
   }
   if (bad) flag(S.status, bad);
 }
