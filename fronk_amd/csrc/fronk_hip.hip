@@ -2096,13 +2096,14 @@ __global__ void synth_kernel(uint8_t* __restrict__ dst, SliceShape routed, Slice
 // that of run() on token t alone (backends/ref.c:57-98). Here the tokens are
 // grouped by routed expert, so that each expert's weights are read once for
 // all of its tokens and the work is a contraction:
-//   prefill_digits   (token, super-block): x as exact int8 digits, once;
+//   prefill_split    (token): x as two f16 parts of x * 2^-e, once;
 //   prefill_gate_up  (tile, slice): a, u of up to 16 tokens over one slice's
-//                    32 neurons on int8 matrix cores (exact integer dots),
-//                    then gate*SiLU(a)*u;
+//                    32 neurons on f16 matrix cores (operands exact), then
+//                    gate*SiLU(a)*u;
 //   prefill_down     (tile, 1024 outputs): the expert's down matrix over all
-//                    owned slices applied to the tile's h on fp32 matrix
-//                    cores, one fp32 partial per (token, expert);
+//                    owned slices applied to the tile's h on bf16 matrix
+//                    cores (operands exact), one fp32 partial per
+//                    (token, expert);
 //   prefill_reduce   (token, 1024 outputs): the token's 10 expert partials
 //                    summed in its routing order in fp64, then narrowed with
 //                    the reference's rule (backends/ref.c:37-40, 95).
@@ -2137,90 +2138,111 @@ struct BatchScratch {
   float* h;                              // [nslots][nblk * 32] gate * h
   float* part;                           // [nslots][hidden] per-(token, expert) partials
   float* y;                              // [tokens][hidden]
-  int8_t* dig;                           // [tokens][super-block][4 digits][256] x as integers
-  float* dscale;                         // [tokens][super-block] 2^e of the digits
-  float* dsum;                           // [tokens][super-block][8] sub-block sums of x
+  uint16_t* xh;                          // [tokens][super-block][2 parts][256] x' = x * 2^-e as f16 hi, lo
+  float* dscale;                         // [tokens] 2^e
+  float* dsum;                           // [tokens][super-block][8] sub-block sums of x'
   uint32_t* status;
 };
 
-// x of the chunk as exact integers for the int8 matrix cores: per (token,
-// super-block), X = rint(x * 2^-e) with 2^e chosen so that |X| < 2^31 for the
-// super-block's largest magnitude, written as four signed base-256 digits
-// (X = ((d0*256 + d1)*256 + d2)*256 + d3, d1..d3 in [-128, 127]), plus 2^e
-// and the fp32 sum of each 32-value sub-block (for the min terms). The
-// digits keep 31 bits of the super-block's range, so the integer dots below
-// are those of x to within 2^-31 of its largest value.
-__global__ __launch_bounds__(256) void prefill_digits(const uint8_t* __restrict__ plan, BatchScratch S) {
+// x of the chunk for the f16 matrix cores: per token, x' = x * 2^-e with 2^e
+// chosen so that |x'| < 2^15, written as two f16 parts hi = f16(x'),
+// lo = f16(x' - hi) (22 significant bits; the f16 subnormal floor 2^-24 is
+// 2^-39 of the token's largest value), plus 2^e and the fp32 sum of each
+// 32-value sub-block of x' (for the min terms).
+__global__ __launch_bounds__(1024) void prefill_split(const uint8_t* __restrict__ plan, BatchScratch S) {
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
-  const unsigned t = blockIdx.x, sb = blockIdx.y, nsb = H.hidden / 256, v = threadIdx.x;
-  const float x = reinterpret_cast<const float*>(plan + H.x_off)[(size_t)t * H.hidden + 256 * sb + v];
-  __shared__ float red[4];
+  const unsigned t = blockIdx.x, hidden = H.hidden, nsb = hidden / 256, v0 = 4 * threadIdx.x;
+  const bool live = v0 < hidden;
+  float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (live) x = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(plan + H.x_off) + (size_t)t * hidden + v0);
+  __shared__ float red[16];
   __shared__ uint32_t nonfinite;
-  if (v == 0) nonfinite = 0;
-  float m = fabsf(x);
+  if (threadIdx.x == 0) nonfinite = 0;
+  float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+  const bool fin = isfinite(x.x) && isfinite(x.y) && isfinite(x.z) && isfinite(x.w);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  float s = x;
+  __syncthreads();
+  if (!fin) nonfinite = 1;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = 0.f;
 #pragma unroll
-  for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o, 64);   // the 32 values of a sub-block
-  __syncthreads();
-  if (!isfinite(x)) nonfinite = 1;
-  if ((v & 63) == 0) red[v >> 6] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const bool fin = nonfinite == 0;
+  for (int w = 0; w < 16; ++w) m = fmaxf(m, red[w]);
+  const bool ok = nonfinite == 0;
   int E = 0;
-  if (fin && m > 0.f) (void)frexpf(m, &E);                   // m < 2^E
-  const int e = max(E - 30, -149);
-  const int X = fin ? (int)rintf(ldexpf(x, -e)) : 0;          // |X| <= 2^30
-  const int d3 = ((X + 128) & 255) - 128, X1 = (X - d3) >> 8;
-  const int d2 = ((X1 + 128) & 255) - 128, X2 = (X1 - d2) >> 8;
-  const int d1 = ((X2 + 128) & 255) - 128, d0 = (X2 - d1) >> 8;
-  int8_t* dst = S.dig + ((size_t)t * nsb + sb) * 1024 + v;
-  dst[0] = (int8_t)d0;
-  dst[256] = (int8_t)d1;
-  dst[512] = (int8_t)d2;
-  dst[768] = (int8_t)d3;
-  if (v == 0) S.dscale[(size_t)t * nsb + sb] = ldexpf(1.f, e);
-  if ((v & 31) == 0) S.dsum[((size_t)t * nsb + sb) * 8 + v / 32] = s;
-  if (v == 0 && !fin) flag(S.status, kErrRange);   // a non-finite x makes the token's a and u non-finite
+  if (ok && m > 0.f) (void)frexpf(m, &E);   // m < 2^E
+  const int e = max(E - 15, -126);
+  const float v[4] = {x.x, x.y, x.z, x.w};
+  float xs[4];
+  _Float16 hi[4], lo[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    xs[j] = ok ? ldexpf(v[j], -e) : 0.f;
+    hi[j] = (_Float16)xs[j];
+    lo[j] = (_Float16)(xs[j] - (float)hi[j]);
+  }
+  float s = (xs[0] + xs[1]) + (xs[2] + xs[3]);
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  s += __shfl_xor(s, 4, 64);   // the 8 threads of a 32-value sub-block
+  if (live) {
+    const unsigned sb = v0 / 256, pos = v0 % 256;
+    uint16_t* dst = S.xh + ((size_t)t * nsb + sb) * 512 + pos;
+    *reinterpret_cast<uint2*>(dst) = make_uint2(
+        (uint32_t)__builtin_bit_cast(uint16_t, hi[0]) | (uint32_t)__builtin_bit_cast(uint16_t, hi[1]) << 16,
+        (uint32_t)__builtin_bit_cast(uint16_t, hi[2]) | (uint32_t)__builtin_bit_cast(uint16_t, hi[3]) << 16);
+    *reinterpret_cast<uint2*>(dst + 256) = make_uint2(
+        (uint32_t)__builtin_bit_cast(uint16_t, lo[0]) | (uint32_t)__builtin_bit_cast(uint16_t, lo[1]) << 16,
+        (uint32_t)__builtin_bit_cast(uint16_t, lo[2]) | (uint32_t)__builtin_bit_cast(uint16_t, lo[3]) << 16);
+    if ((threadIdx.x & 7) == 0) S.dsum[((size_t)t * nsb + sb) * 8 + pos / 32] = s;
+  }
+  if (threadIdx.x == 0) {
+    S.dscale[t] = ldexpf(1.f, e);
+    if (!ok) flag(S.status, kErrRange);   // a non-finite x makes the token's a and u non-finite
+  }
 }
 
-constexpr int kDigRow = 272;             // LDS bytes per (token, digit) row: 256 + 16 of padding
+constexpr int kXhRow = 528;              // LDS bytes per (token, part) row: 512 + 16 of padding
 
 struct GateUpLds {
-  int8_t dig[2][kTileTokens * 4][kDigRow];   // [buffer][token * 4 + digit][position]
-  float scale[2][kTileTokens];               // 2^e of each token for the super-block
-  float xs[2][kTileTokens][8];               // sub-block sums
-  float main[kDecodeWaves][16][kTileTokens]; // [wave][row][token] integer-dot part
+  uint8_t xh[2][kTileTokens * 2][kXhRow];    // [buffer][token * 2 + part][256 f16]: one super-block of x'
+  float xs[2][kTileTokens][8];               // sub-block sums of x'
+  float main[kDecodeWaves][16][kTileTokens]; // [wave][row][token] scale-weighted dot part
   float mins[kDecodeWaves][16][kTileTokens]; // [wave][row][token] min part
 };
 
-// Bytes of v (each below 16) times s (below 8) in one packed 16-bit multiply:
-// every product is below 128, so no byte carries into the next.
-__device__ __forceinline__ uint32_t mul_bytes(uint32_t v, uint32_t s) {
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two nibble values (bytes b and b+1 of v, each below 16) times the 6-bit
+// scale sc as two f16 in one dword: the packed 16-bit multiply-add forms the
+// f16 bits of 1024 + sc*q (exact: sc*q < 1024), and subtracting 1024 in f16
+// leaves sc*q exactly.
+__device__ __forceinline__ uint32_t scaled_pair(uint32_t v, uint32_t sel, uint32_t sc) {
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  const u16x2 a = __builtin_bit_cast(u16x2, v), b = {(unsigned short)s, (unsigned short)s};
-  return __builtin_bit_cast(uint32_t, a * b);
+  const u16x2 p = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, v, sel));
+  const u16x2 m = p * (u16x2){(unsigned short)sc, (unsigned short)sc} + (u16x2){0x6400, 0x6400};
+  const f16x2 f = __builtin_bit_cast(f16x2, m) - (f16x2){(_Float16)1024.f, (_Float16)1024.f};
+  return __builtin_bit_cast(uint32_t, f);
 }
 
 // Workgroup (tile, slice): wavefront w takes row-block w%4 (gate rows of
 // neurons 8rb..8rb+7, then their up rows) and part w/4 (sub-blocks 0-3 or 4-7
 // of every super-block) of the TQ4_KM tiles; lane 16kg + i holds sub-block
-// 4p + kg of row i. Per super-block the int8 matrix cores form, for row i and
-// column (token, digit), sum_k q_k * sc_k * X_k exactly: the 6-bit scale sc of
-// the lane's sub-block is folded into its A operand as sc = 8 sc_hi + sc_lo
-// (two operands q*sc_lo and q*sc_hi, both below 128), so the sum runs over the
-// whole super-block and is scaled once by d * 2^e * digit weight. The min
-// terms, sum_sub dmin * m_sub * sum(x_sub), take one fp32 MFMA per
-// super-block. The digits move through LDS one super-block at a time,
-// double-buffered.
+// 4p + kg of row i, which makes it the A operand of v_mfma_f32_16x16x32_f16
+// (row i, k = 8kg..8kg+7) for 8 positions at a time: A = sc*q, exact in f16,
+// so that each MFMA sums over 4 sub-blocks at once and the super-block is
+// scaled by d only once. B = x' in two f16 parts (two MFMAs). The min terms,
+// sum_sub dmin * m_sub * sum(x'_sub), take one fp32 MFMA per super-block; the
+// token's 2^e multiplies a and u at the end. x' moves through LDS one
+// super-block at a time, double-buffered.
 __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_t* __restrict__ plan,
                                                                     BatchScratch S) {
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
   // Workgroups go round-robin over the 8 XCDs; each XCD takes a contiguous
-  // run of the (tile, slice) list, so that a tile's 20 slices read its x
-  // digits from one L2.
+  // run of the (tile, slice) list, so that a tile's 20 slices read its x'
+  // from one L2.
   const unsigned nblk = H.nblk, per = gridDim.x / 8, b = blockIdx.x;
   const unsigned j = b < 8 * per ? (b % 8) * per + b / 8 : b, brank = j % nblk;
   const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[j / nblk];
@@ -2231,48 +2253,42 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
   const unsigned rb = (unsigned)wave & 3, p = (unsigned)wave >> 2, kg = (unsigned)lane >> 4,
                  col = (unsigned)lane & 15;
   __shared__ __align__(16) GateUpLds L;
-  // Staging: thread -> token tl, 32-byte piece c of its 1 KB of digits.
+  // Staging: thread -> token tl, 32-byte piece c of its 1 KB of x' (part
+  // c/16, positions 16(c%16)..+15).
   const unsigned tl = (unsigned)tid >> 5, c = (unsigned)tid & 31;
   const bool live = tl < T.ntok;
   const size_t trow = (size_t)(live ? slots[tl].token : 0) * nsb;
-  const int8_t* dsrc = S.dig + trow * 1024 + 32 * c;
+  const uint16_t* xsrc = S.xh + trow * 512 + 16 * c;
   const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
   uint4 dr[2] = {z4, z4};
   float sr = 0.f;
-  auto load_d = [&](unsigned s) {
+  auto load_x = [&](unsigned s) {
     if (live) {
-      dr[0] = *reinterpret_cast<const uint4*>(dsrc + 1024 * (size_t)s);
-      dr[1] = *reinterpret_cast<const uint4*>(dsrc + 1024 * (size_t)s + 16);
-      sr = c < 8 ? S.dsum[(trow + s) * 8 + c] : c == 8 ? S.dscale[trow + s] : 0.f;
+      dr[0] = *reinterpret_cast<const uint4*>(xsrc + 512 * (size_t)s);
+      dr[1] = *reinterpret_cast<const uint4*>(xsrc + 512 * (size_t)s + 8);
+      if (c < 8) sr = S.dsum[(trow + s) * 8 + c];
     }
   };
-  auto store_d = [&](unsigned buf) {
-    int8_t* row = &L.dig[buf][4 * tl + c / 8][32 * (c % 8)];
+  auto store_x = [&](unsigned buf) {
+    uint8_t* row = &L.xh[buf][2 * tl + c / 16][32 * (c % 16)];
     *reinterpret_cast<uint4*>(row) = dr[0];
     *reinterpret_cast<uint4*>(row + 16) = dr[1];
     if (c < 8) L.xs[buf][tl][c] = sr;
-    else if (c == 8) L.scale[buf][tl] = sr;
   };
   const uint8_t* wq = slice + 1024 + 2048 * rb + 1024 * p + 16 * (unsigned)lane;   // + 9216 s
   const uint8_t* wh = slice + 256 * rb + 16 * col;
-  const float wdig[4] = {16777216.f, 65536.f, 256.f, 1.f};
-  const unsigned nt4 = (T.ntok + 3) / 4;   // N-tiles of 4 tokens in use
   uint32_t bad = 0;
-  load_d(0);
+  load_x(0);
   uint4 q = ld16(wq), hd = ld16(wh);
-  store_d(0);
+  store_x(0);
   __syncthreads();
-  float acc[4][4];
-#pragma unroll
-  for (int t4 = 0; t4 < 4; ++t4)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[t4][r] = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
   f32x4 cmin = {0.f, 0.f, 0.f, 0.f};
   for (unsigned s = 0; s < nsb; ++s) {
     const unsigned buf = s & 1;
     const uint4 qc = q, hc = hd;
     if (s + 1 < nsb) {
-      load_d(s + 1);
+      load_x(s + 1);
       q = ld16(wq + 9216 * (size_t)(s + 1));
       hd = ld16(wh + 9216 * (size_t)(s + 1));
     }
@@ -2280,69 +2296,49 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     q4k_scale_min(hc.y, hc.z, hc.w, 4 * p + kg, sc, mi);
     if (half_bad(hc.x) || half_bad(hc.x >> 16)) bad |= kErrScale;
     const float d = half_to_float(hc.x & 0xffff);
-    // A operands: positions 16hh..16hh+15 of the lane's sub-block, times
-    // sc_lo and sc_hi.
-    i32x4 a_lo[2], a_hi[2];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const uint32_t w0 = hh ? qc.z : qc.x, w1 = hh ? qc.w : qc.y;
-      const uint32_t b[4] = {nib_lo(w0), nib_hi(w0), nib_lo(w1), nib_hi(w1)};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        a_lo[hh][j] = (int)mul_bytes(b[j], sc & 7u);
-        a_hi[hh][j] = (int)mul_bytes(b[j], sc >> 3);
-      }
-    }
-    // d of the C rows 4(l/16)+r (lanes 0..15 hold rows 0..15).
     float drow[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) drow[r] = __shfl(d, (int)(4 * kg) + r, 64);
-    const int8_t* db = &L.dig[buf][0][32 * (4 * p + kg)];
+    // B row of token col, part h: x' of sub-block 4p + kg at LDS
+    // xh[buf][2 col + h][2 (32 (4p + kg) + 8v)].
+    const uint8_t* xb = &L.xh[buf][2 * col][64 * (4 * p + kg)];
+    f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4) {
-      if ((unsigned)t4 >= nt4) break;   // N-tiles past the tile's tokens hold zeros only
-      i32x4 c_lo = {0, 0, 0, 0}, c_hi = {0, 0, 0, 0};
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const uint4 bv = *reinterpret_cast<const uint4*>(db + (16 * t4 + col) * kDigRow + 16 * hh);
-        const i32x4 bb = {(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w};
-        c_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_lo[hh], bb, c_lo, 0, 0, 0);
-        c_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_hi[hh], bb, c_hi, 0, 0, 0);
-      }
-      // Column col = 4 * token + digit of this N-tile.
-      const float fx = L.scale[buf][4 * t4 + (col >> 2)] * wdig[col & 3];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t4][r] = fmaf((float)(c_lo[r] + 8 * c_hi[r]), drow[r] * fx, acc[t4][r]);
+    for (int v = 0; v < 4; ++v) {
+      // Word v: low nibbles = positions 8v..8v+3, high nibbles 8v+4..8v+7.
+      const uint32_t w = word(qc, v), lo = nib_lo(w), hi = nib_hi(w);
+      const u32x4 aw = {scaled_pair(lo, 0x0c010c00u, sc), scaled_pair(lo, 0x0c030c02u, sc),
+                        scaled_pair(hi, 0x0c010c00u, sc), scaled_pair(hi, 0x0c030c02u, sc)};
+      const f16x8 a = __builtin_bit_cast(f16x8, aw);
+      const uint4 bh = *reinterpret_cast<const uint4*>(xb + 16 * v);
+      const uint4 bl = *reinterpret_cast<const uint4*>(xb + kXhRow + 16 * v);
+      c_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bh), c_hi, 0, 0, 0);
+      c_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bl), c_lo, 0, 0, 0);
     }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = fmaf(drow[r], c_hi[r] + c_lo[r], acc[r]);
     // Min terms: A = -dmin * m of the lane's (row, sub-block), B = the
     // sub-block sum of token col.
     cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-half_to_float(hc.x >> 16) * (float)mi, L.xs[buf][col][4 * p + kg],
                                                 cmin, 0, 0, 0);
-    if (s + 1 < nsb) store_d(buf ^ 1);
+    if (s + 1 < nsb) store_x(buf ^ 1);
     __syncthreads();
   }
-  // Digits of a (row, token) are the 4 neighbouring columns: sum them.
 #pragma unroll
-  for (int t4 = 0; t4 < 4; ++t4)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if ((unsigned)t4 >= nt4) break;
-      float v = acc[t4][r];
-      v += __shfl_xor(v, 1, 64);
-      v += __shfl_xor(v, 2, 64);
-      if ((col & 3) == 0) L.main[wave][4 * kg + r][4 * t4 + (col >> 2)] = v;
-    }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) L.mins[wave][4 * kg + r][col] = cmin[r];
+  for (int r = 0; r < 4; ++r) {
+    L.main[wave][4 * kg + r][col] = acc[r];
+    L.mins[wave][4 * kg + r][col] = cmin[r];
+  }
   __syncthreads();
   // Thread -> (row-block, neuron i, token n): a = gate row i, u = up row 8+i,
-  // each (integer part + min part) of part 0, then of part 1.
+  // each (dot part + min part) of part 0, then of part 1, times 2^e.
   {
     const unsigned trb = (unsigned)tid >> 7, i = ((unsigned)tid >> 4) & 7, n = (unsigned)tid & 15;
-    const float a = (L.main[trb][i][n] + L.mins[trb][i][n]) + (L.main[trb + 4][i][n] + L.mins[trb + 4][i][n]);
-    const float u = (L.main[trb][8 + i][n] + L.mins[trb][8 + i][n]) +
-                    (L.main[trb + 4][8 + i][n] + L.mins[trb + 4][8 + i][n]);
     if (n < T.ntok) {
+      const float sx = S.dscale[slots[n].token];
+      const float a = ((L.main[trb][i][n] + L.mins[trb][i][n]) + (L.main[trb + 4][i][n] + L.mins[trb + 4][i][n])) * sx;
+      const float u = ((L.main[trb][8 + i][n] + L.mins[trb][8 + i][n]) +
+                       (L.main[trb + 4][8 + i][n] + L.mins[trb + 4][8 + i][n])) * sx;
       uint32_t hb = 0;
       const float h = slots[n].gate * silu_mul_f32(a, u, hb);
       bad |= hb;
@@ -2676,7 +2672,7 @@ struct Engine {
   float* bh = nullptr;
   float* bpart = nullptr;
   float* by = nullptr;
-  uint8_t* bdig = nullptr;            // digits, then 2^e, then sub-block sums
+  uint8_t* bdig = nullptr;            // x' parts, then sub-block sums, then 2^e
   size_t bh_bytes = 0, bpart_bytes = 0, by_bytes = 0, bdig_bytes = 0;
   uint32_t* bstatus = nullptr;
   uint32_t* bstatus_host = nullptr;   // pinned
@@ -3060,7 +3056,7 @@ int batch_scratch(const BatchHeader& H) {
     E.bpart_bytes = pb;
     ++E.sample.hot_allocations;
   }
-  const size_t db = (size_t)H.tokens * (H.hidden / 256) * (1024 + 9 * sizeof(float));
+  const size_t db = (size_t)H.tokens * ((H.hidden / 256) * (1024 + 8 * sizeof(float)) + sizeof(float));
   if (db > E.bdig_bytes) {
     (void)hipFree(E.bdig);
     E.bdig = nullptr;
@@ -3091,15 +3087,15 @@ int batch_launch(const uint8_t* dev_plan, const BatchHeader& H, hipStream_t stre
   S.part = E.bpart;
   S.y = E.by;
   const size_t nd = (size_t)H.tokens * (H.hidden / 256);
-  S.dig = reinterpret_cast<int8_t*>(E.bdig);
-  S.dscale = reinterpret_cast<float*>(E.bdig + nd * 1024);
-  S.dsum = S.dscale + nd;
+  S.xh = reinterpret_cast<uint16_t*>(E.bdig);
+  S.dsum = reinterpret_cast<float*>(E.bdig + nd * 1024);
+  S.dscale = S.dsum + nd * 8;
   S.status = E.bstatus;
   hipEvent_t* te = E.timing && E.timed < E.timed_cap ? E.tev + 3 * E.timed++ : nullptr;
   CK(hipMemsetAsync(E.bstatus, 0, sizeof(uint32_t), stream));
   if (te) CK(hipEventRecord(te[0], stream));
   const unsigned ncol = (H.hidden + kDownCols - 1) / kDownCols;
-  hipLaunchKernelGGL(prefill_digits, dim3(H.tokens, H.hidden / 256), dim3(256), 0, stream, dev_plan, S);
+  hipLaunchKernelGGL(prefill_split, dim3(H.tokens), dim3(1024), 0, stream, dev_plan, S);
   hipLaunchKernelGGL(prefill_gate_up, dim3(H.ntiles * H.nblk), dim3(kBatchThreads), 0, stream, dev_plan, S);
   hipLaunchKernelGGL(prefill_down, dim3(H.ntiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S);
   if (te) CK(hipEventRecord(te[1], stream));
