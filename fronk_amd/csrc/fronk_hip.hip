@@ -2259,39 +2259,48 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
   const bool live = tl < T.ntok;
   const size_t trow = (size_t)(live ? slots[tl].token : 0) * nsb;
   const uint16_t* xsrc = S.xh + trow * 512 + 16 * c;
+  // x' runs two super-blocks ahead in two register sets (the loop is
+  // unrolled by two so that no set is copied while its loads are in flight);
+  // the weights one.
+  struct XStage {
+    uint4 d[2];
+    float s;
+  };
   const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
-  uint4 dr[2] = {z4, z4};
-  float sr = 0.f;
-  auto load_x = [&](unsigned s) {
+  auto load_x = [&](unsigned s, XStage& X) {
     if (live) {
-      dr[0] = *reinterpret_cast<const uint4*>(xsrc + 512 * (size_t)s);
-      dr[1] = *reinterpret_cast<const uint4*>(xsrc + 512 * (size_t)s + 8);
-      if (c < 8) sr = S.dsum[(trow + s) * 8 + c];
+      X.d[0] = *reinterpret_cast<const uint4*>(xsrc + 512 * (size_t)s);
+      X.d[1] = *reinterpret_cast<const uint4*>(xsrc + 512 * (size_t)s + 8);
+      if (c < 8) X.s = S.dsum[(trow + s) * 8 + c];
     }
   };
-  auto store_x = [&](unsigned buf) {
+  auto store_x = [&](unsigned buf, const XStage& X) {
     uint8_t* row = &L.xh[buf][2 * tl + c / 16][32 * (c % 16)];
-    *reinterpret_cast<uint4*>(row) = dr[0];
-    *reinterpret_cast<uint4*>(row + 16) = dr[1];
-    if (c < 8) L.xs[buf][tl][c] = sr;
+    *reinterpret_cast<uint4*>(row) = X.d[0];
+    *reinterpret_cast<uint4*>(row + 16) = X.d[1];
+    if (c < 8) L.xs[buf][tl][c] = X.s;
   };
   const uint8_t* wq = slice + 1024 + 2048 * rb + 1024 * p + 16 * (unsigned)lane;   // + 9216 s
   const uint8_t* wh = slice + 256 * rb + 16 * col;
   uint32_t bad = 0;
-  load_x(0);
+  XStage xa = {{z4, z4}, 0.f}, xb = {{z4, z4}, 0.f};
+  load_x(0, xa);
   uint4 q = ld16(wq), hd = ld16(wh);
-  store_x(0);
+  store_x(0, xa);
+  if (1 < nsb) load_x(1, xa);
   __syncthreads();
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   f32x4 cmin = {0.f, 0.f, 0.f, 0.f};
-  for (unsigned s = 0; s < nsb; ++s) {
+  // Super-block s: cur holds x' of s+1 (stored at the end), s+2 is loaded
+  // into nxt.
+  auto step = [&](unsigned s, XStage& cur, XStage& nxt) {
     const unsigned buf = s & 1;
     const uint4 qc = q, hc = hd;
     if (s + 1 < nsb) {
-      load_x(s + 1);
       q = ld16(wq + 9216 * (size_t)(s + 1));
       hd = ld16(wh + 9216 * (size_t)(s + 1));
     }
+    if (s + 2 < nsb) load_x(s + 2, nxt);
     uint32_t sc, mi;
     q4k_scale_min(hc.y, hc.z, hc.w, 4 * p + kg, sc, mi);
     if (half_bad(hc.x) || half_bad(hc.x >> 16)) bad |= kErrScale;
@@ -2301,7 +2310,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     for (int r = 0; r < 4; ++r) drow[r] = __shfl(d, (int)(4 * kg) + r, 64);
     // B row of token col, part h: x' of sub-block 4p + kg at LDS
     // xh[buf][2 col + h][2 (32 (4p + kg) + 8v)].
-    const uint8_t* xb = &L.xh[buf][2 * col][64 * (4 * p + kg)];
+    const uint8_t* xb8 = &L.xh[buf][2 * col][64 * (4 * p + kg)];
     f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -2310,8 +2319,8 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
       const u32x4 aw = {scaled_pair(lo, 0x0c010c00u, sc), scaled_pair(lo, 0x0c030c02u, sc),
                         scaled_pair(hi, 0x0c010c00u, sc), scaled_pair(hi, 0x0c030c02u, sc)};
       const f16x8 a = __builtin_bit_cast(f16x8, aw);
-      const uint4 bh = *reinterpret_cast<const uint4*>(xb + 16 * v);
-      const uint4 bl = *reinterpret_cast<const uint4*>(xb + kXhRow + 16 * v);
+      const uint4 bh = *reinterpret_cast<const uint4*>(xb8 + 16 * v);
+      const uint4 bl = *reinterpret_cast<const uint4*>(xb8 + kXhRow + 16 * v);
       c_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bh), c_hi, 0, 0, 0);
       c_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bl), c_lo, 0, 0, 0);
     }
@@ -2321,8 +2330,12 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     // sub-block sum of token col.
     cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-half_to_float(hc.x >> 16) * (float)mi, L.xs[buf][col][4 * p + kg],
                                                 cmin, 0, 0, 0);
-    if (s + 1 < nsb) store_x(buf ^ 1);
+    if (s + 1 < nsb) store_x(buf ^ 1, cur);
     __syncthreads();
+  };
+  for (unsigned s = 0; s < nsb; s += 2) {
+    step(s, xa, xb);
+    if (s + 1 < nsb) step(s + 1, xb, xa);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
