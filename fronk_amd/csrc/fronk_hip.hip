@@ -2259,9 +2259,10 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
   const bool live = tl < T.ntok;
   const size_t trow = (size_t)(live ? slots[tl].token : 0) * nsb;
   const uint16_t* xsrc = S.xh + trow * 512 + 16 * c;
-  // x' runs two super-blocks ahead in two register sets (the loop is
-  // unrolled by two so that no set is copied while its loads are in flight);
-  // the weights one.
+  // x' runs two super-blocks ahead in two register sets, the weights three
+  // ahead in three (the loop is unrolled by six so that no set is copied
+  // while its loads are in flight; the last weight loads re-read super-block
+  // nsb-1 rather than branch).
   struct XStage {
     uint4 d[2];
     float s;
@@ -2283,23 +2284,26 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
   const uint8_t* wq = slice + 1024 + 2048 * rb + 1024 * p + 16 * (unsigned)lane;   // + 9216 s
   const uint8_t* wh = slice + 256 * rb + 16 * col;
   uint32_t bad = 0;
+  struct WStage {
+    uint4 q, h;
+  };
+  auto load_w = [&](unsigned s) {
+    const size_t o = 9216 * (size_t)min(s, nsb - 1);
+    return WStage{ld16(wq + o), ld16(wh + o)};
+  };
   XStage xa = {{z4, z4}, 0.f}, xb = {{z4, z4}, 0.f};
   load_x(0, xa);
-  uint4 q = ld16(wq), hd = ld16(wh);
+  WStage wa = load_w(0), wb = load_w(1), wc = load_w(2);
   store_x(0, xa);
   if (1 < nsb) load_x(1, xa);
   __syncthreads();
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   f32x4 cmin = {0.f, 0.f, 0.f, 0.f};
-  // Super-block s: cur holds x' of s+1 (stored at the end), s+2 is loaded
-  // into nxt.
-  auto step = [&](unsigned s, XStage& cur, XStage& nxt) {
+  // Super-block s: W holds its weights (reloaded with those of s+3 once
+  // read), cur holds x' of s+1 (stored at the end), s+2 is loaded into nxt.
+  auto step = [&](unsigned s, WStage& W, XStage& cur, XStage& nxt) {
     const unsigned buf = s & 1;
-    const uint4 qc = q, hc = hd;
-    if (s + 1 < nsb) {
-      q = ld16(wq + 9216 * (size_t)(s + 1));
-      hd = ld16(wh + 9216 * (size_t)(s + 1));
-    }
+    const uint4 qc = W.q, hc = W.h;
     if (s + 2 < nsb) load_x(s + 2, nxt);
     uint32_t sc, mi;
     q4k_scale_min(hc.y, hc.z, hc.w, 4 * p + kg, sc, mi);
@@ -2330,12 +2334,17 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     // sub-block sum of token col.
     cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-half_to_float(hc.x >> 16) * (float)mi, L.xs[buf][col][4 * p + kg],
                                                 cmin, 0, 0, 0);
+    W = load_w(s + 3);
     if (s + 1 < nsb) store_x(buf ^ 1, cur);
     __syncthreads();
   };
-  for (unsigned s = 0; s < nsb; s += 2) {
-    step(s, xa, xb);
-    if (s + 1 < nsb) step(s + 1, xb, xa);
+  for (unsigned s = 0; s < nsb; s += 6) {
+    step(s, wa, xa, xb);
+    if (s + 1 < nsb) step(s + 1, wb, xb, xa);
+    if (s + 2 < nsb) step(s + 2, wc, xa, xb);
+    if (s + 3 < nsb) step(s + 3, wa, xb, xa);
+    if (s + 4 < nsb) step(s + 4, wb, xa, xb);
+    if (s + 5 < nsb) step(s + 5, wc, xb, xa);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
