@@ -112,7 +112,7 @@ def slice_sizes(fa, fmt):
 def grid_kernels(lib, plan):
     """The kernels one launch of this plan runs (plan header field `kind`)."""
     kind = int(np.frombuffer(plan[64:68].tobytes(), np.uint32)[0])
-    return "decode_kernel + decode_reduce" if kind == 1 else "layer_kernel"
+    return {1: "decode_kernel + decode_reduce", 2: "decode_rows_kernel + decode_reduce"}.get(kind, "layer_kernel")
 
 
 def copy_kernel(nbytes):

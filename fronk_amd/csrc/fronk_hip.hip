@@ -93,12 +93,12 @@ static_assert(sizeof(PlanHeader) == 80, "header layout");
 // kernel for all-Q4_K units with the transposed down (F32, routed experts
 // only), whose work list is (token, pair) units, token-major, each with its
 // own partial.
-enum : uint32_t { KIND_LAYER = 0, KIND_DECODE = 1 };
+enum : uint32_t { KIND_LAYER = 0, KIND_DECODE = 1, KIND_DECODE_ROWS = 2 };
 // A decode plan's token table (at groups_off): token t's units.
 struct DecodeToken {
   uint32_t first, count;
 };
-constexpr int kDecodeUnitsPerToken = 10 * kBlocks;
+constexpr int kDecodeUnitsPerToken = 11 * kBlocks;   // 10 routed experts and the shared one
 
 struct Scratch {
   uint32_t* done;            // [2][kMaxPairs] phase-A wave completions per pair
@@ -1848,6 +1848,219 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
 static_assert(kDecodeUnitsPerToken <= kReduceDepth * kReduceLanes, "units per token within the reduce's lanes");
 static_assert(kReduceThreads == 256, "the final sum adds four wavefronts");
 
+// ------------------------------------------------- decode kernel, row formats
+//
+// F32 mode, every unit one of the row-format pairs (gate/up, down):
+// (Q4_K, MXFP4) - the reference's native unit format -, (Q8_0, Q8_0) - also
+// the shared expert -, (MXFP4, MXFP4) and (Q4_0, Q4_0). Same work list,
+// unit partials and decode_reduce as decode_kernel: one workgroup of 8
+// wavefronts per (token, pair) unit at a time, no h crossing workgroups.
+//
+// Gate/up: wavefront w takes neurons 4w..4w+3 (4 gate rows, then 4 up
+// rows); lane c holds the row's columns 64c..64c+63 (the re-tiled lane
+// chunks) and x of the same columns in registers, and the row's value is a
+// wave-wide sum of the lanes' fp32 dots (lane_dot_f32, scales as the
+// reference forms them, src/native.c:13-31). h = SiLU(a)*u in double
+// (backends/ref.c:82-83) meets the other wavefronts in LDS.
+//
+// Down: thread (w, l) owns the 8 consecutive outputs 256*(2w + l/32) +
+// 8*(l%32) + 0..7, exactly the 8 positions store_partial gives it, so the
+// partial has decode_kernel's layout. Each output's 16- or 32-byte record
+// over the 32 neurons (byte i: neuron i low nibble, 16+i high; Q8_0: two
+// parts of 16 int8) is dotted with h in fp32, times its scale and the
+// token's gate. The down bytes are requested with the gate/up bytes, so
+// they stream while gate/up is computed (Q4_K after its gate dots, Q8_0
+// after all its dots: their rows hold more registers).
+constexpr int kRowsWaveNeurons = kNeurons / kDecodeWaves;   // 4
+
+struct RowsDown {
+  uint4 q0[8], q1[8];   // records of the thread's 8 outputs (q1: Q8_0 second part)
+  uint4 sc;             // their scales: 8 E8M0 bytes (MXFP4) or 8 fp16 (Q8_0, Q4_0)
+};
+
+template <int DN>
+__device__ __forceinline__ void rows_load_down(const uint8_t* down, unsigned hidden, unsigned c0, RowsDown& R) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    R.q0[i] = ld16(down + 16 * (size_t)(c0 + i));
+    if (DN == TQ8_0) R.q1[i] = ld16(down + 16 * (size_t)hidden + 16 * (size_t)(c0 + i));
+  }
+  if (DN == TMXFP4) {
+    const uint64_t e = gld<uint64_t>(down + 16 * (size_t)hidden + c0);
+    R.sc = make_uint4((uint32_t)e, (uint32_t)(e >> 32), 0u, 0u);
+  } else {
+    R.sc = ld16(down + (DN == TQ8_0 ? 32 : 16) * (size_t)hidden + 2 * (size_t)c0);
+  }
+}
+
+// y[i] = gate * scale_i * sum_n W[c0+i][n] * h[n] for the thread's 8 outputs.
+template <int DN>
+__device__ __forceinline__ void rows_down(const RowsDown& R, const float* hs, float gate, bool valid, float (&y)[8],
+                                          uint32_t& bad) {
+  const float4* h4 = reinterpret_cast<const float4*>(hs);
+  float hsum = 0.f;
+  if (DN == TQ4_0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hsum += (h4[i].x + h4[i].y) + (h4[i].z + h4[i].w);
+  }
+#pragma unroll
+  for (int o = 0; o < 8; ++o) {
+    float sc;
+    if (DN == TMXFP4) {
+      const uint32_t e = (word(R.sc, o >> 2) >> (8 * (o & 3))) & 0xffu;
+      if (valid && e == 255) bad |= kErrScale;
+      sc = e8m0(e);
+    } else {
+      const uint32_t hb = (word(R.sc, o >> 1) >> (16 * (o & 1))) & 0xffffu;
+      if (valid && half_bad(hb)) bad |= kErrScale;
+      sc = half_to_float(hb);
+    }
+    float sum = 0.f;
+    if (DN == TQ8_0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t v = word(i < 4 ? R.q0[o] : R.q1[o], i & 3);
+        const float4 h = h4[i];
+        sum = fmaf((float)(int8_t)v, h.x, sum);
+        sum = fmaf((float)(int8_t)(v >> 8), h.y, sum);
+        sum = fmaf((float)(int8_t)(v >> 16), h.z, sum);
+        sum = fmaf((float)(int8_t)(v >> 24), h.w, sum);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t v = word(R.q0[o], i);
+        const float4 a = h4[i], b = h4[4 + i];
+        if (DN == TMXFP4) {
+          const float2 e0 = fp4_pair(v, 1.0f, 0), e1 = fp4_pair(v, 1.0f, 1), e2 = fp4_pair(v, 1.0f, 2),
+                       e3 = fp4_pair(v, 1.0f, 3);
+          sum = fmaf(e0.x, a.x, sum);
+          sum = fmaf(e1.x, a.y, sum);
+          sum = fmaf(e2.x, a.z, sum);
+          sum = fmaf(e3.x, a.w, sum);
+          sum = fmaf(e0.y, b.x, sum);
+          sum = fmaf(e1.y, b.y, sum);
+          sum = fmaf(e2.y, b.z, sum);
+          sum = fmaf(e3.y, b.w, sum);
+        } else {
+          const uint32_t lo = nib_lo(v), hi = nib_hi(v);
+          sum = fmaf(ub(lo, 0), a.x, sum);
+          sum = fmaf(ub(lo, 1), a.y, sum);
+          sum = fmaf(ub(lo, 2), a.z, sum);
+          sum = fmaf(ub(lo, 3), a.w, sum);
+          sum = fmaf(ub(hi, 0), b.x, sum);
+          sum = fmaf(ub(hi, 1), b.y, sum);
+          sum = fmaf(ub(hi, 2), b.z, sum);
+          sum = fmaf(ub(hi, 3), b.w, sum);
+        }
+      }
+      if (DN == TQ4_0) sum -= 8.f * hsum;
+    }
+    y[o] = valid ? gate * (sc * sum) : 0.f;
+  }
+}
+
+// One unit: pair fields (uniform), x of the unit's token, gate/up rows, h
+// through LDS, the down into y.
+template <int GU, int DN>
+__device__ __forceinline__ uint32_t rows_unit(const PairDesc* P, const float* xg, unsigned hidden, int wave, int lane,
+                                              float* hs, float (&y)[8]) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(P);
+  const uint64_t slice = ((uint64_t)uniform(plan_read(w + 1)) << 32) | uniform(plan_read(w));
+  const uint32_t proj = uniform(plan_read(w + 2));
+  const uint32_t token = uniform(plan_read(w + 3)) >> 24;
+  const float gate = __uint_as_float(uniform(plan_read(reinterpret_cast<const uint32_t*>(P->gate))));
+  const int nch = (int)(hidden / 64);
+  const bool active = lane < nch;
+  const int c = active ? lane : 0;
+  const unsigned n0 = kRowsWaveNeurons * (unsigned)wave;
+  const unsigned cw = 256 * (2 * (unsigned)wave + ((unsigned)lane >> 5)) + 8 * ((unsigned)lane & 31);
+  const bool dvalid = cw < hidden;
+  const unsigned c0 = dvalid ? cw : 0;
+  const uint8_t* down = reinterpret_cast<const uint8_t*>(slice) + 2 * (size_t)proj;
+  // When the down bytes are requested: 0 with the gate/up bytes, 1 after
+  // the gate dots (their registers are free then), 2 after all dots.
+  constexpr int kDownAt = DN == TQ8_0 ? 2 : GU == TQ4_K ? 1 : 0;
+
+  LaneRaw raw[2 * kRowsWaveNeurons];   // [gate rows][up rows]
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int i = 0; i < kRowsWaveNeurons; ++i) load_gu_row<GU>(slice, proj, k, n0 + i, nch, c, raw[kRowsWaveNeurons * k + i]);
+  float4 x[16];
+  {
+    const float4* xs = reinterpret_cast<const float4*>(xg + (size_t)token * hidden + 64 * c);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = xs[i];
+  }
+  RowsDown R;
+  if (kDownAt == 0) rows_load_down<DN>(down, hidden, c0, R);
+  float X0 = 0.f, X1 = 0.f;
+  if (GU == TQ4_K || GU == TQ4_0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      X0 += (x[i].x + x[i].y) + (x[i].z + x[i].w);
+      X1 += (x[8 + i].x + x[8 + i].y) + (x[8 + i].z + x[8 + i].w);
+    }
+  }
+  uint32_t bad = 0;
+  float dot[2 * kRowsWaveNeurons];
+#pragma unroll
+  for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
+    if (kDownAt == 1 && r == kRowsWaveNeurons) rows_load_down<DN>(down, hidden, c0, R);
+    float sc[2], mn[2];
+    const bool ok = raw_scales<GU>(raw[r], c, sc, mn);
+    if (active && !ok) bad |= kErrScale;
+    const float part = lane_dot_f32<GU>(raw[r], sc, mn, x, X0, X1);
+    dot[r] = wave_total(active ? part : 0.f);
+  }
+  if (kDownAt == 2) rows_load_down<DN>(down, hidden, c0, R);
+  if (lane < kRowsWaveNeurons) {
+    float a = dot[0], u = dot[kRowsWaveNeurons];
+#pragma unroll
+    for (int i = 1; i < kRowsWaveNeurons; ++i)
+      if (lane == i) {
+        a = dot[i];
+        u = dot[kRowsWaveNeurons + i];
+      }
+    hs[n0 + lane] = silu_mul(a, u, bad);
+  }
+  __syncthreads();   // the unit's 32 h are in LDS
+  rows_down<DN>(R, hs, gate, dvalid, y, bad);
+  __syncthreads();   // h is read before the next unit writes it
+  return bad;
+}
+
+__global__ __launch_bounds__(kDecodeThreads) void decode_rows_kernel(const uint8_t* __restrict__ plan, Scratch S) {
+  const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
+  uint32_t* status = S.out + (size_t)S.parity * S.out_words;
+  if (blockIdx.x == 0) clear_other_parity(S);
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
+  const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden));
+  const unsigned np = plan_field(PH, offsetof(PlanHeader, npairs)), tpw = plan_field(PH, offsetof(PlanHeader, tpw));
+  const unsigned burst = plan_field(PH, offsetof(PlanHeader, burst));
+  const uint32_t* upart = reinterpret_cast<const uint32_t*>(plan + plan_field(PH, offsetof(PlanHeader, groups_off)) +
+                                                          burst * sizeof(DecodeToken));
+  const float* xg = reinterpret_cast<const float*>(plan + plan_field(PH, offsetof(PlanHeader, x_off)));
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __shared__ __align__(16) float hs[kNeurons];
+  uint32_t bad = 0;
+  float y[8];
+  const unsigned pend = min((blockIdx.x + 1) * tpw, np);
+  for (unsigned p = blockIdx.x * tpw; p < pend; ++p) {
+    const PairDesc* P = pairs + p;
+    // gu and dn are bytes 12 and 13 of the descriptor: word 3.
+    const uint32_t w3 = uniform(plan_read(reinterpret_cast<const uint32_t*>(P) + 3));
+    const uint32_t gu = w3 & 0xffu, dn = (w3 >> 8) & 0xffu;
+    if (gu == TQ4_K && dn == TMXFP4) bad |= rows_unit<TQ4_K, TMXFP4>(P, xg, hidden, wave, lane, hs, y);
+    else if (gu == TQ8_0 && dn == TQ8_0) bad |= rows_unit<TQ8_0, TQ8_0>(P, xg, hidden, wave, lane, hs, y);
+    else if (gu == TMXFP4 && dn == TMXFP4) bad |= rows_unit<TMXFP4, TMXFP4>(P, xg, hidden, wave, lane, hs, y);
+    else bad |= rows_unit<TQ4_0, TQ4_0>(P, xg, hidden, wave, lane, hs, y);
+    store_partial(S, plan_read(upart + p), wave, lane, y);
+  }
+  if (bad) flag(status, bad);
+}
+
 // ------------------------------------------------------- load re-tiling
 //
 // dst[o] = src[source(o)] for every byte o of a slice; the permutations are
@@ -2750,7 +2963,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
       float g = r->gate[t * 11 + e];
       if (e == 10 && g == 0.f) continue;
       uint16_t id = e == 10 ? (uint16_t)kShared : r->expert[t * 10 + e];
-      if (id > kShared) return FR_HIP_INVALID;
+      if (e < 10 && id >= kShared) return FR_HIP_INVALID;   // routed ids < 512 (backends/ref.c:46)
       int s = 0;
       while (s < nu && ids[s] != id) ++s;
       if (s == nu) ids[nu++] = id;
@@ -2826,10 +3039,20 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   // pair) units, token-major, each token's experts in request order and
   // blocks ascending (the single-token pair order), so that a token's units
   // and their summation order do not depend on the rest of the burst.
-  bool decode = r->mode == MODE_F32 && np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
-  for (uint32_t i = 0; decode && i < np; ++i)
-    decode = pairs[i].gu == TQ4_KM && pairs[i].dn == TQ4_KT;
-  for (int s2 = 0; decode && s2 < nu; ++s2) decode = ids[s2] != kShared;
+  // F32 and every pair one of the row-format pairs (shared expert included):
+  // decode_rows_kernel, on the same work list.
+  const bool base = r->mode == MODE_F32 && np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
+  bool q4kt = base, rows = base;
+  for (uint32_t i = 0; base && i < np; ++i) {
+    const uint8_t gu = pairs[i].gu, dn = pairs[i].dn;
+    q4kt = q4kt && gu == TQ4_KM && dn == TQ4_KT;
+    rows = rows && ((gu == TQ4_K && dn == TMXFP4) || (gu == TQ8_0 && dn == TQ8_0) ||
+                    (gu == TMXFP4 && dn == TMXFP4) || (gu == TQ4_0 && dn == TQ4_0));
+  }
+  for (int s2 = 0; q4kt && s2 < nu; ++s2) q4kt = ids[s2] != kShared;
+  uint32_t nunits = 0;
+  for (uint32_t t = 0; t < T; ++t) nunits += (10u + (r->gate[t * 11 + 10] != 0.f ? 1u : 0u)) * (uint32_t)nloaded;
+  const bool decode = (q4kt || rows) && nunits <= (uint32_t)kMaxPairs;
   if (decode && !env_int("FRONK_HIP_NO_DECODE", 0)) {
     // Units are (token, pair). Their partials are numbered token-major in the
     // reference's order (token, routed expert in request order, ascending
@@ -2837,11 +3060,10 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     // that the units of one pair are consecutive in one workgroup's chunk and
     // its bytes are read again while they are still cached.
     DecodeToken tok[kMaxBurst];
-    uint32_t nunits = 0;
-    for (uint32_t t = 0; t < T; ++t) {
-      tok[t].first = nunits;
-      tok[t].count = 10u * (uint32_t)nloaded;
-      nunits += tok[t].count;
+    for (uint32_t t = 0, first = 0; t < T; ++t) {
+      tok[t].first = first;
+      tok[t].count = (10u + (r->gate[t * 11 + 10] != 0.f ? 1u : 0u)) * (uint32_t)nloaded;
+      first += tok[t].count;
     }
     uint32_t* upart = reinterpret_cast<uint32_t*>(out + H->pairs_off + nunits * sizeof(PairDesc) +
                                                   T * sizeof(DecodeToken));
@@ -2851,16 +3073,19 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
       for (int b = 0; b < kBlocks; ++b) {
         if (!E.block[b]) continue;
         const Layout& l = E.lay[b];
+        const bool shared = ids[s2] == kShared;
         for (uint32_t t = 0; t < T; ++t) {
           if (!(masks[s2] >> t & 1u)) continue;
-          int e = 0;
-          while (r->expert[t * 10 + e] != ids[s2]) ++e;   // the expert's place in the token's list
+          int e = 0;   // the expert's place in the token's list; the shared expert follows the 10 routed
+          if (shared) e = 10;
+          else
+            while (r->expert[t * 10 + e] != ids[s2]) ++e;
           PairDesc& U = pairs[w];
           memset(&U, 0, sizeof(U));
           U.slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer + (uint64_t)ids[s2] * l.slice);
-          U.proj = (uint32_t)l.proj;
-          U.gu = (uint8_t)l.gu;
-          U.dn = (uint8_t)l.dn;
+          U.proj = (uint32_t)(shared ? l.shared_proj : l.proj);
+          U.gu = (uint8_t)(shared ? l.shared_gu : l.gu);
+          U.dn = (uint8_t)(shared ? l.shared_dn : l.dn);
           U.tmask = (uint8_t)(1u << t);
           U.pad = (uint8_t)t;
           U.gate[0] = r->gate[t * 11 + e];
@@ -2870,6 +3095,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
       }
     }
     if (w != nunits) return FR_HIP_INVALID;   // every token routes 10 distinct experts
+    if (w > (uint32_t)kMaxPairs) return FR_HIP_INVALID;
     H->npairs = nunits;
     H->ngroups = T;
     H->groups_off = H->pairs_off + nunits * sizeof(PairDesc);
@@ -2881,7 +3107,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     // ceil(units / cap) units of the work list.
     const uint32_t cap = E.cus < (unsigned)kDecodeGridMax ? E.cus : (unsigned)kDecodeGridMax;
     const uint32_t ppw = (nunits + cap - 1) / cap;
-    H->kind = KIND_DECODE;
+    H->kind = q4kt ? KIND_DECODE : KIND_DECODE_ROWS;
     H->tpw = ppw;
     H->grid = (nunits + ppw - 1) / ppw;
     np = nunits;
@@ -2902,8 +3128,8 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
 
 int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream) {
   if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
-  if (H.kind == KIND_DECODE && (grid > (unsigned)kDecodeGridMax || grid > H.npairs || H.ngroups != H.burst))
-    return FR_HIP_INVALID;
+  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS;
+  if (decode && (grid > (unsigned)kDecodeGridMax || grid > H.npairs || H.ngroups != H.burst)) return FR_HIP_INVALID;
   Scratch S;
   S.done = E.done;
   S.fin = E.fin;
@@ -2918,8 +3144,9 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
   const bool one = H.burst == 1;
   hipEvent_t* te = E.timing && E.timed < E.timed_cap ? E.tev + 3 * E.timed++ : nullptr;
   if (te && hipEventRecord(te[0], stream) != hipSuccess) return FR_HIP_IO;
-  if (H.kind == KIND_DECODE) {
-    hipLaunchKernelGGL(decode_kernel, g, dim3(kDecodeThreads), 0, stream, dev_plan, S);
+  if (decode) {
+    if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, dim3(kDecodeThreads), 0, stream, dev_plan, S);
+    else hipLaunchKernelGGL(decode_rows_kernel, g, dim3(kDecodeThreads), 0, stream, dev_plan, S);
     if (te && hipEventRecord(te[1], stream) != hipSuccess) return FR_HIP_IO;
     hipLaunchKernelGGL(decode_reduce, dim3(kMaxHidden / kReducePositions, H.burst), dim3(kReduceThreads), 0, stream,
                        dev_plan, S);
@@ -2938,7 +3165,7 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
       break;
   }
   if (te) {
-    if (H.kind != KIND_DECODE && hipEventRecord(te[1], stream) != hipSuccess) return FR_HIP_IO;
+    if (!decode && hipEventRecord(te[1], stream) != hipSuccess) return FR_HIP_IO;
     if (hipEventRecord(te[2], stream) != hipSuccess) return FR_HIP_IO;
   }
   if (hipGetLastError() != hipSuccess) return FR_HIP_IO;
@@ -3375,7 +3602,8 @@ int fr_hip_launch(const void* host_plan, const void* device_plan, void* stream) 
   if (!host_plan || !device_plan) return FR_HIP_INVALID;
   const PlanHeader& H = *static_cast<const PlanHeader*>(host_plan);
   if (!H.burst || H.burst > (unsigned)kMaxBurst || !H.ntA || !H.ntB) return FR_HIP_INVALID;
-  if (H.kind == KIND_LAYER ? H.grid != H.ntA + H.ntB : (H.kind != KIND_DECODE || !H.grid)) return FR_HIP_INVALID;
+  if (H.kind == KIND_LAYER ? H.grid != H.ntA + H.ntB : ((H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS) || !H.grid))
+    return FR_HIP_INVALID;
   return launch(static_cast<const uint8_t*>(device_plan), H, H.grid,
                 stream ? static_cast<hipStream_t>(stream) : E.stream);
 }

@@ -1,0 +1,140 @@
+"""decode_rows_kernel: single-token and burst requests whose units are all
+row-format pairs - the reference's native units (Q4_K gate/up, MXFP4 down,
+src/native.h:9-21), all-Q8_0 (also the shared expert), all-MXFP4 - run one
+workgroup per (token, pair) unit and the fixed-order decode_reduce.
+
+Each request is checked against the oracle's restatement of backends/ref.c
+(F32 tolerance: rel. L2 1e-5, normalized max-abs 1e-3, as fr_compare reads
+it), against the same request forced onto the two-phase layer kernel, run to
+run bit for bit, and - for bursts - row by row bit for bit against the same
+token run alone (the batching property of src/native.c:94-117).
+"""
+import numpy as np
+import pytest
+
+import fronk_amd as fa
+import oracle
+from fixtures import oracle_request, slice_view, softmax_gates, sparse_unit, zipf_routes
+from test_gpu_parity import check_close
+
+pytestmark = pytest.mark.gpu
+
+KIND_DECODE_ROWS = 2
+
+
+@pytest.fixture(scope="module")
+def eng():
+    e = fa.Engine(0)
+    yield e
+    for b in range(20):
+        e.release(b)
+
+
+def plan_kind(eng, layer, experts, gates, x):
+    plan, grid = eng.plan(layer, experts, gates, x, fa.MODE_F32)
+    return int(np.frombuffer(plan[64:68].tobytes(), np.uint32)[0]), grid
+
+
+def host_units(lay, seed, experts, shared):
+    used = set(int(e) for e in np.asarray(experts).ravel()) | ({512} if shared else set())
+    units = []
+    for b in range(20):
+        u = sparse_unit(lay)
+        for e in used:
+            slice_view(u, lay, 0, e)[:] = oracle.synth_slice(lay, seed, b, 0, e)
+        units.append(u)
+    return units
+
+
+@pytest.mark.parametrize("fmt,hidden", [(fa.FMT_NATIVE, 4096), (fa.FMT_NATIVE, 2560), (fa.FMT_Q8, 4096),
+                                        (fa.FMT_MXFP4, 4096)])
+@pytest.mark.parametrize("shared", [False, True])
+def test_rows_kernel_agrees_with_oracle_and_layer_kernel(eng, fmt, hidden, shared, monkeypatch):
+    lay = oracle.layout(hidden, fmt)
+    seed = 9100 + 10 * fmt + hidden
+    rng = np.random.default_rng(seed)
+    for b in range(20):
+        assert eng.synthetic(b, hidden, fmt, 1, seed) == fa.OK
+    try:
+        experts = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+        gates = np.zeros((1, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, 1)
+        gates[:, 10] = 0.5 if shared else 0.0
+        x = rng.standard_normal((1, hidden)).astype(np.float32)
+        rc, ref = oracle.ref_run(host_units(lay, seed, experts, shared), fmt, False,
+                                 oracle_request(0, experts, gates, x))
+        assert rc == 0
+        kind, grid = plan_kind(eng, 0, experts, gates, x)
+        assert kind == KIND_DECODE_ROWS and 0 < grid <= 256, (kind, grid)
+        print(f"rows kernel fmt={fmt} hidden={hidden} shared={shared} grid={grid}", flush=True)
+        rc, y = eng.run(0, experts, gates, x, fa.MODE_F32)
+        assert rc == fa.OK
+        check_close(ref, y, fa.MODE_F32, ("rows", fmt, hidden, shared))
+        rc, again = eng.run(0, experts, gates, x, fa.MODE_F32)
+        assert rc == fa.OK
+        assert np.array_equal(y.view(np.uint32), again.view(np.uint32))
+        monkeypatch.setenv("FRONK_HIP_NO_DECODE", "1")
+        kind, _ = plan_kind(eng, 0, experts, gates, x)
+        assert kind == 0
+        print(f"layer kernel fmt={fmt} hidden={hidden} shared={shared}", flush=True)
+        rc, y_lay = eng.run(0, experts, gates, x, fa.MODE_F32)
+        assert rc == fa.OK
+        check_close(ref, y_lay, fa.MODE_F32, ("layer", fmt, hidden, shared))
+    finally:
+        for b in range(20):
+            eng.release(b)
+
+
+@pytest.mark.parametrize("fmt,burst,shared_tokens", [(fa.FMT_NATIVE, 3, (1,)), (fa.FMT_Q8, 4, ()),
+                                                     (fa.FMT_NATIVE, 8, (0,))])
+def test_rows_burst_rows_equal_single_token_runs(eng, fmt, burst, shared_tokens):
+    """The last case fills the unit list exactly: 8 tokens x 10 experts x 20
+    blocks plus one token's shared expert on 20 blocks = 1,620 units."""
+    hidden, seed = 4096, 4321 + fmt
+    lay = oracle.layout(hidden, fmt)
+    rng = np.random.default_rng(burst)
+    for b in range(20):
+        assert eng.synthetic(b, hidden, fmt, 1, seed) == fa.OK
+    try:
+        experts = zipf_routes(rng, burst)
+        gates = np.zeros((burst, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, burst)
+        for t in shared_tokens:
+            gates[t, 10] = 0.25
+        x = rng.standard_normal((burst, hidden)).astype(np.float32)
+        kind, grid = plan_kind(eng, 0, experts, gates, x)
+        assert kind == KIND_DECODE_ROWS and 0 < grid <= 256, (kind, grid)
+        print(f"rows burst fmt={fmt} burst={burst} grid={grid}", flush=True)
+        rc, y = eng.run(0, experts, gates, x, fa.MODE_F32)
+        assert rc == fa.OK
+        units = host_units(lay, seed, experts, bool(shared_tokens))
+        rc, ref = oracle.ref_run(units, fmt, False, oracle_request(0, experts, gates, x))
+        assert rc == 0
+        check_close(ref, y, fa.MODE_F32, ("rows burst", fmt, burst))
+        for t in range(burst):
+            rc, y1 = eng.run(0, experts[t:t + 1], gates[t:t + 1], x[t:t + 1], fa.MODE_F32)
+            assert rc == fa.OK
+            assert np.array_equal(y1[0].view(np.uint32), y[t].view(np.uint32)), f"token {t} differs from its T=1 run"
+    finally:
+        for b in range(20):
+            eng.release(b)
+
+
+def test_rows_unit_list_overflow_falls_back_to_layer_kernel(eng):
+    """Eight tokens that all use the shared expert need 1,760 units, more than
+    the unit partials hold: the request runs on the layer kernel."""
+    hidden, fmt, seed = 4096, fa.FMT_Q8, 55
+    for b in range(20):
+        assert eng.synthetic(b, hidden, fmt, 1, seed) == fa.OK
+    try:
+        rng = np.random.default_rng(8)
+        experts = zipf_routes(rng, 8)
+        gates = np.zeros((8, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, 8)
+        gates[:, 10] = 0.125
+        x = rng.standard_normal((8, hidden)).astype(np.float32)
+        kind, _ = plan_kind(eng, 0, experts, gates, x)
+        assert kind == 0
+    finally:
+        for b in range(20):
+            eng.release(b)
