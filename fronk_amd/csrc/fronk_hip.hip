@@ -1447,9 +1447,13 @@ __device__ __forceinline__ void load_dn(const PairBuf& B, unsigned r, uint32_t d
 
 // x of a token into digits in slot `slot` (thread: sub-block tid/4, values
 // 8*(tid%4)..+7, from v). The four threads of a sub-block agree on its
-// largest magnitude and sum through butterflies within their quad.
-__device__ __forceinline__ void stage_x(const float4 (&v4)[2], unsigned slot, unsigned nsub, bool routed,
-                                        DecodeLds& L, uint32_t& bad) {
+// largest magnitude and sum through butterflies within their quad. With
+// kLanes the digits go to the lane-major layout of the row-format kernel,
+// xl[digit][j][k][c]: values 16k..16k+15 of sub-block 2c + j, so that lane c
+// reads its two sub-blocks' 16-byte pieces next to lanes c-1 and c+1.
+template <class Lds, bool kLanes = false>
+__device__ __forceinline__ void stage_x(const float4 (&v4)[2], unsigned slot, unsigned nsub, bool routed, Lds& L,
+                                        uint32_t& bad) {
   const unsigned tid = threadIdx.x, s = tid >> 2, q = tid & 3;
   const float v[8] = {v4[0].x, v4[0].y, v4[0].z, v4[0].w, v4[1].x, v4[1].y, v4[1].z, v4[1].w};
   float m = 0.f;
@@ -1483,8 +1487,14 @@ __device__ __forceinline__ void stage_x(const float4 (&v4)[2], unsigned slot, un
     w[3][i >> 2] |= (uint32_t)(d3 & 255) << (8 * (i & 3));
   }
   if (s < nsub) {
+    if constexpr (kLanes) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) *reinterpret_cast<uint2*>(&L.xd[slot][d][s][8 * q]) = make_uint2(w[d][0], w[d][1]);
+      for (int d = 0; d < 4; ++d)
+        *reinterpret_cast<uint2*>(&L.xl[d][s & 1][q >> 1][s >> 1][2 * (q & 1)]) = make_uint2(w[d][0], w[d][1]);
+    } else {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) *reinterpret_cast<uint2*>(&L.xd[slot][d][s][8 * q]) = make_uint2(w[d][0], w[d][1]);
+    }
     if (q == 0) {
       L.xf[slot][s] = ldexpf(1.f, e);
       L.xs[slot][s] = sum;
@@ -1629,8 +1639,8 @@ __device__ __forceinline__ void down_round(const DecodeDnBytes& R, const float* 
 // covers 1 KB: wavefront w, half h, lane l -> positions 4*(128w + 64h + l)..+3,
 // columns 256*sb + 8j + 4h..+3 (sb = 2w + l/32, j = l%32); y restarts at 0.
 // The kernel boundary makes the partials visible to decode_reduce.
-__device__ __forceinline__ void store_partial(const Scratch& S, unsigned unit, int wave, int lane, float (&y)[8]) {
-  float* mine = S.wgpart + (size_t)unit * kMaxHidden;
+__device__ __forceinline__ void store_partial(float* wgpart, unsigned unit, int wave, int lane, float (&y)[8]) {
+  float* mine = wgpart + (size_t)unit * kMaxHidden;
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh)
     *reinterpret_cast<float4*>(mine + 4 * (128 * wave + 64 * hh + lane)) =
@@ -1768,7 +1778,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
       __builtin_amdgcn_wave_barrier();
     }
     down_round(D[3], L.h[wave], wave, lane, nsb, L, y, bad);
-    store_partial(S, plan_read(upart + p), wave, lane, y);
+    store_partial(S.wgpart, plan_read(upart + p), wave, lane, y);
     if (!more) break;
     stage_x(xv, par ^ 1, nsub, true, L, bad);
     __syncthreads();   // the next unit's x is in LDS
@@ -1873,6 +1883,91 @@ static_assert(kReduceThreads == 256, "the final sum adds four wavefronts");
 // after all its dots: their rows hold more registers).
 constexpr int kRowsWaveNeurons = kNeurons / kDecodeWaves;   // 4
 
+struct RowsLds {
+  int xl[4][2][2][kSubBlocks / 2][4];   // x of the unit's token as int8 digits, lane-major (stage_x)
+  float xf[1][kSubBlocks];              // 2^e of each 32-value sub-block
+  float xs[1][kSubBlocks];           // fp32 sum of each sub-block
+  float h[kNeurons];
+};
+
+// The lane's x digits of sub-block 2c + J (J = 0, 1 of the lane's 64
+// columns): digit d, dword i = values 4i..4i+3 of the sub-block.
+struct LaneDigits {
+  int q[4][8];
+  float f;   // 2^e of the sub-block
+  float s;   // fp32 sum of the sub-block
+};
+
+template <int J>
+__device__ __forceinline__ void load_digits(const RowsLds& L, int c, LaneDigits& X) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int4 v = *reinterpret_cast<const int4*>(&L.xl[d][J][k][c][0]);
+      X.q[d][4 * k] = v.x;
+      X.q[d][4 * k + 1] = v.y;
+      X.q[d][4 * k + 2] = v.z;
+      X.q[d][4 * k + 3] = v.w;
+    }
+  X.f = L.xf[0][2 * c + J];
+  X.s = L.xs[0][2 * c + J];
+}
+
+// sum_k w_k x_k over the sub-block from its four exact integer digit dots:
+// x = 2^e (2^24 d0 + 2^16 d1 + 2^8 d2 + d3); each dot is below 2^24, so
+// its conversion and the power-of-two weights are exact.
+__device__ __forceinline__ float digit_sum(const int (&a)[4], float f) {
+  return f * ((16777216.f * (float)a[0] + 65536.f * (float)a[1]) + (256.f * (float)a[2] + (float)a[3]));
+}
+
+// The lane's fp32 part of a row dot over sub-block 2c + J from exact
+// integer dots (v_dot4_i32_i8 of the weights' integers and x's digits),
+// scaled as the reference scales each weight (src/native.c:13-31): Q8_0
+// d*q; Q4_K (d*sc)*q - dmin*m, the min term against the sub-block's fp32
+// sum of x; Q4_0 d*(q-8), the offset against the same sum.
+template <int type, int J>
+__device__ __forceinline__ float lane_dot_digits(const LaneRaw& r, const float* sc, const float* mn,
+                                                 const LaneDigits& X) {
+  int acc[4] = {0, 0, 0, 0};
+  if (type == TQ8_0) {
+    // Part p: values 16p..16p+15 of the lane's 64; parts 2J, 2J+1 are the sub-block's.
+#pragma unroll
+    for (int p = 2 * J; p < 2 * J + 2; ++p)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int w = (int)word(r.q[p], i);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc[d] = __builtin_amdgcn_sdot4(w, X.q[d][4 * (p & 1) + i], acc[d], false);
+      }
+    return sc[J] * digit_sum(acc, X.f);
+  }
+  if (type == TQ4_K) {
+    // Byte i of the 32-byte chunk: value i (low nibble, sub-block 2c) and
+    // value 32+i (high nibble, sub-block 2c+1).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t v = word(r.q[i >> 2], i & 3);
+      const int n = (int)(J ? nib_hi(v) : nib_lo(v));
+#pragma unroll
+      for (int d = 0; d < 4; ++d) acc[d] = __builtin_amdgcn_sdot4(n, X.q[d][i], acc[d], false);
+    }
+    return sc[J] * digit_sum(acc, X.f) - mn[J] * X.s;
+  }
+  // Q4_0: block J of the lane, byte i: value i (low nibble), 16+i (high).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t v = word(r.q[J], i);
+    const int lo = (int)nib_lo(v), hi = (int)nib_hi(v);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      acc[d] = __builtin_amdgcn_sdot4(lo, X.q[d][i], acc[d], false);
+      acc[d] = __builtin_amdgcn_sdot4(hi, X.q[d][4 + i], acc[d], false);
+    }
+  }
+  return sc[J] * (digit_sum(acc, X.f) - 8.f * X.s);
+}
+
 struct RowsDown {
   uint4 q0[8], q1[8];   // records of the thread's 8 outputs (q1: Q8_0 second part)
   uint4 sc;             // their scales: 8 E8M0 bytes (MXFP4) or 8 fp16 (Q8_0, Q4_0)
@@ -1961,16 +2056,19 @@ __device__ __forceinline__ void rows_down(const RowsDown& R, const float* hs, fl
 }
 
 // One unit: pair fields (uniform), x of the unit's token, gate/up rows, h
-// through LDS, the down into y.
+// through LDS, the down into y. MXFP4 rows dot in fp32 against x held in
+// registers (two codes per conversion); the integer formats dot in integers
+// against x's digits staged in LDS.
 template <int GU, int DN>
-__device__ __forceinline__ uint32_t rows_unit(const PairDesc* P, const float* xg, unsigned hidden, int wave, int lane,
-                                              float* hs, float (&y)[8]) {
+__device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, const PairDesc* P, const float* xg,
+                                              unsigned hidden, int wave, int lane, RowsLds& L) {
   const uint32_t* w = reinterpret_cast<const uint32_t*>(P);
   const uint64_t slice = ((uint64_t)uniform(plan_read(w + 1)) << 32) | uniform(plan_read(w));
   const uint32_t proj = uniform(plan_read(w + 2));
   const uint32_t token = uniform(plan_read(w + 3)) >> 24;
   const float gate = __uint_as_float(uniform(plan_read(reinterpret_cast<const uint32_t*>(P->gate))));
   const int nch = (int)(hidden / 64);
+  const unsigned nsub = hidden / 32;
   const bool active = lane < nch;
   const int c = active ? lane : 0;
   const unsigned n0 = kRowsWaveNeurons * (unsigned)wave;
@@ -1978,43 +2076,69 @@ __device__ __forceinline__ uint32_t rows_unit(const PairDesc* P, const float* xg
   const bool dvalid = cw < hidden;
   const unsigned c0 = dvalid ? cw : 0;
   const uint8_t* down = reinterpret_cast<const uint8_t*>(slice) + 2 * (size_t)proj;
-  // When the down bytes are requested: 0 with the gate/up bytes, 1 after
-  // the gate dots (their registers are free then), 2 after all dots.
-  constexpr int kDownAt = DN == TQ8_0 ? 2 : GU == TQ4_K ? 1 : 0;
+  constexpr bool kDigits = GU != TMXFP4;
+  // The down bytes are requested with the gate/up bytes for MXFP4 rows and
+  // after the dots for the integer formats, whose digits hold more registers.
+  constexpr bool kEarlyDown = !kDigits;
+  const float* xt = xg + (size_t)token * hidden;
+  uint32_t bad = 0;
 
+  // x first, so that staging it waits for x alone.
+  float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  float4 x[16];
+  const unsigned tid = threadIdx.x;
+  if (kDigits) {
+    if ((tid >> 2) < nsub) {
+      const float4* xs = reinterpret_cast<const float4*>(xt + 32 * (tid >> 2) + 8 * (tid & 3));
+      xv[0] = xs[0];
+      xv[1] = xs[1];
+    }
+  } else {
+    const float4* xs = reinterpret_cast<const float4*>(xt + 64 * c);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = xs[i];
+  }
   LaneRaw raw[2 * kRowsWaveNeurons];   // [gate rows][up rows]
 #pragma unroll
   for (int k = 0; k < 2; ++k)
 #pragma unroll
     for (int i = 0; i < kRowsWaveNeurons; ++i) load_gu_row<GU>(slice, proj, k, n0 + i, nch, c, raw[kRowsWaveNeurons * k + i]);
-  float4 x[16];
-  {
-    const float4* xs = reinterpret_cast<const float4*>(xg + (size_t)token * hidden + 64 * c);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = xs[i];
-  }
   RowsDown R;
-  if (kDownAt == 0) rows_load_down<DN>(down, hidden, c0, R);
-  float X0 = 0.f, X1 = 0.f;
-  if (GU == TQ4_K || GU == TQ4_0) {
+  if (kEarlyDown) rows_load_down<DN>(down, hidden, c0, R);
+  float dot[2 * kRowsWaveNeurons];
+  if constexpr (kDigits) {
+    stage_x<RowsLds, true>(xv, 0, nsub, true, L, bad);
+    __syncthreads();   // x's digits are in LDS
+    // The lane's two sub-blocks in turn, every row each time: half the
+    // digit registers of holding both.
+    float part[2 * kRowsWaveNeurons];
+    LaneDigits X;
+    load_digits<0>(L, c, X);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      X0 += (x[i].x + x[i].y) + (x[i].z + x[i].w);
-      X1 += (x[8 + i].x + x[8 + i].y) + (x[8 + i].z + x[8 + i].w);
+    for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
+      float sc[2], mn[2];
+      const bool ok = raw_scales<GU>(raw[r], c, sc, mn);
+      if (active && !ok) bad |= kErrScale;
+      part[r] = lane_dot_digits<GU, 0>(raw[r], sc, mn, X);
+    }
+    load_digits<1>(L, c, X);
+#pragma unroll
+    for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
+      float sc[2], mn[2];
+      (void)raw_scales<GU>(raw[r], c, sc, mn);
+      part[r] += lane_dot_digits<GU, 1>(raw[r], sc, mn, X);
+      dot[r] = wave_total(active ? part[r] : 0.f);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
+      float sc[2], mn[2];
+      const bool ok = raw_scales<GU>(raw[r], c, sc, mn);
+      if (active && !ok) bad |= kErrScale;
+      dot[r] = wave_total(active ? lane_dot_f32<GU>(raw[r], sc, mn, x, 0.f, 0.f) : 0.f);
     }
   }
-  uint32_t bad = 0;
-  float dot[2 * kRowsWaveNeurons];
-#pragma unroll
-  for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
-    if (kDownAt == 1 && r == kRowsWaveNeurons) rows_load_down<DN>(down, hidden, c0, R);
-    float sc[2], mn[2];
-    const bool ok = raw_scales<GU>(raw[r], c, sc, mn);
-    if (active && !ok) bad |= kErrScale;
-    const float part = lane_dot_f32<GU>(raw[r], sc, mn, x, X0, X1);
-    dot[r] = wave_total(active ? part : 0.f);
-  }
-  if (kDownAt == 2) rows_load_down<DN>(down, hidden, c0, R);
+  if (!kEarlyDown) rows_load_down<DN>(down, hidden, c0, R);
   if (lane < kRowsWaveNeurons) {
     float a = dot[0], u = dot[kRowsWaveNeurons];
 #pragma unroll
@@ -2023,14 +2147,19 @@ __device__ __forceinline__ uint32_t rows_unit(const PairDesc* P, const float* xg
         a = dot[i];
         u = dot[kRowsWaveNeurons + i];
       }
-    hs[n0 + lane] = silu_mul(a, u, bad);
+    L.h[n0 + lane] = silu_mul(a, u, bad);
   }
-  __syncthreads();   // the unit's 32 h are in LDS
-  rows_down<DN>(R, hs, gate, dvalid, y, bad);
+  __syncthreads();   // the unit's 32 h are in LDS (and every lane has its digits)
+  float y[8];
+  rows_down<DN>(R, L.h, gate, dvalid, y, bad);
+  store_partial(wgpart, unit, wave, lane, y);
   __syncthreads();   // h is read before the next unit writes it
   return bad;
 }
 
+// One instantiation per unit format: the routed pairs' (GA, DA) and the
+// shared expert's (GB, DB); a launch runs both, each unit on its own.
+template <int GA, int DA, int GB, int DB>
 __global__ __launch_bounds__(kDecodeThreads) void decode_rows_kernel(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
   uint32_t* status = S.out + (size_t)S.parity * S.out_words;
@@ -2043,20 +2172,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rows_kernel(const uint8
                                                           burst * sizeof(DecodeToken));
   const float* xg = reinterpret_cast<const float*>(plan + plan_field(PH, offsetof(PlanHeader, x_off)));
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  __shared__ __align__(16) float hs[kNeurons];
+  __shared__ __align__(16) RowsLds L;
   uint32_t bad = 0;
-  float y[8];
   const unsigned pend = min((blockIdx.x + 1) * tpw, np);
   for (unsigned p = blockIdx.x * tpw; p < pend; ++p) {
     const PairDesc* P = pairs + p;
     // gu and dn are bytes 12 and 13 of the descriptor: word 3.
     const uint32_t w3 = uniform(plan_read(reinterpret_cast<const uint32_t*>(P) + 3));
     const uint32_t gu = w3 & 0xffu, dn = (w3 >> 8) & 0xffu;
-    if (gu == TQ4_K && dn == TMXFP4) bad |= rows_unit<TQ4_K, TMXFP4>(P, xg, hidden, wave, lane, hs, y);
-    else if (gu == TQ8_0 && dn == TQ8_0) bad |= rows_unit<TQ8_0, TQ8_0>(P, xg, hidden, wave, lane, hs, y);
-    else if (gu == TMXFP4 && dn == TMXFP4) bad |= rows_unit<TMXFP4, TMXFP4>(P, xg, hidden, wave, lane, hs, y);
-    else bad |= rows_unit<TQ4_0, TQ4_0>(P, xg, hidden, wave, lane, hs, y);
-    store_partial(S, plan_read(upart + p), wave, lane, y);
+    const unsigned unit = plan_read(upart + p);
+    if (GA == GB && DA == DB) bad |= rows_unit<GA, DA>(S.wgpart, unit, P, xg, hidden, wave, lane, L);
+    else if (gu == GA && dn == DA) bad |= rows_unit<GA, DA>(S.wgpart, unit, P, xg, hidden, wave, lane, L);
+    else bad |= rows_unit<GB, DB>(S.wgpart, unit, P, xg, hidden, wave, lane, L);
   }
   if (bad) flag(status, bad);
 }
@@ -2938,6 +3065,19 @@ uint32_t group_pairs(uint8_t dn) {
   return g < 1 ? 1 : g > cap ? cap : g;
 }
 
+// The row-format kernel instantiation for a block's formats: (routed
+// gate/up, down) and the shared expert's, or kNoCombo.
+constexpr uint32_t kNoCombo = ~0u;
+constexpr uint32_t kComboShared = 0x10;   // the request has shared-expert units
+enum : uint32_t { COMBO_NATIVE = 0, COMBO_Q8 = 1, COMBO_MXFP4 = 2, COMBO_Q4_0 = 3 };
+uint32_t rows_combo(const Layout& l) {
+  if (l.gu == TQ4_K && l.dn == TMXFP4 && l.shared_gu == TQ8_0 && l.shared_dn == TQ8_0) return COMBO_NATIVE;
+  if (l.gu == TQ8_0 && l.dn == TQ8_0 && l.shared_gu == TQ8_0 && l.shared_dn == TQ8_0) return COMBO_Q8;
+  if (l.gu == TMXFP4 && l.dn == TMXFP4 && l.shared_gu == TQ8_0 && l.shared_dn == TQ8_0) return COMBO_MXFP4;
+  if (l.gu == TQ4_0 && l.dn == TQ4_0 && l.shared_gu == TQ4_0 && l.shared_dn == TQ4_0) return COMBO_Q4_0;
+  return kNoCombo;
+}
+
 int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, unsigned* grid) {
   if (!r || !out || !used || !grid || !r->expert || !r->gate || !r->x) return FR_HIP_INVALID;
   if (r->burst < 1 || r->burst > (unsigned)kMaxBurst || r->layer >= (unsigned)kLayers || r->mode > 2)
@@ -3043,12 +3183,15 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   // decode_rows_kernel, on the same work list.
   const bool base = r->mode == MODE_F32 && np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
   bool q4kt = base, rows = base;
-  for (uint32_t i = 0; base && i < np; ++i) {
-    const uint8_t gu = pairs[i].gu, dn = pairs[i].dn;
-    q4kt = q4kt && gu == TQ4_KM && dn == TQ4_KT;
-    rows = rows && ((gu == TQ4_K && dn == TMXFP4) || (gu == TQ8_0 && dn == TQ8_0) ||
-                    (gu == TMXFP4 && dn == TMXFP4) || (gu == TQ4_0 && dn == TQ4_0));
-  }
+  // The row-format kernel is instantiated per unit format: every loaded
+  // block must have the first one's routed and shared formats.
+  int first = 0;
+  while (!E.block[first]) ++first;
+  const uint32_t combo = rows_combo(E.lay[first]);
+  rows = rows && combo != kNoCombo;
+  for (int b = 0; rows && b < kBlocks; ++b)
+    rows = !E.block[b] || rows_combo(E.lay[b]) == combo;
+  for (uint32_t i = 0; base && i < np; ++i) q4kt = q4kt && pairs[i].gu == TQ4_KM && pairs[i].dn == TQ4_KT;
   for (int s2 = 0; q4kt && s2 < nu; ++s2) q4kt = ids[s2] != kShared;
   uint32_t nunits = 0;
   for (uint32_t t = 0; t < T; ++t) nunits += (10u + (r->gate[t * 11 + 10] != 0.f ? 1u : 0u)) * (uint32_t)nloaded;
@@ -3108,6 +3251,9 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     const uint32_t cap = E.cus < (unsigned)kDecodeGridMax ? E.cus : (unsigned)kDecodeGridMax;
     const uint32_t ppw = (nunits + cap - 1) / cap;
     H->kind = q4kt ? KIND_DECODE : KIND_DECODE_ROWS;
+    bool with_shared = false;
+    for (uint32_t t = 0; t < T; ++t) with_shared = with_shared || r->gate[t * 11 + 10] != 0.f;
+    H->pad = q4kt ? 0u : combo | (with_shared ? kComboShared : 0u);
     H->tpw = ppw;
     H->grid = (nunits + ppw - 1) / ppw;
     np = nunits;
@@ -3130,6 +3276,7 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
   if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
   const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS;
   if (decode && (grid > (unsigned)kDecodeGridMax || grid > H.npairs || H.ngroups != H.burst)) return FR_HIP_INVALID;
+  if (H.kind == KIND_DECODE_ROWS && (H.pad & ~kComboShared) > COMBO_Q4_0) return FR_HIP_INVALID;
   Scratch S;
   S.done = E.done;
   S.fin = E.fin;
@@ -3145,8 +3292,29 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
   hipEvent_t* te = E.timing && E.timed < E.timed_cap ? E.tev + 3 * E.timed++ : nullptr;
   if (te && hipEventRecord(te[0], stream) != hipSuccess) return FR_HIP_IO;
   if (decode) {
-    if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, dim3(kDecodeThreads), 0, stream, dev_plan, S);
-    else hipLaunchKernelGGL(decode_rows_kernel, g, dim3(kDecodeThreads), 0, stream, dev_plan, S);
+    const dim3 b(kDecodeThreads);
+    if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, b, 0, stream, dev_plan, S);
+    else switch (H.pad) {   // (routed formats, shared formats) of the units the request has
+      case COMBO_NATIVE:
+        hipLaunchKernelGGL((decode_rows_kernel<TQ4_K, TMXFP4, TQ4_K, TMXFP4>), g, b, 0, stream, dev_plan, S);
+        break;
+      case COMBO_NATIVE | kComboShared:
+        hipLaunchKernelGGL((decode_rows_kernel<TQ4_K, TMXFP4, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
+        break;
+      case COMBO_Q8:
+      case COMBO_Q8 | kComboShared:
+        hipLaunchKernelGGL((decode_rows_kernel<TQ8_0, TQ8_0, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
+        break;
+      case COMBO_MXFP4:
+        hipLaunchKernelGGL((decode_rows_kernel<TMXFP4, TMXFP4, TMXFP4, TMXFP4>), g, b, 0, stream, dev_plan, S);
+        break;
+      case COMBO_MXFP4 | kComboShared:
+        hipLaunchKernelGGL((decode_rows_kernel<TMXFP4, TMXFP4, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
+        break;
+      default:
+        hipLaunchKernelGGL((decode_rows_kernel<TQ4_0, TQ4_0, TQ4_0, TQ4_0>), g, b, 0, stream, dev_plan, S);
+        break;
+    }
     if (te && hipEventRecord(te[1], stream) != hipSuccess) return FR_HIP_IO;
     hipLaunchKernelGGL(decode_reduce, dim3(kMaxHidden / kReducePositions, H.burst), dim3(kReduceThreads), 0, stream,
                        dev_plan, S);
