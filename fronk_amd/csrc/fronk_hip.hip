@@ -106,7 +106,7 @@ struct Scratch {
   float* hbuf;               // [kMaxPairs][8][32]
   double* partial;           // [groups][burst][hidden]
   uint32_t* out;             // [2][out_words]: status, pad x3, y
-  float* wgpart;             // [kMaxPairs][hidden]: decode unit partials
+  float* wgpart;             // decode unit partials, [kMaxHidden/16][kMaxPairs][16] (partial_index)
   uint32_t* bar;             // [2]: decode workgroups past their partial store
   uint32_t out_words;
   uint32_t parity;
@@ -1635,15 +1635,22 @@ __device__ __forceinline__ void down_round(const DecodeDnBytes& R, const float* 
   __builtin_amdgcn_wave_barrier();   // the table and headers are read before the next round writes them
 }
 
-// The unit's fp32 partial, position-major so that each store instruction
-// covers 1 KB: wavefront w, half h, lane l -> positions 4*(128w + 64h + l)..+3,
-// columns 256*sb + 8j + 4h..+3 (sb = 2w + l/32, j = l%32); y restarts at 0.
-// The kernel boundary makes the partials visible to decode_reduce.
+// Unit partials, [position block][unit][16 positions]: position p of unit u
+// at float (p/16 * kMaxPairs + u) * 16 + p%16, so that decode_reduce's
+// workgroup for one block of 16 positions reads its units' values as one
+// contiguous run.
+__device__ __forceinline__ size_t partial_index(unsigned unit, unsigned p) {
+  return ((size_t)(p >> 4) * kMaxPairs + unit) * 16 + (p & 15);
+}
+
+// The unit's fp32 partial: wavefront w, half h, lane l -> positions
+// 4*(128w + 64h + l)..+3, columns 256*sb + 8j + 4h..+3 (sb = 2w + l/32,
+// j = l%32), four lanes to a 64-byte piece; y restarts at 0. The kernel
+// boundary makes the partials visible to decode_reduce.
 __device__ __forceinline__ void store_partial(float* wgpart, unsigned unit, int wave, int lane, float (&y)[8]) {
-  float* mine = wgpart + (size_t)unit * kMaxHidden;
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh)
-    *reinterpret_cast<float4*>(mine + 4 * (128 * wave + 64 * hh + lane)) =
+    *reinterpret_cast<float4*>(wgpart + partial_index(unit, 4 * (128 * wave + 64 * hh + lane))) =
         make_float4(y[4 * hh], y[4 * hh + 1], y[4 * hh + 2], y[4 * hh + 3]);
 #pragma unroll
   for (int i = 0; i < 8; ++i) y[i] = 0.f;
@@ -1824,7 +1831,7 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
 #pragma unroll
   for (unsigned k = 0; k < kReduceDepth; ++k) {
     const unsigned g = ps + kReduceLanes * k;
-    r[k] = g < tk.count ? *reinterpret_cast<const float4*>(S.wgpart + (size_t)(tk.first + g) * kMaxHidden + p0)
+    r[k] = g < tk.count ? *reinterpret_cast<const float4*>(S.wgpart + partial_index(tk.first + g, p0))
                         : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   double v[4] = {0.0, 0.0, 0.0, 0.0};
