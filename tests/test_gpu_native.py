@@ -58,9 +58,12 @@ def test_native_fixture_deterministic_and_burst_invariant(eng, native2560):
         assert rc == fa.OK
         same += np.array_equal(y1[0].view(np.uint32), y8[t].view(np.uint32))
         check_close(y1, y8[t:t + 1], fa.MODE_F32)
-    # fp64 accumulation over pairs: a burst differs from T=1 only in summation
-    # order, so nearly every token is bit-identical.
-    assert same >= 6
+    # The request runs on the row-format decode kernel: (token, pair) units
+    # summed per token in a fixed order, so every burst row is bit-identical
+    # to its single-token run (src/native.c:94-117 checks this with memcmp).
+    plan, _ = eng.plan(47, experts, gates, x, fa.MODE_F32)
+    assert int(np.frombuffer(plan[64:68].tobytes(), np.uint32)[0]) == 2
+    assert same == 8
 
 
 def test_native_error_paths(eng, native2560):
