@@ -1891,6 +1891,7 @@ static_assert(kReduceThreads == 256, "the final sum adds four wavefronts");
 constexpr int kRowsWaveNeurons = kNeurons / kDecodeWaves;   // 4
 
 struct RowsLds {
+  float4 xq[16][kSubBlocks / 2];        // x of the unit's token in fp32, lane-major: [value/4 % 16][lane]
   int xl[4][2][2][kSubBlocks / 2][4];   // x of the unit's token as int8 digits, lane-major (stage_x)
   float xf[1][kSubBlocks];              // 2^e of each 32-value sub-block
   float xs[1][kSubBlocks];           // fp32 sum of each sub-block
@@ -2063,9 +2064,9 @@ __device__ __forceinline__ void rows_down(const RowsDown& R, const float* hs, fl
 }
 
 // One unit: pair fields (uniform), x of the unit's token, gate/up rows, h
-// through LDS, the down into y. MXFP4 rows dot in fp32 against x held in
-// registers (two codes per conversion); the integer formats dot in integers
-// against x's digits staged in LDS.
+// through LDS, the down into y. MXFP4 rows dot in fp32 against x staged in
+// LDS and held in registers (two codes per conversion); the integer formats
+// dot in integers against x's digits staged in LDS.
 template <int GU, int DN>
 __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, const PairDesc* P, const float* xg,
                                               unsigned hidden, int wave, int lane, RowsLds& L) {
@@ -2090,20 +2091,15 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
   const float* xt = xg + (size_t)token * hidden;
   uint32_t bad = 0;
 
-  // x first, so that staging it waits for x alone.
+  // x first, so that staging it waits for x alone: thread t holds values
+  // 8t..8t+7, staged once per workgroup in LDS.
   float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
   float4 x[16];
   const unsigned tid = threadIdx.x;
-  if (kDigits) {
-    if ((tid >> 2) < nsub) {
-      const float4* xs = reinterpret_cast<const float4*>(xt + 32 * (tid >> 2) + 8 * (tid & 3));
-      xv[0] = xs[0];
-      xv[1] = xs[1];
-    }
-  } else {
-    const float4* xs = reinterpret_cast<const float4*>(xt + 64 * c);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = xs[i];
+  if ((tid >> 2) < nsub) {
+    const float4* xs = reinterpret_cast<const float4*>(xt + 32 * (tid >> 2) + 8 * (tid & 3));
+    xv[0] = xs[0];
+    xv[1] = xs[1];
   }
   LaneRaw raw[2 * kRowsWaveNeurons];   // [gate rows][up rows]
 #pragma unroll
@@ -2112,6 +2108,16 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
     for (int i = 0; i < kRowsWaveNeurons; ++i) load_gu_row<GU>(slice, proj, k, n0 + i, nch, c, raw[kRowsWaveNeurons * k + i]);
   RowsDown R;
   if (kEarlyDown) rows_load_down<DN>(down, hidden, c0, R);
+  if constexpr (!kDigits) {
+    // Values 8t..8t+7 are float4s 2(t%8), 2(t%8)+1 of lane t/8's 64 values.
+    if ((tid >> 2) < nsub) {
+      L.xq[2 * (tid & 7)][tid >> 3] = xv[0];
+      L.xq[2 * (tid & 7) + 1][tid >> 3] = xv[1];
+    }
+    __syncthreads();   // x is in LDS
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = L.xq[i][c];
+  }
   float dot[2 * kRowsWaveNeurons];
   if constexpr (kDigits) {
     stage_x<RowsLds, true>(xv, 0, nsub, true, L, bad);
