@@ -1885,9 +1885,8 @@ static_assert(kReduceThreads == 256, "the final sum adds four wavefronts");
 // partial has decode_kernel's layout. Each output's 16- or 32-byte record
 // over the 32 neurons (byte i: neuron i low nibble, 16+i high; Q8_0: two
 // parts of 16 int8) is dotted with h in fp32, times its scale and the
-// token's gate. The down bytes are requested with the gate/up bytes, so
-// they stream while gate/up is computed (Q4_K after its gate dots, Q8_0
-// after all its dots: their rows hold more registers).
+// token's gate. The down bytes are requested once the gate/up dots are
+// done and arrive while h is formed.
 constexpr int kRowsWaveNeurons = kNeurons / kDecodeWaves;   // 4
 
 struct RowsLds {
@@ -2085,9 +2084,9 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
   const unsigned c0 = dvalid ? cw : 0;
   const uint8_t* down = reinterpret_cast<const uint8_t*>(slice) + 2 * (size_t)proj;
   constexpr bool kDigits = GU != TMXFP4;
-  // The down bytes are requested with the gate/up bytes for MXFP4 rows and
-  // after the dots for the integer formats, whose digits hold more registers.
-  constexpr bool kEarlyDown = !kDigits;
+  // The down bytes are requested after the dots: requested with the rows,
+  // they delay the rows the dots wait for (measured: MXFP4 20.2 against
+  // 19.0 us per call, native 21.9 against 20.3 us).
   const float* xt = xg + (size_t)token * hidden;
   uint32_t bad = 0;
 
@@ -2107,7 +2106,6 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
 #pragma unroll
     for (int i = 0; i < kRowsWaveNeurons; ++i) load_gu_row<GU>(slice, proj, k, n0 + i, nch, c, raw[kRowsWaveNeurons * k + i]);
   RowsDown R;
-  if (kEarlyDown) rows_load_down<DN>(down, hidden, c0, R);
   if constexpr (!kDigits) {
     // Values 8t..8t+7 are float4s 2(t%8), 2(t%8)+1 of lane t/8's 64 values.
     if ((tid >> 2) < nsub) {
@@ -2151,7 +2149,7 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
       dot[r] = wave_total(active ? lane_dot_f32<GU>(raw[r], sc, mn, x, 0.f, 0.f) : 0.f);
     }
   }
-  if (!kEarlyDown) rows_load_down<DN>(down, hidden, c0, R);
+  rows_load_down<DN>(down, hidden, c0, R);
   if (lane < kRowsWaveNeurons) {
     float a = dot[0], u = dot[kRowsWaveNeurons];
 #pragma unroll
