@@ -1885,8 +1885,8 @@ static_assert(kReduceThreads == 256, "the final sum adds four wavefronts");
 // partial has decode_kernel's layout. Each output's 16- or 32-byte record
 // over the 32 neurons (byte i: neuron i low nibble, 16+i high; Q8_0: two
 // parts of 16 int8) is dotted with h in fp32, times its scale and the
-// token's gate. The down bytes are requested once the gate/up dots are
-// done and arrive while h is formed.
+// token's gate. The down bytes are requested halfway through the gate/up
+// dots.
 constexpr int kRowsWaveNeurons = kNeurons / kDecodeWaves;   // 4
 
 struct RowsLds {
@@ -2084,9 +2084,11 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
   const unsigned c0 = dvalid ? cw : 0;
   const uint8_t* down = reinterpret_cast<const uint8_t*>(slice) + 2 * (size_t)proj;
   constexpr bool kDigits = GU != TMXFP4;
-  // The down bytes are requested after the dots: requested with the rows,
-  // they delay the rows the dots wait for (measured: MXFP4 20.2 against
-  // 19.0 us per call, native 21.9 against 20.3 us).
+  // The down bytes are requested halfway through the dots (after the gate
+  // rows, or after the first sub-block pass, by when every row has
+  // arrived): requested with the rows, they delay the rows the dots wait
+  // for; requested after all dots, they arrive late (measured per call:
+  // MXFP4 20.2 with the rows, 19.0 after, 17.9 halfway).
   const float* xt = xg + (size_t)token * hidden;
   uint32_t bad = 0;
 
@@ -2132,6 +2134,7 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
       if (active && !ok) bad |= kErrScale;
       part[r] = lane_dot_digits<GU, 0>(raw[r], sc, mn, X);
     }
+    rows_load_down<DN>(down, hidden, c0, R);
     load_digits<1>(L, c, X);
 #pragma unroll
     for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
@@ -2143,13 +2146,13 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
   } else {
 #pragma unroll
     for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
+      if (r == kRowsWaveNeurons) rows_load_down<DN>(down, hidden, c0, R);
       float sc[2], mn[2];
       const bool ok = raw_scales<GU>(raw[r], c, sc, mn);
       if (active && !ok) bad |= kErrScale;
       dot[r] = wave_total(active ? lane_dot_f32<GU>(raw[r], sc, mn, x, 0.f, 0.f) : 0.f);
     }
   }
-  rows_load_down<DN>(down, hidden, c0, R);
   if (lane < kRowsWaveNeurons) {
     float a = dot[0], u = dot[kRowsWaveNeurons];
 #pragma unroll
