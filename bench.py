@@ -1,9 +1,11 @@
 #!/usr/bin/env python3
 """Layer-share measurement of the expert neuron-slice path on one MI355X.
 
-A step is one layer call of the node backend's run() (src/backend.h:63): one
-kernel launch over every (routed expert, owned 32-neuron slice) pair of a
-request. Default workload: 512 experts x 20 owned slices resident at
+A step is one layer call of the node backend's run() (src/backend.h:63): the
+launch of one decode kernel over every (token, routed expert, owned 32-neuron
+slice) unit of a request, then its fixed-order reduction kernel (the Q4_K
+workloads run decode_kernel, the Q8_0 / MXFP4 / native ones
+decode_rows_kernel). Default workload: 512 experts x 20 owned slices resident at
 hidden=4096, all Q4_K (down stored transposed), one token, 10 experts drawn
 uniformly without replacement, gates = softmax of N(0,1) logits, x ~ N(0,1).
 Weights are synthetic (seeded, generated on the device), resident in HBM
@@ -15,6 +17,9 @@ stdout: exactly one JSON line. Everything else goes to stderr.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload q4k]
                   [--cpu-seconds S] [--no-cpu]
+                  workloads: q4k (the default), mtp4 (4-token Zipf burst),
+                  q8, mxfp4 (all-Q8_0 / all-MXFP4 shares), native (Q4_K
+                  gate/up with an MXFP4 down)
   python bench.py --workload prefill   a step is one 48-layer chunk of 512
                                         tokens through fr_hip_run_batch
   python bench.py --copy-kernel BYTES   plain device copy, for scaling the
