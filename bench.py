@@ -120,6 +120,129 @@ def grid_kernels(lib, plan):
     return {1: "decode_kernel + decode_reduce", 2: "decode_rows_kernel + decode_reduce"}.get(kind, "layer_kernel")
 
 
+def plan_slices(plan):
+    """(device address, bytes) of every unit of a layer plan: the plan header's
+    pair count (byte 12) and pair table offset (byte 40), 48-byte pair
+    descriptors with the slice address at 0 and the gate-row bytes at 8 (a
+    Q4_K slice is three such projections)."""
+    npairs = int(np.frombuffer(plan[12:16].tobytes(), np.uint32)[0])
+    off = int(np.frombuffer(plan[40:44].tobytes(), np.uint32)[0])
+    desc = np.frombuffer(plan[off:off + 48 * npairs].tobytes(), np.uint8).reshape(npairs, 48)
+    addr = desc[:, 0:8].copy().view(np.uint64).ravel()
+    proj = desc[:, 8:12].copy().view(np.uint32).ravel().astype(np.uint64)
+    return addr, 3 * proj
+
+
+def cut_pieces(addr, length, parts):
+    """Each (address, length) range cut into `parts` 16-byte aligned pieces."""
+    out = []
+    for a, n in zip(addr.tolist(), length.tolist()):
+        step = ((n + parts - 1) // parts + 15) // 16 * 16
+        for p in range(parts):
+            lo = p * step
+            if lo < n:
+                out.append((a + lo, min(step, n - lo)))
+    return np.array(out, np.uint64).reshape(-1, 2)
+
+
+def time_probe(lib, tables, threads, depth, reps, sink, stream):
+    """Events around `reps` probe launches on `stream`, rotating over the
+    device piece tables; returns microseconds per launch."""
+    import torch
+    sptr = C.c_void_p(stream.cuda_stream)
+
+    def go(i):
+        t = tables[i % len(tables)]
+        fa_rc = lib.fr_hip_stream_probe(C.c_void_p(t.data_ptr()), t.shape[0], threads, depth,
+                                        C.c_void_p(sink.data_ptr()), sptr)
+        if fa_rc != 0:
+            raise RuntimeError(f"fr_hip_stream_probe failed with {fa_rc}")
+
+    for i in range(len(tables)):
+        go(i)
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(reps):
+            go(i)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):   # replay() runs on the current stream
+        g.replay()
+        stream.synchronize()
+        ev0.record(stream)
+        g.replay()
+        ev1.record(stream)
+    stream.synchronize()
+    return ev0.elapsed_time(ev1) * 1e3 / reps
+
+
+def stream_ceiling(eng, lib, plans, sweep, reps=200):
+    """Achievable read bandwidth for the decode workload: the probe reading
+    (a) the same scattered per-unit slices as the layer plans `plans` and
+    (b) one contiguous buffer of the same size per call, rotated over 8
+    buffers (beyond the 256 MB Infinity Cache), over `sweep` = [(pieces per
+    slice or total pieces, threads, depth)]. Returns the table and the best
+    rate of each kind."""
+    import torch
+    slices = [plan_slices(p) for p in plans]
+    total = int(slices[0][1].sum())
+    stream = torch.cuda.Stream()
+    sink = torch.zeros(16 * 8192, dtype=torch.int32, device="cuda")
+    region = torch.empty(8 * ((total + 4095) // 4096 * 4096), dtype=torch.uint8, device="cuda")
+    region.fill_(7)
+    base = region.data_ptr()
+    rows, best = [], {}
+    for kind, parts, threads, depth in sweep:
+        tables = []
+        for i, (addr, length) in enumerate(slices[:8]):
+            if kind == "scattered":
+                pc = cut_pieces(addr, length, parts)
+            else:
+                start = base + i * ((total + 4095) // 4096 * 4096)
+                pc = cut_pieces(np.array([start], np.uint64), np.array([total], np.uint64), parts)
+            tables.append(torch.from_numpy(pc.view(np.int64).copy()).to("cuda"))
+        us = time_probe(lib, tables, threads, depth, reps, sink, stream)
+        gbs = total / (us * 1e-6) / 1e9
+        rows.append({"kind": kind, "workgroups": int(tables[0].shape[0]), "threads": threads,
+                     "depth": depth, "in_flight_kib_per_wg": threads * depth * 16 // 1024,
+                     "us": round(us, 3), "gbs": round(gbs, 1)})
+        log(f"stream {kind:10s} wg={rows[-1]['workgroups']:5d} threads={threads:4d} depth={depth} "
+            f"{us:8.3f} us {gbs:8.1f} GB/s")
+        if gbs > best.get(kind, {}).get("gbs", 0):
+            best[kind] = rows[-1]
+    return rows, best, total
+
+
+def bench_stream(args):
+    """--workload stream: the achievable-bandwidth sweep over the decode
+    workload's own slices and over a contiguous buffer of the same size."""
+    import torch
+    import fronk_amd as fa
+    lib = fa.lib()
+    eng = fa.Engine(0)
+    for b in range(SLICES):
+        fa.check(eng.synthetic(b, HIDDEN, fa.FMT_Q4KT, LAYERS, SEED), "fr_hip_synthetic")
+    reqs = make_requests(8, 1, "uniform", SEED + 1)
+    plans = [eng.plan(*r, fa.MODE_F32)[0] for r in reqs]
+    sweep = [("scattered", p, t, d) for p in (1, 2, 4) for t in (256, 512, 1024) for d in (1, 2, 4)]
+    sweep += [("contiguous", g, t, d) for g in (200, 256, 512, 1024) for t in (256, 512, 1024) for d in (1, 2, 4)]
+    rows, best, total = stream_ceiling(eng, lib, plans, sweep)
+    for b in range(SLICES):
+        eng.release(b)
+    sc = best["scattered"]
+    print(json.dumps({
+        "metric": "achievable HBM read GB/s (streaming probe over the decode slices)",
+        "value": sc["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": 64, "warmup": 8,
+        "ms_per_step": round(sc["us"] * 1e-3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+        "config": {"workload": "read the 200 Q4_K slices (221,184 B) of a 10-of-512 x 20-slice layer share, "
+                               "or one contiguous buffer of the same size, rotated over 8 layers",
+                   "bytes_per_call": total},
+        "best": best, "sweep": rows, "peak": HBM_PEAK_GBS,
+    }), flush=True)
+
+
 def copy_kernel(nbytes):
     import torch
     a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
@@ -411,7 +534,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="q4k", choices=sorted(WORKLOADS) + ["prefill"])
+    ap.add_argument("--workload", default="q4k", choices=sorted(WORKLOADS) + ["prefill", "stream"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--run-calls", type=int, default=200)
@@ -426,6 +549,9 @@ def main():
         return
     if args.workload == "prefill":
         bench_prefill(args)
+        return
+    if args.workload == "stream":
+        bench_stream(args)
         return
     if args.steps is None:
         args.steps = 1000

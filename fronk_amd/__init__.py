@@ -16,6 +16,9 @@ FMT_LEGACY, FMT_NATIVE, FMT_Q4KT, FMT_Q8, FMT_MXFP4 = 0, 1, 2, 3, 4
 MODE_F32, MODE_F64, MODE_Q8 = 0, 1, 2
 Q4_0, Q8_0, Q4_K, MXFP4 = 2, 8, 12, 39
 MAX_BURST, MAX_HIDDEN, BLOCKS = 8, 4096, 20
+ROUTE_NO_DECODE = 2
+# Plan kinds (the kernel a plan runs), plan header word 16.
+KIND_LAYER, KIND_DECODE, KIND_DECODE_ROWS = 0, 1, 2
 
 LIB_PATH = _build.HIP_LIB
 
@@ -56,6 +59,8 @@ SIGNATURES = {
     "fr_hip_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "fr_hip_last_output": (C.c_int, [C.c_void_p, C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_uint)]),
     "fr_hip_sample_get": (C.c_int, [C.POINTER(Sample)]),
+    "fr_hip_route": (C.c_int, [C.c_uint]),
+    "fr_hip_stream_probe": (C.c_int, [C.c_void_p, C.c_uint, C.c_uint, C.c_uint, C.c_void_p, C.c_void_p]),
     "fr_hip_run_batch": (C.c_int, [C.POINTER(Batch), C.POINTER(C.c_float)]),
     "fr_hip_batch_plan_bytes": (C.c_size_t, [C.c_uint, C.c_uint]),
     "fr_hip_batch_plan": (C.c_int, [C.POINTER(Batch), C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -77,6 +82,14 @@ def lib():
     fallback path."""
     global _lib
     if _lib is None:
+        # torch carries its own HIP runtime (torch/lib/libamdhip64.so, soname
+        # libamdhip64.so.7). Loaded first, it also satisfies this library's
+        # dependency, so the process has one runtime; loaded after this
+        # library, torch would start a second one that finds no GPU.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() (hipcc, gfx950)")
         L = C.CDLL(LIB_PATH)
@@ -195,6 +208,11 @@ class Engine:
         rc = lib().fr_hip_batch_plan(C.byref(req), buf.ctypes.data, cap, C.byref(used))
         check(rc, "fr_hip_batch_plan")
         return buf[:used.value].copy()
+
+    def route(self, flags):
+        """fr_hip_route: send requests past the decode kernels to layer_kernel
+        (ROUTE_NO_DECODE) for plans built from now on; 0 restores the default."""
+        check(lib().fr_hip_route(flags), "fr_hip_route")
 
     def sample(self):
         s = Sample()

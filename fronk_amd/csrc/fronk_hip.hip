@@ -1523,7 +1523,8 @@ __device__ __forceinline__ float header_pass(const uint4& h, unsigned sb, unsign
 // j = l%16 = 4 * sub-block + digit) holds digit j%4 of values 16hh..16hh+15
 // of sub-block 4G + kg for product m = 2G + hh when its column's sub-block
 // is kg, zero otherwise; fx[G] = 2^e * digit weight of its column's sub-block.
-__device__ __forceinline__ void x_operands(unsigned t, unsigned sb, int lane, const DecodeLds& L, i32x4 (&b)[4],
+template <class Lds>
+__device__ __forceinline__ void x_operands(unsigned t, unsigned sb, int lane, const Lds& L, i32x4 (&b)[4],
                                            float (&fx)[2]) {
   const unsigned kg = (unsigned)lane >> 4, j = (unsigned)lane & 15, js = j >> 2, jd = j & 3;
 #pragma unroll
@@ -2956,6 +2957,33 @@ __global__ void debug_quantize32(float* x, uint32_t groups) {
 
 // ================================================================ host
 
+// ------------------------------------------------------------ stream probe
+//
+// Measurement only: the achievable read bandwidth of a set of byte ranges,
+// in the spirit of backends/metal.m:265-270 and tools/avx2-probe.c:12-30.
+// Workgroup b reads pieces[b] = (device address, length) with 16-byte raw
+// buffer loads, each thread keeping DEPTH loads in flight (a load past the
+// piece returns zero without a memory access), and each wavefront stores the
+// XOR of what it read so that the loads stay live.
+template <int DEPTH>
+__global__ __launch_bounds__(1024) void stream_probe(const uint64_t* __restrict__ pieces, uint32_t* __restrict__ sink) {
+  const uint64_t addr = pieces[2 * blockIdx.x], len = pieces[2 * blockIdx.x + 1];
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(addr), (short)0, (int)len, 0x00020000);
+  const uint32_t step = 16u * blockDim.x;
+  uint32_t acc = 0;
+  for (uint32_t off = 16u * threadIdx.x; off < (uint32_t)len; off += DEPTH * step) {
+    u32x4 v[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) v[d] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + d * step), 0, 0);
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) acc ^= v[d][0] ^ v[d][1] ^ v[d][2] ^ v[d][3];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, o, 64);
+  if ((threadIdx.x & 63) == 0) sink[16 * blockIdx.x + (threadIdx.x >> 6)] = acc;
+}
+
 struct Layout {
   uint32_t hidden, format, gu, dn, shared_gu, shared_dn;
   uint64_t proj, down, slice, shared_proj, shared_slice, layer, block;
@@ -3029,6 +3057,11 @@ struct Engine {
   uint32_t out_words = 0;
   float* wgpart = nullptr;        // [kMaxPairs][kMaxHidden]
   uint32_t* bar = nullptr;        // [2]
+  // Read once at open (environment), not per run: the down-phase group
+  // bytes of layer_kernel and the switch that routes requests past the
+  // decode kernels (fr_hip_route changes it later).
+  uint32_t group_bytes = 49152;
+  bool no_decode = false;
   uint8_t* plan_dev = nullptr;
   uint8_t* plan_host = nullptr;   // pinned
   size_t plan_cap = 0;
@@ -3074,8 +3107,7 @@ int env_int(const char* name, int dflt) {
 uint32_t group_pairs(uint8_t dn) {
   uint32_t per = dn == TQ4_KT ? 4608u : kCols * (uint32_t)row_bytes(dn, kNeurons);
   uint32_t cap = dn == TQ8_0 ? group_max<TQ8_0>() : dn == TQ4_KT ? group_max<TQ4_KT>() : group_max<TMXFP4>();
-  int over = env_int("FRONK_HIP_GROUP_BYTES", 49152);
-  uint32_t g = (uint32_t)over / per;
+  uint32_t g = E.group_bytes / per;
   return g < 1 ? 1 : g > cap ? cap : g;
 }
 
@@ -3210,7 +3242,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   uint32_t nunits = 0;
   for (uint32_t t = 0; t < T; ++t) nunits += (10u + (r->gate[t * 11 + 10] != 0.f ? 1u : 0u)) * (uint32_t)nloaded;
   const bool decode = (q4kt || rows) && nunits <= (uint32_t)kMaxPairs;
-  if (decode && !env_int("FRONK_HIP_NO_DECODE", 0)) {
+  if (decode && !E.no_decode) {
     // Units are (token, pair). Their partials are numbered token-major in the
     // reference's order (token, routed expert in request order, ascending
     // block), which the reduction follows; the work list is pair-major, so
@@ -3589,6 +3621,8 @@ int fr_hip_open(int device) {
   CK(hipMalloc(&E.wgpart, (size_t)kMaxPairs * kMaxHidden * sizeof(float)));
   CK(hipMalloc(&E.bar, 2 * sizeof(uint32_t)));
   CK(hipMemset(E.bar, 0, 2 * sizeof(uint32_t)));
+  E.group_bytes = (uint32_t)env_int("FRONK_HIP_GROUP_BYTES", 49152);
+  E.no_decode = env_int("FRONK_HIP_NO_DECODE", 0) != 0;
   CK(hipMemset(E.done, 0, 2 * kMaxPairs * sizeof(uint32_t)));
   CK(hipMemset(E.fin, 0, 2 * kMaxRanges * sizeof(uint32_t)));
   CK(hipMemset(E.out, 0, 2 * (size_t)E.out_words * sizeof(uint32_t)));
@@ -3918,6 +3952,33 @@ int fr_hip_timing_read(double* main_ms, double* total_ms, unsigned* launches) {
 int fr_hip_sample_get(fr_hip_sample* out) {
   if (!out) return FR_HIP_INVALID;
   *out = E.sample;
+  return FR_HIP_OK;
+}
+
+int fr_hip_route(unsigned flags) {
+  if (!g_open) return FR_HIP_STATE;
+  if (flags & ~(unsigned)FR_HIP_ROUTE_NO_DECODE) return FR_HIP_INVALID;
+  E.no_decode = (flags & FR_HIP_ROUTE_NO_DECODE) != 0;
+  return FR_HIP_OK;
+}
+
+int fr_hip_stream_probe(const void* device_pieces, unsigned count, unsigned threads, unsigned depth,
+                        void* device_sink, void* stream) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!device_pieces || !device_sink || !count || count > (1u << 20) || !threads || threads > 1024 || threads % 64)
+    return FR_HIP_INVALID;
+  CK(hipSetDevice(E.device));
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : E.stream;
+  const uint64_t* p = static_cast<const uint64_t*>(device_pieces);
+  uint32_t* k = static_cast<uint32_t*>(device_sink);
+  switch (depth) {
+    case 1: hipLaunchKernelGGL(stream_probe<1>, dim3(count), dim3(threads), 0, s, p, k); break;
+    case 2: hipLaunchKernelGGL(stream_probe<2>, dim3(count), dim3(threads), 0, s, p, k); break;
+    case 4: hipLaunchKernelGGL(stream_probe<4>, dim3(count), dim3(threads), 0, s, p, k); break;
+    case 8: hipLaunchKernelGGL(stream_probe<8>, dim3(count), dim3(threads), 0, s, p, k); break;
+    default: return FR_HIP_INVALID;
+  }
+  CK(hipGetLastError());
   return FR_HIP_OK;
 }
 

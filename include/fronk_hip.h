@@ -111,6 +111,27 @@ int fr_hip_last_output(void *stream, float *y, size_t count, unsigned *status);
 
 int fr_hip_sample_get(fr_hip_sample *out);
 
+/* Kernel selection for comparison tests and measurements (no reference
+ * counterpart). By default a request runs on the first kernel that covers
+ * it: the decode kernels (decode_kernel / decode_rows_kernel and their
+ * fixed-order reduction), then layer_kernel. FR_HIP_ROUTE_NO_DECODE sends
+ * every request to layer_kernel. Applies to plans built after the call;
+ * FRONK_HIP_NO_DECODE in the environment gives the value at open. */
+enum { FR_HIP_ROUTE_NO_DECODE = 2 };
+int fr_hip_route(unsigned flags);
+
+/* Streaming-read probe for the achievable-bandwidth figure (no reference
+ * counterpart; the reference reads its own machine's stream rate in
+ * backends/metal.m:265-270 and tools/avx2-probe.c:12-30). Enqueues on
+ * `stream` one launch of `count` workgroups of `threads` threads (a multiple
+ * of 64, at most 1024): workgroup b reads the device byte range
+ * (pieces[2b], pieces[2b+1]) = (16-byte aligned address, length < 2^31) with
+ * 16-byte loads, `depth` (1, 2, 4 or 8) loads in flight per thread, and
+ * stores 16 words to sink[16b..16b+15]. `device_pieces` and `device_sink`
+ * are device memory the caller owns. */
+int fr_hip_stream_probe(const void *device_pieces, unsigned count, unsigned threads, unsigned depth,
+                        void *device_sink, void *stream);
+
 /* Prefill chunk on matrix cores (config "resident node, 512-token prefill").
  * The reference has no multi-token entry beyond run()'s burst of 8: its
  * client cuts longer prompts into bursts (client/fronk_client.h:41-42) and

@@ -49,7 +49,7 @@ def host_units(lay, seed, experts, shared):
 @pytest.mark.parametrize("fmt,hidden", [(fa.FMT_NATIVE, 4096), (fa.FMT_NATIVE, 2560), (fa.FMT_Q8, 4096),
                                         (fa.FMT_MXFP4, 4096)])
 @pytest.mark.parametrize("shared", [False, True])
-def test_rows_kernel_agrees_with_oracle_and_layer_kernel(eng, fmt, hidden, shared, monkeypatch):
+def test_rows_kernel_agrees_with_oracle_and_layer_kernel(eng, fmt, hidden, shared):
     lay = oracle.layout(hidden, fmt)
     seed = 9100 + 10 * fmt + hidden
     rng = np.random.default_rng(seed)
@@ -73,7 +73,7 @@ def test_rows_kernel_agrees_with_oracle_and_layer_kernel(eng, fmt, hidden, share
         rc, again = eng.run(0, experts, gates, x, fa.MODE_F32)
         assert rc == fa.OK
         assert np.array_equal(y.view(np.uint32), again.view(np.uint32))
-        monkeypatch.setenv("FRONK_HIP_NO_DECODE", "1")
+        eng.route(fa.ROUTE_NO_DECODE)
         kind, _ = plan_kind(eng, 0, experts, gates, x)
         assert kind == 0
         print(f"layer kernel fmt={fmt} hidden={hidden} shared={shared}", flush=True)
@@ -81,6 +81,7 @@ def test_rows_kernel_agrees_with_oracle_and_layer_kernel(eng, fmt, hidden, share
         assert rc == fa.OK
         check_close(ref, y_lay, fa.MODE_F32, ("layer", fmt, hidden, shared))
     finally:
+        eng.route(0)
         for b in range(20):
             eng.release(b)
 

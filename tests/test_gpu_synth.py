@@ -158,10 +158,10 @@ def plan_kind(eng, layer, experts, gates, x):
 
 
 @pytest.mark.parametrize("hidden", [4096, 2560])
-def test_decode_kernel_and_layer_kernel_agree_with_oracle(eng, hidden, monkeypatch):
-    """Single-token all-Q4_K requests run on the decode kernel (tasks of 8
-    neurons, no h exchange); the same request forced onto the two-phase
-    layer kernel must match the oracle as well."""
+def test_decode_kernel_and_layer_kernel_agree_with_oracle(eng, hidden):
+    """Single-token all-Q4_K requests run on decode_kernel + decode_reduce;
+    the same request routed to the two-phase layer_kernel must match the
+    oracle as well, and each route repeats bit for bit."""
     lay = oracle.layout(hidden, fa.FMT_Q4KT)
     seed = 4242 + hidden
     rng = np.random.default_rng(hidden)
@@ -181,22 +181,19 @@ def test_decode_kernel_and_layer_kernel_agree_with_oracle(eng, hidden, monkeypat
         req = oracle_request(0, experts, gates, x)
         rc, ref = oracle.ref_run(units, fa.FMT_Q4KT, False, req)
         assert rc == 0
-        kind, grid = plan_kind(eng, 0, experts, gates, x)
-        assert kind == 1 and 0 < grid <= 256, (kind, grid)
-        print(f"decode kernel hidden={hidden} grid={grid}", flush=True)
-        rc, y_dec = eng.run(0, experts, gates, x, fa.MODE_F32)
-        assert rc == fa.OK
-        check_close(ref, y_dec, fa.MODE_F32, ("decode", hidden))
-        rc, again = eng.run(0, experts, gates, x, fa.MODE_F32)
-        assert np.array_equal(y_dec.view(np.uint32), again.view(np.uint32))
-        monkeypatch.setenv("FRONK_HIP_NO_DECODE", "1")
-        kind, grid = plan_kind(eng, 0, experts, gates, x)
-        assert kind == 0
-        print(f"layer kernel hidden={hidden} grid={grid}", flush=True)
-        rc, y_lay = eng.run(0, experts, gates, x, fa.MODE_F32)
-        assert rc == fa.OK
-        check_close(ref, y_lay, fa.MODE_F32, ("layer", hidden))
+        for route, want in [(0, fa.KIND_DECODE), (fa.ROUTE_NO_DECODE, fa.KIND_LAYER)]:
+            eng.route(route)
+            kind, grid = plan_kind(eng, 0, experts, gates, x)
+            assert kind == want, (route, kind)
+            print(f"route={route} kind={kind} hidden={hidden} grid={grid}", flush=True)
+            rc, y = eng.run(0, experts, gates, x, fa.MODE_F32)
+            assert rc == fa.OK
+            check_close(ref, y, fa.MODE_F32, ("route", route, hidden))
+            rc, again = eng.run(0, experts, gates, x, fa.MODE_F32)
+            assert rc == fa.OK
+            assert np.array_equal(y.view(np.uint32), again.view(np.uint32))
     finally:
+        eng.route(0)
         for b in range(20):
             eng.release(b)
 
@@ -219,7 +216,7 @@ def test_decode_burst_rows_equal_single_token_runs(eng, burst):
         gates[:, :10] = softmax_gates(rng, burst)
         x = rng.standard_normal((burst, hidden)).astype(np.float32)
         kind, grid = plan_kind(eng, 0, experts, gates, x)
-        assert kind == 1 and 0 < grid <= 256, (kind, grid)
+        assert kind == fa.KIND_DECODE and 0 < grid <= 256, (kind, grid)
         print(f"decode burst={burst} grid={grid}", flush=True)
         rc, y = eng.run(0, experts, gates, x, fa.MODE_F32)
         assert rc == fa.OK
