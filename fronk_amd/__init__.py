@@ -58,6 +58,7 @@ SIGNATURES = {
                               C.POINTER(C.c_uint)]),
     "fr_hip_launch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "fr_hip_last_output": (C.c_int, [C.c_void_p, C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_uint)]),
+    "fr_hip_launch_static": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "fr_hip_sample_get": (C.c_int, [C.POINTER(Sample)]),
     "fr_hip_route": (C.c_int, [C.c_uint]),
     "fr_hip_stream_probe": (C.c_int, [C.c_void_p, C.c_uint, C.c_uint, C.c_uint, C.c_void_p, C.c_void_p]),

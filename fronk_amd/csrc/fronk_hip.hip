@@ -106,10 +106,16 @@ struct Scratch {
   float* hbuf;               // [kMaxPairs][8][32]
   double* partial;           // [groups][burst][hidden]
   uint32_t* out;             // [2][out_words]: status, pad x3, y
-  float* wgpart;             // decode unit partials, [kMaxHidden/16][kMaxPairs][16] (partial_index)
+  float* wgpart;             // decode unit partials, [kMaxHidden/16][ustride][16] (partial_index)
   uint32_t* bar;             // [2]: decode workgroups past their partial store
   uint32_t out_words;
   uint32_t parity;
+  uint32_t ustride;          // units per position block of wgpart
+  // Set by fr_hip_launch_static, null otherwise: the caller's status word
+  // and y, and the decode kernels' error word in the static scratch array.
+  uint32_t* ystat;
+  float* yout;
+  uint32_t* dstat;
 };
 
 // ------------------------------------------------------------ scalars
@@ -1637,30 +1643,43 @@ __device__ __forceinline__ void down_round(const DecodeDnBytes& R, const float* 
 }
 
 // Unit partials, [position block][unit][16 positions]: position p of unit u
-// at float (p/16 * kMaxPairs + u) * 16 + p%16, so that decode_reduce's
-// workgroup for one block of 16 positions reads its units' values as one
-// contiguous run.
-__device__ __forceinline__ size_t partial_index(unsigned unit, unsigned p) {
-  return ((size_t)(p >> 4) * kMaxPairs + unit) * 16 + (p & 15);
+// at float (p/16 * stride + u) * 16 + p%16 (stride: units per block), so
+// that decode_reduce's workgroup for one block of 16 positions reads its
+// units' values as one contiguous run.
+__device__ __forceinline__ size_t partial_index(unsigned unit, unsigned p, unsigned stride) {
+  return ((size_t)(p >> 4) * stride + unit) * 16 + (p & 15);
 }
 
 // The unit's fp32 partial: wavefront w, half h, lane l -> positions
 // 4*(128w + 64h + l)..+3, columns 256*sb + 8j + 4h..+3 (sb = 2w + l/32,
 // j = l%32), four lanes to a 64-byte piece; y restarts at 0. The kernel
 // boundary makes the partials visible to decode_reduce.
-__device__ __forceinline__ void store_partial(float* wgpart, unsigned unit, int wave, int lane, float (&y)[8]) {
+__device__ __forceinline__ void store_partial(float* wgpart, unsigned stride, unsigned unit, int wave, int lane,
+                                              float (&y)[8]) {
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh)
-    *reinterpret_cast<float4*>(wgpart + partial_index(unit, 4 * (128 * wave + 64 * hh + lane))) =
+    *reinterpret_cast<float4*>(wgpart + partial_index(unit, 4 * (128 * wave + 64 * hh + lane), stride)) =
         make_float4(y[4 * hh], y[4 * hh + 1], y[4 * hh + 2], y[4 * hh + 3]);
 #pragma unroll
   for (int i = 0; i < 8; ++i) y[i] = 0.f;
 }
 
+// The status word the decode kernels flag errors into, and block 0's
+// set-up: the engine's launches clear the next launch's parity; a static
+// launch zeroes the caller's status word (which only decode_reduce, a later
+// kernel, writes) and flags into the static error word, which decode_reduce
+// folds into it and zeroes again.
+__device__ __forceinline__ uint32_t* decode_status(const Scratch& S) {
+  if (blockIdx.x == 0) {
+    if (!S.ystat) clear_other_parity(S);
+    else if (threadIdx.x == 0) *S.ystat = 0;
+  }
+  return S.ystat ? S.dstat : S.out + (size_t)S.parity * S.out_words;
+}
+
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
-  uint32_t* status = S.out + (size_t)S.parity * S.out_words;
-  if (blockIdx.x == 0) clear_other_parity(S);
+  uint32_t* status = decode_status(S);
   const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
   const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden)), nsb = hidden / 256, nsub = hidden / 32;
   const unsigned np = plan_field(PH, offsetof(PlanHeader, npairs)), tpw = plan_field(PH, offsetof(PlanHeader, tpw));
@@ -1786,7 +1805,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
       __builtin_amdgcn_wave_barrier();
     }
     down_round(D[3], L.h[wave], wave, lane, nsb, L, y, bad);
-    store_partial(S.wgpart, plan_read(upart + p), wave, lane, y);
+    store_partial(S.wgpart, S.ustride, plan_read(upart + p), wave, lane, y);
     if (!more) break;
     stage_x(xv, par ^ 1, nsub, true, L, bad);
     __syncthreads();   // the next unit's x is in LDS
@@ -1823,8 +1842,13 @@ __device__ __forceinline__ double xor_d(double v, int m) {
 __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
   const DecodeToken tk = reinterpret_cast<const DecodeToken*>(plan + H.groups_off)[blockIdx.y];
-  uint32_t* status = S.out + (size_t)S.parity * S.out_words;
-  float* yout = reinterpret_cast<float*>(status + 4) + (size_t)blockIdx.y * H.hidden;
+  uint32_t* status = S.ystat ? S.ystat : S.out + (size_t)S.parity * S.out_words;
+  float* yout = (S.ystat ? S.yout : reinterpret_cast<float*>(status + 4)) + (size_t)blockIdx.y * H.hidden;
+  if (S.ystat && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+    const uint32_t e = *S.dstat;   // written by decode_kernel (kernel boundary)
+    if (e) flag(status, e);
+    *S.dstat = 0;                  // zero for the next static launch
+  }
   const unsigned tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane & 3;
   const unsigned ps = 16 * wave + (lane >> 2);
   const unsigned p0 = kReducePositions * blockIdx.x + 4 * q;
@@ -1832,7 +1856,7 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
 #pragma unroll
   for (unsigned k = 0; k < kReduceDepth; ++k) {
     const unsigned g = ps + kReduceLanes * k;
-    r[k] = g < tk.count ? *reinterpret_cast<const float4*>(S.wgpart + partial_index(tk.first + g, p0))
+    r[k] = g < tk.count ? *reinterpret_cast<const float4*>(S.wgpart + partial_index(tk.first + g, p0, S.ustride))
                         : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   double v[4] = {0.0, 0.0, 0.0, 0.0};
@@ -2068,7 +2092,8 @@ __device__ __forceinline__ void rows_down(const RowsDown& R, const float* hs, fl
 // LDS and held in registers (two codes per conversion); the integer formats
 // dot in integers against x's digits staged in LDS.
 template <int GU, int DN>
-__device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, const PairDesc* P, const float* xg,
+__device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned ustride, unsigned unit, const PairDesc* P,
+                                              const float* xg,
                                               unsigned hidden, int wave, int lane, RowsLds& L) {
   const uint32_t* w = reinterpret_cast<const uint32_t*>(P);
   const uint64_t slice = ((uint64_t)uniform(plan_read(w + 1)) << 32) | uniform(plan_read(w));
@@ -2167,7 +2192,7 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
   __syncthreads();   // the unit's 32 h are in LDS (and every lane has its digits)
   float y[8];
   rows_down<DN>(R, L.h, gate, dvalid, y, bad);
-  store_partial(wgpart, unit, wave, lane, y);
+  store_partial(wgpart, ustride, unit, wave, lane, y);
   __syncthreads();   // h is read before the next unit writes it
   return bad;
 }
@@ -2177,8 +2202,7 @@ __device__ __forceinline__ uint32_t rows_unit(float* wgpart, unsigned unit, cons
 template <int GA, int DA, int GB, int DB>
 __global__ __launch_bounds__(kDecodeThreads) void decode_rows_kernel(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
-  uint32_t* status = S.out + (size_t)S.parity * S.out_words;
-  if (blockIdx.x == 0) clear_other_parity(S);
+  uint32_t* status = decode_status(S);
   const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
   const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden));
   const unsigned np = plan_field(PH, offsetof(PlanHeader, npairs)), tpw = plan_field(PH, offsetof(PlanHeader, tpw));
@@ -2196,9 +2220,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rows_kernel(const uint8
     const uint32_t w3 = uniform(plan_read(reinterpret_cast<const uint32_t*>(P) + 3));
     const uint32_t gu = w3 & 0xffu, dn = (w3 >> 8) & 0xffu;
     const unsigned unit = plan_read(upart + p);
-    if (GA == GB && DA == DB) bad |= rows_unit<GA, DA>(S.wgpart, unit, P, xg, hidden, wave, lane, L);
-    else if (gu == GA && dn == DA) bad |= rows_unit<GA, DA>(S.wgpart, unit, P, xg, hidden, wave, lane, L);
-    else bad |= rows_unit<GB, DB>(S.wgpart, unit, P, xg, hidden, wave, lane, L);
+    if (GA == GB && DA == DB) bad |= rows_unit<GA, DA>(S.wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
+    else if (gu == GA && dn == DA) bad |= rows_unit<GA, DA>(S.wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
+    else bad |= rows_unit<GB, DB>(S.wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
   }
   if (bad) flag(status, bad);
 }
@@ -2957,6 +2981,19 @@ __global__ void debug_quantize32(float* x, uint32_t groups) {
 
 // ================================================================ host
 
+// ------------------------------------------------------ static scratch
+//
+// fr_hip_launch_static's scratch, for callers that cannot allocate: the
+// decode kernels' error word (in a 256-byte first block), then the unit
+// partials of up to kStaticUnits units ([position block][unit][16]). Each
+// GPU the library runs on holds it (3.7 MB) until the process ends. Host
+// code reaches it only through the address hipGetSymbolAddress returns.
+constexpr uint32_t kStaticUnits = 224;   // one token: 10 routed and the shared expert x 20 blocks
+constexpr size_t kStaticHead = 64;       // floats before the partials (the error word, padded)
+constexpr size_t kStaticFloats = kStaticHead + (size_t)(kMaxHidden / 16) * kStaticUnits * 16;
+static __device__ __align__(256) float scratch[kStaticFloats];
+static_assert(kDecodeUnitsPerToken <= (int)kStaticUnits, "a token's units fit the static scratch");
+
 // ------------------------------------------------------------ stream probe
 //
 // Measurement only: the achievable read bandwidth of a set of byte ranges,
@@ -3057,6 +3094,7 @@ struct Engine {
   uint32_t out_words = 0;
   float* wgpart = nullptr;        // [kMaxPairs][kMaxHidden]
   uint32_t* bar = nullptr;        // [2]
+  float* static_scratch = nullptr;   // device address of `scratch` on this engine's device
   // Read once at open (environment), not per run: the down-phase group
   // bytes of layer_kernel and the switch that routes requests past the
   // decode kernels (fr_hip_route changes it later).
@@ -3318,6 +3356,40 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   return FR_HIP_OK;
 }
 
+// decode_kernel or the decode_rows_kernel instantiation of the plan's unit
+// formats, then decode_reduce, on `stream`; `mid`, if set, is recorded
+// between them. Returns false if an event could not be recorded.
+bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, const Scratch& S, hipStream_t stream,
+                   hipEvent_t mid) {
+  const dim3 g(grid), b(kDecodeThreads);
+  if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, b, 0, stream, dev_plan, S);
+  else switch (H.pad) {   // (routed formats, shared formats) of the units the request has
+    case COMBO_NATIVE:
+      hipLaunchKernelGGL((decode_rows_kernel<TQ4_K, TMXFP4, TQ4_K, TMXFP4>), g, b, 0, stream, dev_plan, S);
+      break;
+    case COMBO_NATIVE | kComboShared:
+      hipLaunchKernelGGL((decode_rows_kernel<TQ4_K, TMXFP4, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
+      break;
+    case COMBO_Q8:
+    case COMBO_Q8 | kComboShared:
+      hipLaunchKernelGGL((decode_rows_kernel<TQ8_0, TQ8_0, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
+      break;
+    case COMBO_MXFP4:
+      hipLaunchKernelGGL((decode_rows_kernel<TMXFP4, TMXFP4, TMXFP4, TMXFP4>), g, b, 0, stream, dev_plan, S);
+      break;
+    case COMBO_MXFP4 | kComboShared:
+      hipLaunchKernelGGL((decode_rows_kernel<TMXFP4, TMXFP4, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_rows_kernel<TQ4_0, TQ4_0, TQ4_0, TQ4_0>), g, b, 0, stream, dev_plan, S);
+      break;
+  }
+  if (mid && hipEventRecord(mid, stream) != hipSuccess) return false;
+  hipLaunchKernelGGL(decode_reduce, dim3(kMaxHidden / kReducePositions, H.burst), dim3(kReduceThreads), 0, stream,
+                     dev_plan, S);
+  return true;
+}
+
 int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream) {
   if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
   const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS;
@@ -3333,37 +3405,16 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
   S.bar = E.bar;
   S.out_words = E.out_words;
   S.parity = E.parity;
+  S.ustride = kMaxPairs;
+  S.ystat = nullptr;
+  S.yout = nullptr;
+  S.dstat = nullptr;
   const dim3 g(grid), blk(kThreads);
   const bool one = H.burst == 1;
   hipEvent_t* te = E.timing && E.timed < E.timed_cap ? E.tev + 3 * E.timed++ : nullptr;
   if (te && hipEventRecord(te[0], stream) != hipSuccess) return FR_HIP_IO;
   if (decode) {
-    const dim3 b(kDecodeThreads);
-    if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, b, 0, stream, dev_plan, S);
-    else switch (H.pad) {   // (routed formats, shared formats) of the units the request has
-      case COMBO_NATIVE:
-        hipLaunchKernelGGL((decode_rows_kernel<TQ4_K, TMXFP4, TQ4_K, TMXFP4>), g, b, 0, stream, dev_plan, S);
-        break;
-      case COMBO_NATIVE | kComboShared:
-        hipLaunchKernelGGL((decode_rows_kernel<TQ4_K, TMXFP4, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
-        break;
-      case COMBO_Q8:
-      case COMBO_Q8 | kComboShared:
-        hipLaunchKernelGGL((decode_rows_kernel<TQ8_0, TQ8_0, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
-        break;
-      case COMBO_MXFP4:
-        hipLaunchKernelGGL((decode_rows_kernel<TMXFP4, TMXFP4, TMXFP4, TMXFP4>), g, b, 0, stream, dev_plan, S);
-        break;
-      case COMBO_MXFP4 | kComboShared:
-        hipLaunchKernelGGL((decode_rows_kernel<TMXFP4, TMXFP4, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
-        break;
-      default:
-        hipLaunchKernelGGL((decode_rows_kernel<TQ4_0, TQ4_0, TQ4_0, TQ4_0>), g, b, 0, stream, dev_plan, S);
-        break;
-    }
-    if (te && hipEventRecord(te[1], stream) != hipSuccess) return FR_HIP_IO;
-    hipLaunchKernelGGL(decode_reduce, dim3(kMaxHidden / kReducePositions, H.burst), dim3(kReduceThreads), 0, stream,
-                       dev_plan, S);
+    if (!launch_decode(dev_plan, H, grid, S, stream, te ? te[1] : nullptr)) return FR_HIP_IO;
   } else switch (H.mode) {
     case MODE_F32:
       if (one) hipLaunchKernelGGL((layer_kernel<MODE_F32, 1>), g, blk, H.lds, stream, dev_plan, S);
@@ -3621,6 +3672,9 @@ int fr_hip_open(int device) {
   CK(hipMalloc(&E.wgpart, (size_t)kMaxPairs * kMaxHidden * sizeof(float)));
   CK(hipMalloc(&E.bar, 2 * sizeof(uint32_t)));
   CK(hipMemset(E.bar, 0, 2 * sizeof(uint32_t)));
+  // The static scratch array's address on this device (the name is a host
+  // stand-in); it starts zeroed, as the error word must.
+  CK(hipGetSymbolAddress(reinterpret_cast<void**>(&E.static_scratch), HIP_SYMBOL(scratch)));
   E.group_bytes = (uint32_t)env_int("FRONK_HIP_GROUP_BYTES", 49152);
   E.no_decode = env_int("FRONK_HIP_NO_DECODE", 0) != 0;
   CK(hipMemset(E.done, 0, 2 * kMaxPairs * sizeof(uint32_t)));
@@ -3822,6 +3876,32 @@ int fr_hip_launch(const void* host_plan, const void* device_plan, void* stream) 
     return FR_HIP_INVALID;
   return launch(static_cast<const uint8_t*>(device_plan), H, H.grid,
                 stream ? static_cast<hipStream_t>(stream) : E.stream);
+}
+
+int fr_hip_launch_static(const void* host_plan, const void* device_plan, float* device_y, unsigned* device_status,
+                         void* stream) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!host_plan || !device_plan || !device_y || !device_status) return FR_HIP_INVALID;
+  const PlanHeader& H = *static_cast<const PlanHeader*>(host_plan);
+  // Plans this variant runs: one token, decode kernels, units within the
+  // static scratch.
+  if (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS) return FR_HIP_UNSUPPORTED;
+  if (H.burst != 1 || H.npairs > kStaticUnits || !H.hidden || H.hidden > (unsigned)kMaxHidden) return FR_HIP_UNSUPPORTED;
+  if (!H.grid || H.grid > (unsigned)kDecodeGridMax || H.grid > H.npairs || H.ngroups != H.burst) return FR_HIP_INVALID;
+  if (H.kind == KIND_DECODE_ROWS && (H.pad & ~kComboShared) > COMBO_Q4_0) return FR_HIP_INVALID;
+  if (!E.static_scratch) return FR_HIP_STATE;
+  CK(hipSetDevice(E.device));
+  Scratch S = {};
+  S.wgpart = E.static_scratch + kStaticHead;
+  S.ustride = kStaticUnits;
+  S.ystat = reinterpret_cast<uint32_t*>(device_status);
+  S.yout = device_y;
+  S.dstat = reinterpret_cast<uint32_t*>(E.static_scratch);
+  if (!launch_decode(static_cast<const uint8_t*>(device_plan), H, H.grid, S,
+                     stream ? static_cast<hipStream_t>(stream) : E.stream, nullptr))
+    return FR_HIP_IO;
+  CK(hipGetLastError());
+  return FR_HIP_OK;
 }
 
 int fr_hip_last_output(void* stream, float* y, size_t count, unsigned* status) {

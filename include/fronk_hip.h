@@ -109,6 +109,24 @@ int fr_hip_launch(const void *host_plan, const void *device_plan, void *stream);
  * (burst*hidden floats) to the host. */
 int fr_hip_last_output(void *stream, float *y, size_t count, unsigned *status);
 
+/* fr_hip_launch for callers that cannot allocate (no reference counterpart):
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. It calls no allocating routine: the decode kernels' scratch is
+ * a static device array of the library (the unit partials of up to 224
+ * units, 3.7 MB, held by each GPU the library runs on until the process
+ * ends), and y and the status word are device memory the caller passes.
+ * Runs plans of one token whose units take the decode kernels
+ * (decode_kernel or decode_rows_kernel, then the fixed-order reduction):
+ * up to 224 units, i.e. 10 routed experts and the shared one over 20
+ * blocks; anything else returns FR_HIP_UNSUPPORTED. Enqueued on `stream`
+ * (NULL = the library stream); when it completes, *device_status is 0 and
+ * device_y holds the hidden outputs, or *device_status has the error bits
+ * (FR_NUMERIC cases; device_y is then unspecified). Calls that overlap on
+ * one GPU share its static array and race; successive calls need nothing
+ * cleared between them. */
+int fr_hip_launch_static(const void *host_plan, const void *device_plan, float *device_y, unsigned *device_status,
+                         void *stream);
+
 int fr_hip_sample_get(fr_hip_sample *out);
 
 /* Kernel selection for comparison tests and measurements (no reference

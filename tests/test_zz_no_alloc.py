@@ -1,0 +1,101 @@
+"""fr_hip_launch_static: the launch that allocates nothing (for callers under
+graph capture or in loops that forbid hipMalloc). Its unit partials live in
+the library's static device array; y and the status word are the caller's.
+
+Checked against the engine's own launch of the same plan (fr_hip_launch +
+fr_hip_last_output) bit for bit, on two calls in a row, the second with a
+smaller request (half the owned blocks, so half the units), and on the error
+path; plans it does not run return FR_UNSUPPORTED.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import fronk_amd as fa
+from fixtures import softmax_gates, zipf_routes
+
+pytestmark = pytest.mark.gpu
+
+H = 4096
+
+
+def device_plan(plan):
+    import torch
+    return torch.from_numpy(plan.copy()).to("cuda")
+
+
+def engine_launch(lib, plan, dplan, stream):
+    assert lib.fr_hip_launch(plan.ctypes.data, C.c_void_p(dplan.data_ptr()), stream) == fa.OK
+    y = np.zeros(H, np.float32)
+    st = C.c_uint(0)
+    assert lib.fr_hip_last_output(stream, fa.fptr(y), H, C.byref(st)) == fa.OK
+    return y, st.value
+
+
+def static_launch(lib, plan, dplan, ydev, sdev, stream):
+    import torch
+    rc = lib.fr_hip_launch_static(plan.ctypes.data, C.c_void_p(dplan.data_ptr()), C.c_void_p(ydev.data_ptr()),
+                                  C.c_void_p(sdev.data_ptr()), stream)
+    if rc != fa.OK:
+        return rc, None, None
+    torch.cuda.synchronize()
+    return rc, ydev.cpu().numpy().copy(), int(sdev.cpu().numpy()[0])
+
+
+def test_static_launch_matches_engine_launch():
+    import torch
+    lib = fa.lib()
+    eng = fa.Engine(0)
+    rng = np.random.default_rng(77)
+    s = torch.cuda.Stream()
+    sp = C.c_void_p(s.cuda_stream)
+    # The caller's outputs, filled with garbage that the launch must replace.
+    ydev = torch.full((H,), float("nan"), dtype=torch.float32, device="cuda")
+    sdev = torch.full((1,), 0x5A5A, dtype=torch.int32, device="cuda")
+    for b in range(20):
+        assert eng.synthetic(b, H, fa.FMT_Q4KT, 1, 4040 + b) == fa.OK
+    try:
+        for call, blocks in enumerate((20, 10)):
+            for b in range(blocks, 20):
+                eng.release(b)
+            experts = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+            gates = np.zeros((1, 11), np.float32)
+            gates[:, :10] = softmax_gates(rng, 1)
+            x = rng.standard_normal((1, H)).astype(np.float32)
+            plan, grid = eng.plan(0, experts, gates, x, fa.MODE_F32)
+            npairs = int(plan[12:16].view(np.uint32)[0])
+            assert npairs == 10 * blocks
+            dplan = device_plan(plan)
+            print(f"static launch call {call}: {npairs} units, grid {grid}", flush=True)
+            rc, ys, st = static_launch(lib, plan, dplan, ydev, sdev, sp)
+            assert rc == fa.OK and st == 0, (rc, st)
+            ye, ste = engine_launch(lib, plan, dplan, sp)
+            assert ste == 0
+            assert np.array_equal(ys.view(np.uint32), ye.view(np.uint32)), call
+        # Error path: an fp32 overflow sets the status word; then a clean
+        # call clears it.
+        print("static launch error path", flush=True)
+        big = np.full((1, H), 3e38, np.float32)
+        plan, _ = eng.plan(0, experts, gates, big, fa.MODE_F32)
+        rc, _, st = static_launch(lib, plan, device_plan(plan), ydev, sdev, sp)
+        assert rc == fa.OK and st != 0
+        plan, _ = eng.plan(0, experts, gates, x, fa.MODE_F32)
+        dplan = device_plan(plan)
+        rc, ys, st = static_launch(lib, plan, dplan, ydev, sdev, sp)
+        assert rc == fa.OK and st == 0
+        ye, _ = engine_launch(lib, plan, dplan, sp)
+        assert np.array_equal(ys.view(np.uint32), ye.view(np.uint32))
+        # Plans it does not run: a 4-token burst, a layer_kernel plan.
+        ex4 = zipf_routes(rng, 4)
+        g4 = np.zeros((4, 11), np.float32)
+        g4[:, :10] = softmax_gates(rng, 4)
+        plan4, _ = eng.plan(0, ex4, g4, rng.standard_normal((4, H)).astype(np.float32), fa.MODE_F32)
+        assert lib.fr_hip_launch_static(plan4.ctypes.data, C.c_void_p(device_plan(plan4).data_ptr()),
+                                        C.c_void_p(ydev.data_ptr()), C.c_void_p(sdev.data_ptr()), sp) == fa.UNSUPPORTED
+        planf, _ = eng.plan(0, experts, gates, x, fa.MODE_F64)
+        assert lib.fr_hip_launch_static(planf.ctypes.data, C.c_void_p(device_plan(planf).data_ptr()),
+                                        C.c_void_p(ydev.data_ptr()), C.c_void_p(sdev.data_ptr()), sp) == fa.UNSUPPORTED
+    finally:
+        for b in range(20):
+            eng.release(b)
