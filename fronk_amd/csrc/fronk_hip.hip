@@ -129,6 +129,18 @@ __device__ __forceinline__ bool half_bad(uint32_t bits) { return (bits & 0x7c00u
 __device__ __forceinline__ float e8m0(uint32_t e) {
   return __uint_as_float(e ? e << 23 : 0x00400000u);
 }
+// An MXFP4 block (E8M0 exponent e, its 32 codes in q) holding a weight that
+// the reference decodes to a non-finite value (src/native.c:23-27: the fp32
+// product 2^(e-127) * code value, which run() turns into FR_NUMERIC): e = 255,
+// a code of magnitude >= 2 (codes with bit 2 set: 2, 3, 4, 6) at e = 254,
+// where 2 * 2^127 = 2^128 overflows, or of magnitude >= 4 (bits 2 and 1 set:
+// 4, 6) at e = 253.
+__device__ __forceinline__ bool mx_block_bad(uint32_t e, const uint4& q) {
+  const uint32_t ge2 = (q.x | q.y | q.z | q.w) & 0x44444444u;
+  const uint32_t ge4 = ((q.x & (q.x >> 1)) | (q.y & (q.y >> 1)) | (q.z & (q.z >> 1)) | (q.w & (q.w >> 1))) & 0x22222222u;
+  return e == 255u || (e == 254u && ge2 != 0u) || (e == 253u && ge4 != 0u);
+}
+
 // Two OCP E2M1 codes (byte b of v: low nibble first) -> floats times
 // `scale`, with the gfx950 conversion instruction. The products are exact
 // (E2M1 values have two significant bits, scales are powers of two, the
@@ -425,7 +437,7 @@ __device__ __forceinline__ bool raw_scales(const LaneRaw& r, int c, float s[2], 
     s[0] = e8m0(r.h.x & 0xff);
     s[1] = e8m0((r.h.x >> 8) & 0xff);
     m[0] = m[1] = 0.f;
-    return (r.h.x & 0xff) != 255 && ((r.h.x >> 8) & 0xff) != 255;
+    return !mx_block_bad(r.h.x & 0xff, r.q[0]) && !mx_block_bad((r.h.x >> 8) & 0xff, r.q[1]);
   } else {  // Q8_0, Q4_0: two fp16 scales
     s[0] = half_to_float(r.h.x & 0xffff);
     s[1] = half_to_float(r.h.x >> 16);
@@ -845,7 +857,7 @@ __device__ bool decode_down_row(uint8_t dn, const uint8_t* down, unsigned hidden
   if (dn == TMXFP4) {
     uint4 q = ld16(down + 16 * (size_t)d);
     uint32_t e = down[16 * (size_t)hidden + d];
-    ok = e != 255;
+    ok = !mx_block_bad(e, q);
     float sc = e8m0(e);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -993,7 +1005,7 @@ __device__ __forceinline__ uint32_t phase_b_rows(const PlanHeader& H, const Scra
     if (MODE == MODE_F32) {
       float sc;
       if (DN == TMXFP4) {
-        if (sw[j] == 255) bad |= kErrScale;
+        if (mx_block_bad(sw[j], q0[j])) bad |= kErrScale;
         sc = e8m0(sw[j]);
       } else {
         if (half_bad(sw[j])) bad |= kErrScale;
@@ -1052,7 +1064,7 @@ __device__ __forceinline__ uint32_t phase_b_rows(const PlanHeader& H, const Scra
       // Exact decode of the row (decode_down_row semantics) from registers.
       float w[32];
       if (DN == TMXFP4) {
-        if (sw[j] == 255) bad |= kErrScale;
+        if (mx_block_bad(sw[j], q0[j])) bad |= kErrScale;
         const float sc = e8m0(sw[j]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -2035,7 +2047,7 @@ __device__ __forceinline__ void rows_down(const RowsDown& R, const float* hs, fl
     float sc;
     if (DN == TMXFP4) {
       const uint32_t e = (word(R.sc, o >> 2) >> (8 * (o & 3))) & 0xffu;
-      if (valid && e == 255) bad |= kErrScale;
+      if (valid && mx_block_bad(e, R.q0[o])) bad |= kErrScale;
       sc = e8m0(e);
     } else {
       const uint32_t hb = (word(R.sc, o >> 1) >> (16 * (o & 1))) & 0xffffu;
@@ -2083,7 +2095,11 @@ __device__ __forceinline__ void rows_down(const RowsDown& R, const float* hs, fl
       }
       if (DN == TQ4_0) sum -= 8.f * hsum;
     }
-    y[o] = valid ? gate * (sc * sum) : 0.f;
+    // The reference forms gate * (W h) in fp64 (backends/ref.c:86-92): a zero
+    // gate adds exactly nothing, and a product that only overflows fp32 in
+    // the order sc * sum is formed as (gate * sc) * sum instead.
+    const float t = sc * sum;
+    y[o] = !valid || gate == 0.f ? 0.f : isfinite(t) ? gate * t : (gate * sc) * sum;
   }
 }
 
@@ -3130,6 +3146,7 @@ struct Engine {
 };
 Engine E;
 bool g_open = false;
+void release_engine();
 
 size_t plan_capacity(uint32_t burst, uint32_t hidden) {
   return sizeof(PlanHeader) + (size_t)kMaxPairs * sizeof(PairDesc) + (size_t)kMaxPairs * sizeof(GroupDesc) + 256 +
@@ -3142,9 +3159,17 @@ int env_int(const char* name, int dflt) {
 }
 
 // Pairs per down-phase group: about 48 KB of down weights per task.
+// The group size is also capped so that phase B's LDS (the group's h for
+// 8 tokens, the per-wave tables and the fp64 partial sums; the ldsB formula
+// of build_plan) stays within kLdsLimit for any burst.
 uint32_t group_pairs(uint8_t dn) {
   uint32_t per = dn == TQ4_KT ? 4608u : kCols * (uint32_t)row_bytes(dn, kNeurons);
   uint32_t cap = dn == TQ8_0 ? group_max<TQ8_0>() : dn == TQ4_KT ? group_max<TQ4_KT>() : group_max<TMXFP4>();
+  constexpr size_t kWstride = 2 * 8 * kTabStride + kMaxBurst * 8 * kTabStride;
+  constexpr size_t kFixed = kWaves * kWstride * sizeof(float) + kWaves * kCols * sizeof(double);
+  constexpr uint32_t kLdsGroups = (uint32_t)((kLdsLimit - kFixed) / (kMaxBurst * kNeurons * sizeof(float)));
+  static_assert(kLdsGroups >= 1, "one pair per group fits the LDS limit");
+  if (cap > kLdsGroups) cap = kLdsGroups;
   uint32_t g = E.group_bytes / per;
   return g < 1 ? 1 : g > cap ? cap : g;
 }
@@ -3650,6 +3675,8 @@ uint64_t fr_hip_unit_bytes(unsigned hidden, unsigned format) {
   return layout_of(hidden, format, l) ? l.block : 0;
 }
 
+static int open_engine(int device);
+
 int fr_hip_open(int device) {
   if (g_open) return E.device == device ? FR_HIP_OK : FR_HIP_STATE;
   int rc = fr_hip_probe(device, nullptr, 0);
@@ -3657,6 +3684,13 @@ int fr_hip_open(int device) {
   CK(hipSetDevice(device));
   E = Engine();
   E.device = device;
+  rc = open_engine(device);
+  if (rc) release_engine();   // nothing of a failed open stays allocated
+  return rc;
+}
+
+// fr_hip_open's allocations; on failure the caller releases what exists.
+static int open_engine(int device) {
   int cus = 0;
   CK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
   E.cus = cus > 0 ? (unsigned)cus : 1u;
@@ -3698,8 +3732,18 @@ int fr_hip_close(void) {
   if (!g_open) return FR_HIP_OK;
   for (int b = 0; b < kBlocks; ++b)
     if (E.block[b]) return FR_HIP_STATE;
+  release_engine();
+  return FR_HIP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+// Frees whatever the engine holds (null handles are skipped) and resets it:
+// fr_hip_close, and fr_hip_open when one of its steps fails.
+void release_engine() {
   (void)hipSetDevice(E.device);
-  (void)hipStreamSynchronize(E.stream);
+  if (E.stream) (void)hipStreamSynchronize(E.stream);
   (void)hipFree(E.done);
   (void)hipFree(E.fin);
   (void)hipFree(E.hbuf);
@@ -3719,15 +3763,17 @@ int fr_hip_close(void) {
   (void)hipHostFree(E.bstatus_host);
   (void)hipHostFree(E.plan_host);
   (void)hipHostFree(E.out_host);
-  (void)hipEventDestroy(E.ev0);
-  (void)hipEventDestroy(E.ev1);
+  if (E.ev0) (void)hipEventDestroy(E.ev0);
+  if (E.ev1) (void)hipEventDestroy(E.ev1);
   for (unsigned i = 0; i < 3 * E.timed_cap; ++i) (void)hipEventDestroy(E.tev[i]);
   free(E.tev);
-  (void)hipStreamDestroy(E.stream);
+  if (E.stream) (void)hipStreamDestroy(E.stream);
   E = Engine();
   g_open = false;
-  return FR_HIP_OK;
 }
+}  // namespace
+
+extern "C" {
 
 static int ensure_staging(size_t bytes) {
   if (E.staging_bytes >= bytes) return FR_HIP_OK;
@@ -3778,8 +3824,10 @@ int fr_hip_upload(unsigned block, const void* unit, uint64_t len, unsigned hidde
     uint32_t nl = layer + 2 <= (uint32_t)kLayers ? 2 : 1;
     int rc = upload_slices((int)block, src, layer * 513, nl * 513);
     if (rc) {
+      (void)hipStreamSynchronize(E.stream);
       (void)hipFree(dev);
       E.block[block] = nullptr;
+      E.layers[block] = 0;
       return rc;
     }
   }

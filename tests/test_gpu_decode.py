@@ -20,14 +20,18 @@ def eng():
     return fa.Engine(0)
 
 
-def special_row(rng, typ, n):
+def special_row(rng, typ, n, finite=True):
     """Random row with the edge scales the reference tests: subnormal and zero
-    fp16 scales, negative scales, E8M0 0 (2^-127) and 254."""
+    fp16 scales, negative scales, E8M0 0 (2^-127) and 254. With `finite`, the
+    E8M0 254 block's codes have magnitude <= 1.5 (weights below 2^128);
+    otherwise they are random, and some decode to infinity."""
     per, size = {oracle.Q4_K: (256, 144), oracle.Q8_0: (32, 34), oracle.MXFP4: (32, 17), oracle.Q4_0: (32, 18)}[typ]
     b = baseline_row(rng, typ, n).reshape(-1, size)
     nb = b.shape[0]
     if typ == oracle.MXFP4:
         b[0, 0], b[1 % nb, 0] = 0, 254
+        if finite:
+            b[1 % nb, 1:] &= 0xBB   # clear bit 2 of both nibbles: magnitude index <= 3
     else:
         b[0, 0:2] = [0x01, 0x00]          # smallest subnormal
         b[1 % nb, 0:2] = [0x00, 0x80]     # -0
@@ -41,12 +45,14 @@ def special_row(rng, typ, n):
 @pytest.mark.parametrize("typ", [oracle.Q4_K, oracle.Q8_0, oracle.MXFP4, oracle.Q4_0])
 @pytest.mark.parametrize("n", [2560, 4096])
 def test_dequant_rows_bit_exact(eng, typ, n):
+    """Every weight bit for bit, infinities included; FR_NUMERIC exactly when
+    a weight is not finite (the rows fr_native_dot rejects, src/native.c:7-37)."""
     rng = np.random.default_rng(typ * 100 + n)
-    for trial in range(3):
-        row = special_row(rng, typ, n) if trial else baseline_row(rng, typ, n)
+    for trial in range(4):
+        row = special_row(rng, typ, n, finite=trial < 3) if trial else baseline_row(rng, typ, n)
         rc, got = eng.dequant(typ, row, n)
-        assert rc == fa.OK
         want = oracle.dequant(row, typ, n)
+        assert rc == (fa.OK if np.all(np.isfinite(want)) else fa.NUMERIC), (typ, n, trial, rc)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (typ, n, trial)
 
 
@@ -60,6 +66,23 @@ def test_dequant_rejects_nonfinite_scale(eng, typ):
         row[1] = 0x7c
     rc, _ = eng.dequant(typ, row, 4096)
     assert rc == fa.NUMERIC
+
+
+@pytest.mark.parametrize("e,code,ok", [(254, 0x4, False), (254, 0xB, True), (253, 0x6, False), (253, 0xD, True)])
+def test_dequant_mxfp4_top_exponents(eng, e, code, ok):
+    """E8M0 254 with code 4 (2.0) and 253 with code 6 (4.0) decode to 2^128:
+    infinite, FR_NUMERIC; 254 with code 11 (-1.5) and 253 with code 13 (-3.0)
+    stay finite."""
+    rng = np.random.default_rng(6)
+    row = baseline_row(rng, oracle.MXFP4, 4096).reshape(-1, 17)
+    row[3, 0] = e
+    row[3, 1:] = 0x11 if ok else 0x00
+    row[3, 5] = code | (1 << 4)
+    rc, got = eng.dequant(oracle.MXFP4, row.reshape(-1), 4096)
+    want = oracle.dequant(row.reshape(-1), oracle.MXFP4, 4096)
+    assert rc == (fa.OK if ok else fa.NUMERIC)
+    assert np.all(np.isfinite(want)) == ok
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("fmt,hidden", [(oracle.FMT_NATIVE, 2560), (oracle.FMT_NATIVE, 4096),
