@@ -116,6 +116,10 @@ struct Scratch {
   uint32_t* ystat;
   float* yout;
   uint32_t* dstat;
+  // Set by fr_hip_run on the decode path, null otherwise: one status word
+  // per decode_reduce workgroup in mapped host memory (yout is then mapped
+  // host memory too, and dstat a device word of the engine).
+  uint32_t* hstat;
 };
 
 // ------------------------------------------------------------ scalars
@@ -1683,10 +1687,13 @@ __device__ __forceinline__ void store_partial(float* wgpart, unsigned stride, un
 // folds into it and zeroes again.
 __device__ __forceinline__ uint32_t* decode_status(const Scratch& S) {
   if (blockIdx.x == 0) {
-    if (!S.ystat) clear_other_parity(S);
-    else if (threadIdx.x == 0) *S.ystat = 0;
+    if (S.ystat) {
+      if (threadIdx.x == 0) *S.ystat = 0;
+    } else if (!S.hstat) {
+      clear_other_parity(S);
+    }
   }
-  return S.ystat ? S.dstat : S.out + (size_t)S.parity * S.out_words;
+  return S.ystat || S.hstat ? S.dstat : S.out + (size_t)S.parity * S.out_words;
 }
 
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* __restrict__ plan, Scratch S) {
@@ -1855,7 +1862,7 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
   const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
   const DecodeToken tk = reinterpret_cast<const DecodeToken*>(plan + H.groups_off)[blockIdx.y];
   uint32_t* status = S.ystat ? S.ystat : S.out + (size_t)S.parity * S.out_words;
-  float* yout = (S.ystat ? S.yout : reinterpret_cast<float*>(status + 4)) + (size_t)blockIdx.y * H.hidden;
+  float* yout = (S.ystat || S.hstat ? S.yout : reinterpret_cast<float*>(status + 4)) + (size_t)blockIdx.y * H.hidden;
   if (S.ystat && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
     const uint32_t e = *S.dstat;   // written by decode_kernel (kernel boundary)
     if (e) flag(status, e);
@@ -1888,14 +1895,33 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) red[wave][4 * q + cc] = v[cc];
   __syncthreads();
-  if (tid < kReducePositions) {
-    const double t = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
-    const unsigned col = decode_column(kReducePositions * blockIdx.x + tid);
-    if (col < H.hidden) {
-      float f = 0.f;
-      if (!isfinite(t) || fabs(t) > (double)FLT_MAX) flag(status, kErrRange);
-      else f = (float)t;
-      yout[col] = f;
+  if (tid < 64) {
+    bool over = false;
+    if (tid < kReducePositions) {
+      const double t = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
+      const unsigned col = decode_column(kReducePositions * blockIdx.x + tid);
+      if (col < H.hidden) {
+        float f = 0.f;
+        if (!isfinite(t) || fabs(t) > (double)FLT_MAX) over = true;
+        else f = (float)t;
+        yout[col] = f;
+      }
+    }
+    if (S.hstat) {
+      // This workgroup's status word, written whether or not it is zero (the
+      // host ORs them); workgroup (0, 0) adds decode_kernel's error bits and
+      // zeroes them for the next launch.
+      const bool any = __ballot(over) != 0;
+      if (tid == 0) {
+        uint32_t bits = any ? kErrRange : 0u;
+        if (blockIdx.x == 0 && blockIdx.y == 0) {
+          bits |= *S.dstat;   // written by decode_kernel (kernel boundary)
+          *S.dstat = 0;
+        }
+        S.hstat[(size_t)blockIdx.y * gridDim.x + blockIdx.x] = bits;
+      }
+    } else if (over) {
+      flag(status, kErrRange);
     }
   }
 }
@@ -3111,13 +3137,22 @@ struct Engine {
   float* wgpart = nullptr;        // [kMaxPairs][kMaxHidden]
   uint32_t* bar = nullptr;        // [2]
   float* static_scratch = nullptr;   // device address of `scratch` on this engine's device
+  // fr_hip_run's decode-path outputs in mapped pinned host memory (the host
+  // pointer and the device's view of it): y [8][4096] and one status word
+  // per decode_reduce workgroup [8][256]; and decode_kernel's error word.
+  float* hy_host = nullptr;
+  float* hy_dev = nullptr;
+  uint32_t* hstat_host = nullptr;
+  uint32_t* hstat_dev = nullptr;
+  uint32_t* hdstat = nullptr;
   // Read once at open (environment), not per run: the down-phase group
   // bytes of layer_kernel and the switch that routes requests past the
   // decode kernels (fr_hip_route changes it later).
   uint32_t group_bytes = 49152;
   bool no_decode = false;
   uint8_t* plan_dev = nullptr;
-  uint8_t* plan_host = nullptr;   // pinned
+  uint8_t* plan_host = nullptr;   // pinned, mapped
+  const uint4* plan_mapped = nullptr;   // the device's view of plan_host
   size_t plan_cap = 0;
   uint32_t* out_host = nullptr;   // pinned: status, pad x3, y
   uint8_t* staging = nullptr;     // device staging for uploads
@@ -3415,7 +3450,19 @@ bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, 
   return true;
 }
 
-int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream) {
+// Copies a plan from mapped pinned host memory into device memory, one
+// 16-byte word per lane with every load in flight at once: one PCIe round
+// trip, where a DMA copy first waits for its engine and then for the kernels'
+// queue (about 4 us more per run, measured).
+__global__ __launch_bounds__(64) void stage_plan(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                 unsigned words) {
+  const unsigned i = blockIdx.x * 64 + threadIdx.x;
+  if (i < words) dst[i] = src[i];
+}
+
+// `host`: a decode plan's y and status words go to the engine's mapped host
+// buffers (fr_hip_run), and the engine's output parity is left as it is.
+int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream, bool host = false) {
   if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
   const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS;
   if (decode && (grid > (unsigned)kDecodeGridMax || grid > H.npairs || H.ngroups != H.burst)) return FR_HIP_INVALID;
@@ -3434,6 +3481,13 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
   S.ystat = nullptr;
   S.yout = nullptr;
   S.dstat = nullptr;
+  S.hstat = nullptr;
+  host = host && decode;
+  if (host) {
+    S.hstat = E.hstat_dev;
+    S.yout = E.hy_dev;
+    S.dstat = E.hdstat;
+  }
   const dim3 g(grid), blk(kThreads);
   const bool one = H.burst == 1;
   hipEvent_t* te = E.timing && E.timed < E.timed_cap ? E.tev + 3 * E.timed++ : nullptr;
@@ -3459,8 +3513,10 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
     if (hipEventRecord(te[2], stream) != hipSuccess) return FR_HIP_IO;
   }
   if (hipGetLastError() != hipSuccess) return FR_HIP_IO;
-  E.last_parity = E.parity;
-  E.parity ^= 1u;
+  if (!host) {
+    E.last_parity = E.parity;
+    E.parity ^= 1u;
+  }
   return FR_HIP_OK;
 }
 
@@ -3709,14 +3765,28 @@ static int open_engine(int device) {
   // The static scratch array's address on this device (the name is a host
   // stand-in); it starts zeroed, as the error word must.
   CK(hipGetSymbolAddress(reinterpret_cast<void**>(&E.static_scratch), HIP_SYMBOL(scratch)));
+  CK(hipHostMalloc(reinterpret_cast<void**>(&E.hy_host), (size_t)kMaxBurst * kMaxHidden * sizeof(float),
+                   hipHostMallocMapped));
+  CK(hipHostGetDevicePointer(reinterpret_cast<void**>(&E.hy_dev), E.hy_host, 0));
+  CK(hipHostMalloc(reinterpret_cast<void**>(&E.hstat_host),
+                   (size_t)kMaxBurst * (kMaxHidden / kReducePositions) * sizeof(uint32_t), hipHostMallocMapped));
+  CK(hipHostGetDevicePointer(reinterpret_cast<void**>(&E.hstat_dev), E.hstat_host, 0));
+  CK(hipMalloc(&E.hdstat, sizeof(uint32_t)));
+  CK(hipMemset(E.hdstat, 0, sizeof(uint32_t)));
   E.group_bytes = (uint32_t)env_int("FRONK_HIP_GROUP_BYTES", 49152);
   E.no_decode = env_int("FRONK_HIP_NO_DECODE", 0) != 0;
   CK(hipMemset(E.done, 0, 2 * kMaxPairs * sizeof(uint32_t)));
   CK(hipMemset(E.fin, 0, 2 * kMaxRanges * sizeof(uint32_t)));
   CK(hipMemset(E.out, 0, 2 * (size_t)E.out_words * sizeof(uint32_t)));
   E.plan_cap = plan_capacity(kMaxBurst, kMaxHidden);
-  CK(hipMalloc(&E.plan_dev, E.plan_cap));
-  CK(hipHostMalloc(reinterpret_cast<void**>(&E.plan_host), E.plan_cap, hipHostMallocDefault));
+  // Rounded to whole 16-byte words for stage_plan.
+  CK(hipMalloc(&E.plan_dev, (E.plan_cap + 15) & ~size_t(15)));
+  CK(hipHostMalloc(reinterpret_cast<void**>(&E.plan_host), (E.plan_cap + 15) & ~size_t(15), hipHostMallocMapped));
+  {
+    void* mapped = nullptr;
+    CK(hipHostGetDevicePointer(&mapped, E.plan_host, 0));
+    E.plan_mapped = static_cast<const uint4*>(mapped);
+  }
   CK(hipHostMalloc(reinterpret_cast<void**>(&E.out_host), (size_t)E.out_words * sizeof(uint32_t), hipHostMallocDefault));
   CK(hipMalloc(&E.bstatus, sizeof(uint32_t)));
   CK(hipMemset(E.bstatus, 0, sizeof(uint32_t)));
@@ -3763,6 +3833,9 @@ void release_engine() {
   (void)hipHostFree(E.bstatus_host);
   (void)hipHostFree(E.plan_host);
   (void)hipHostFree(E.out_host);
+  (void)hipHostFree(E.hy_host);
+  (void)hipHostFree(E.hstat_host);
+  (void)hipFree(E.hdstat);
   if (E.ev0) (void)hipEventDestroy(E.ev0);
   if (E.ev1) (void)hipEventDestroy(E.ev1);
   for (unsigned i = 0; i < 3 * E.timed_cap; ++i) (void)hipEventDestroy(E.tev[i]);
@@ -3939,7 +4012,7 @@ int fr_hip_launch_static(const void* host_plan, const void* device_plan, float* 
   if (H.kind == KIND_DECODE_ROWS && (H.pad & ~kComboShared) > COMBO_Q4_0) return FR_HIP_INVALID;
   if (!E.static_scratch) return FR_HIP_STATE;
   CK(hipSetDevice(E.device));
-  Scratch S = {};
+  Scratch S = {};   // no engine buffers, no host outputs
   S.wgpart = E.static_scratch + kStaticHead;
   S.ustride = kStaticUnits;
   S.ystat = reinterpret_cast<uint32_t*>(device_status);
@@ -3967,22 +4040,34 @@ int fr_hip_run(const fr_hip_request* req, float* y) {
   int rc = build_plan(req, E.plan_host, E.plan_cap, &used, &grid);
   if (rc) return rc;
   const PlanHeader& H = *reinterpret_cast<const PlanHeader*>(E.plan_host);
-  CK(hipMemcpyAsync(E.plan_dev, E.plan_host, used, hipMemcpyHostToDevice, E.stream));
-  CK(hipEventRecord(E.ev0, E.stream));
-  rc = launch(E.plan_dev, H, grid, E.stream);
+  // The plan (with x) is staged into device memory by a copy kernel, then
+  // the launch, then one wait. On the decode path decode_reduce writes y and
+  // its status words to mapped host memory, so no copy out is needed; the
+  // layer kernel's outputs are copied back. No events on this path
+  // (fr_hip_timing times launches on request).
+  {
+    const unsigned words = (unsigned)((used + 15) / 16);
+    hipLaunchKernelGGL(stage_plan, dim3((words + 63) / 64), dim3(64), 0, E.stream, E.plan_mapped,
+                       reinterpret_cast<uint4*>(E.plan_dev), words);
+  }
+  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS;
+  rc = launch(E.plan_dev, H, grid, E.stream, decode);
   if (rc) return rc;
-  CK(hipEventRecord(E.ev1, E.stream));
   const size_t count = (size_t)H.burst * H.hidden;
   unsigned status = 0;
-  rc = fetch_output(E.stream, count, nullptr, &status);
-  if (rc) return rc;
-  float ms = 0.f;
-  if (hipEventElapsedTime(&ms, E.ev0, E.ev1) == hipSuccess) E.sample.last_kernel_ns = ms * 1e6;
+  if (decode) {
+    CK(hipStreamSynchronize(E.stream));
+    const size_t words = (size_t)H.burst * (kMaxHidden / kReducePositions);
+    for (size_t i = 0; i < words; ++i) status |= __atomic_load_n(E.hstat_host + i, __ATOMIC_RELAXED);
+  } else {
+    rc = fetch_output(E.stream, count, nullptr, &status);
+    if (rc) return rc;
+  }
   ++E.sample.runs;
   if (status & kErrTimeout) return FR_HIP_IO;
   if (status) return FR_HIP_NUMERIC;
   // y is written only on success: untouched on failure.
-  memcpy(y, E.out_host + 4, count * sizeof(float));
+  memcpy(y, decode ? E.hy_host : reinterpret_cast<const float*>(E.out_host + 4), count * sizeof(float));
   return FR_HIP_OK;
 }
 
