@@ -94,15 +94,15 @@ def make_requests(n, burst, routing, seed):
     return reqs
 
 
-def algorithmic_bytes(fa, fmt, experts, gates):
-    """Weight bytes read once per unique (expert, owned slice), plus x and y
-    (4*T*H bytes each)."""
+def algorithmic_bytes(fa, fmt, experts, gates, blocks=SLICES):
+    """Weight bytes read once per unique (expert, owned slice) over `blocks`
+    owned slices, plus x and y (4*T*H bytes each)."""
     T = experts.shape[0]
     lay_slice, lay_shared = slice_sizes(fa, fmt)
     unique = len(set(int(e) for e in experts.ravel()))
-    weights = unique * SLICES * lay_slice
+    weights = unique * blocks * lay_slice
     if np.any(gates[:, 10] != 0):
-        weights += SLICES * lay_shared
+        weights += blocks * lay_shared
     return weights, weights + 8 * T * HIDDEN
 
 
@@ -348,14 +348,12 @@ def prefill_cpu_baseline(fa, y0, req, budget_s):
     }
 
 
-def bench_prefill(args):
+def prefill_leg(fa, lib, eng, steps, warmup):
+    """Config 5 on the device: 48 layers x 20 blocks of synthetic Q4_K resident,
+    one 512-token chunk per step through fr_hip_batch_launch, timed with
+    events on the launch stream. Returns the measures and the first layer's
+    request (for the CPU leg); the blocks stay resident for the caller."""
     import torch
-    import fronk_amd as fa
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    steps = args.steps if args.steps is not None else 3
-    warmup = args.warmup if args.warmup is not None else 1
-    lib = fa.lib()
-    eng = fa.Engine(0)
     t0 = time.perf_counter()
     for b in range(SLICES):
         fa.check(eng.synthetic(b, HIDDEN, fa.FMT_Q4KT, PREFILL_LAYERS, SEED), "fr_hip_synthetic")
@@ -414,28 +412,42 @@ def bench_prefill(args):
     achieved = alg / (chunk_ms * 1e-3) / 1e9
     flops = PREFILL_LAYERS * 2.0 * PREFILL_TOKENS * 10 * SLICES * 3 * 32 * HIDDEN   # useful multiply-adds x 2
     tflops = flops / (chunk_ms * 1e-3) / 1e12
-
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "prefill_traffic.json")
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+    return {
+        "wall_s": wall, "steps": steps, "warmup": warmup, "weights": float(wts.sum()),
+        "chunk_ms": chunk_ms, "achieved": achieved, "tflops": tflops, "traffic": traffic,
+        "main_us": main_ms.value * 1e3 / counted.value, "launch_us": total_ms.value * 1e3 / counted.value,
+    }, reqs[0]
 
+
+def bench_prefill(args):
+    import fronk_amd as fa
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    steps = args.steps if args.steps is not None else 3
+    warmup = args.warmup if args.warmup is not None else 1
+    lib = fa.lib()
+    eng = fa.Engine(0)
+    m, req0 = prefill_leg(fa, lib, eng, steps, warmup)
     cpu = None
     if not args.no_cpu:
-        layer, experts, gates, x = reqs[0]
+        layer, experts, gates, x = req0
         rc, y0 = eng.run_batch(layer, experts, gates, x)
         fa.check(rc, "fr_hip_run_batch")
-        cpu = prefill_cpu_baseline(fa, y0, reqs[0], args.cpu_seconds)
+        cpu = prefill_cpu_baseline(fa, y0, req0, args.cpu_seconds)
     for b in range(SLICES):
         eng.release(b)
+    chunk_ms = m["chunk_ms"]
     out = {
         "metric": METRIC,
-        "value": round(wts.sum() * steps / wall / 1e9, 2),
+        "value": round(m["weights"] * steps / m["wall_s"] / 1e9, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": round(wall * 1e3 / steps, 4),
+        "ms_per_step": round(m["wall_s"] * 1e3 / steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -444,89 +456,328 @@ def bench_prefill(args):
         "config": {"workload": PREFILL_TEXT, "hidden": HIDDEN, "experts": 512, "active_experts": 10,
                    "slices": SLICES, "tokens": PREFILL_TOKENS, "layers": PREFILL_LAYERS, "format": "Q4KT",
                    "mode": "f32"},
-        "hbm_frac": round(wts.sum() * steps / wall / 1e9 / HBM_PEAK_GBS, 4),
+        "hbm_frac": round(m["weights"] * steps / m["wall_s"] / 1e9 / HBM_PEAK_GBS, 4),
         "tokens_per_s_per_layer": round(PREFILL_TOKENS / (chunk_ms * 1e-3 / PREFILL_LAYERS), 1),
         "chunk_ms": round(chunk_ms, 4),
         "layer_us": round(chunk_ms * 1e3 / PREFILL_LAYERS, 2),
-        "kernel_split_us": {"gate_up+down": round(main_ms.value * 1e3 / counted.value, 2),
-                            "launch": round(total_ms.value * 1e3 / counted.value, 2),
+        "kernel_split_us": {"gate_up+down": round(m["main_us"], 2), "launch": round(m["launch_us"], 2),
                             "note": "per layer launch, events on the launch stream, one extra chunk"},
-        "weight_bytes_per_chunk": float(wts.sum()),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+        "weight_bytes_per_chunk": m["weights"],
+        "roofline": {"bound": "hbm", "achieved": round(m["achieved"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(m["achieved"] / HBM_PEAK_GBS, 4), "traffic": m["traffic"],
                      "traffic_note": "HBM bytes per layer launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
                      "kernel": "prefill_digits + prefill_gate_up + prefill_down + prefill_reduce per layer"},
-        "mfma": {"achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s (fp32 matrix)",
-                 "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4)},
+        "mfma": {"achieved": round(m["tflops"], 2), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s (fp32 matrix)",
+                 "frac": round(m["tflops"] / MFMA_F32_PEAK_TFLOPS, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
 
 
-def avx2_reference_baseline(budget_s, workers=16):
-    """The reference's own AVX2 backend (backends/avx2.c, the fr_avx2 vtable),
-    compiled from its sources into oracle/_ref, run multi-threaded on the host
-    cores. The reference fixes H = 2560 (src/model.h:16), so the sample is the
-    same layer-share shape at that width in its native format (Q4_K gate/up,
-    MXFP4 down): 10 of 512 experts uniform, 20 owned slices, one token per
-    call; GB/s = routed slice bytes per call / time. None when oracle/_ref is
-    absent."""
+def percentiles(ns):
+    """p50 and p99 as the reference's bench takes them (src/bench.c:432-436):
+    sorted[(n+1)/2-1] and sorted[(99n+99)/100-1]."""
+    v = sorted(ns)
+    n = len(v)
+    return v[(n + 1) // 2 - 1], v[(99 * n + 99) // 100 - 1]
+
+
+def time_run_calls(call, count, warmup=512, samples=1024):
+    """The reference's run() timing protocol (src/bench.c:352-377): `warmup`
+    untimed calls, then a monotonic timer around each of `samples` calls.
+    `call(i)` makes the i-th call and raises on failure. Returns the per-call
+    times in microseconds."""
+    for i in range(warmup):
+        call(i % count)
+    out = np.zeros(samples)
+    clock = time.perf_counter_ns
+    for k in range(samples):
+        i = (warmup + k) % count
+        t0 = clock()
+        call(i)
+        out[k] = (clock() - t0) * 1e-3
+    return out
+
+
+def run_leg(fa, lib, reqs, weight_bytes, warmup=512, samples=1024):
+    """fr_hip_run timed the reference's way over prepared requests (layers
+    rotating as the requests do); ctypes call overhead is inside the timer."""
+    prepared = [fa.make_request(*r, fa.MODE_F32) for r in reqs]
+    y = np.zeros((8, HIDDEN), np.float32)
+    yp = fa.fptr(y)
+    run = lib.fr_hip_run
+
+    def call(i):
+        rc = run(C.byref(prepared[i][0]), yp)
+        if rc != fa.OK:
+            raise RuntimeError(f"fr_hip_run failed with {rc}")
+
+    us = time_run_calls(call, len(prepared), warmup, samples)
+    p50, p99 = percentiles(us)
+    burst = reqs[0][1].shape[0]
+    return {"p50_us": round(p50, 2), "p99_us": round(p99, 2), "mean_us": round(float(us.mean()), 2),
+            "warmup": warmup, "samples": samples,
+            "run_tokens_per_s": round(burst * samples / (us.sum() * 1e-6), 1),
+            "gbs_at_p50": round(weight_bytes / (p50 * 1e-6) / 1e9, 2),
+            "timer": "perf_counter_ns around each fr_hip_run call (ctypes call included), "
+                     "512 warm-ups first (src/bench.c:352-377)"}
+
+
+class Launches:
+    """A workload's launch plans resident in HBM and enqueued with fr_hip_launch
+    on one stream."""
+
+    def __init__(self, fa, lib, eng, fmt, reqs, blocks=SLICES):
+        import torch
+        self.fa, self.lib = fa, lib
+        n = len(reqs)
+        burst = reqs[0][1].shape[0]
+        cap = lib.fr_hip_plan_bytes(burst, HIDDEN)
+        self.stride = (cap + 255) // 256 * 256
+        self.host = np.zeros((n, self.stride), np.uint8)
+        self.alg = np.zeros(n)
+        self.wts = np.zeros(n)
+        self.grid = 0
+        for i, (layer, experts, gates, x) in enumerate(reqs):
+            plan, self.grid = eng.plan(layer, experts, gates, x, fa.MODE_F32)
+            self.host[i, :plan.size] = plan
+            self.wts[i], self.alg[i] = algorithmic_bytes(fa, fmt, experts, gates, blocks)
+        self.dev = torch.from_numpy(self.host).to("cuda")
+        self.stream = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        self.hptr, self.dptr = self.host.ctypes.data, self.dev.data_ptr()
+        self.sptr = C.c_void_p(self.stream.cuda_stream)
+        self.kernels = grid_kernels(lib, self.host[0])
+
+    def enqueue(self, i):
+        rc = self.lib.fr_hip_launch(C.c_void_p(self.hptr + i * self.stride), C.c_void_p(self.dptr + i * self.stride),
+                                    self.sptr)
+        if rc != self.fa.OK:
+            raise RuntimeError(f"fr_hip_launch failed with {rc}")
+
+    def timed(self, first, last):
+        """Events around launches first..last-1 on the launch stream; returns
+        (wall seconds, ms per launch). Checks the last launch's status."""
+        import torch
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        with torch.cuda.stream(self.stream):
+            ev0.record(self.stream)
+            for i in range(first, last):
+                self.enqueue(i)
+            ev1.record(self.stream)
+        self.stream.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        status = C.c_uint(0)
+        self.fa.check(self.lib.fr_hip_last_output(self.sptr, None, 0, C.byref(status)), "fr_hip_last_output")
+        if status.value:
+            raise RuntimeError(f"decode kernels reported status {status.value}")
+        return wall, ev0.elapsed_time(ev1) / (last - first)
+
+    def split(self, first, count):
+        """Main kernel and whole launch in microseconds from events between
+        the kernels of `count` more launches (the markers add a little)."""
+        fa, lib = self.fa, self.lib
+        fa.check(lib.fr_hip_timing(count), "fr_hip_timing")
+        for i in range(first, first + count):
+            self.enqueue(i)
+        main_ms, total_ms, counted = C.c_double(), C.c_double(), C.c_uint()
+        fa.check(lib.fr_hip_timing_read(C.byref(main_ms), C.byref(total_ms), C.byref(counted)),
+                 "fr_hip_timing_read")
+        return main_ms.value * 1e3 / counted.value, total_ms.value * 1e3 / counted.value
+
+
+def decode_leg(fa, lib, eng, key, steps, warmup, seed, blocks=SLICES):
+    """One decode workload with its `blocks` owned slices already resident:
+    `warmup` then `steps` pipelined launches. Returns the extra-key record."""
+    wl = WORKLOADS[key]
+    fmt = getattr(fa, wl["fmt"])
+    reqs = make_requests(warmup + steps, wl["burst"], wl["routing"], seed)
+    L = Launches(fa, lib, eng, fmt, reqs, blocks)
+    for i in range(warmup):
+        L.enqueue(i)
+    wall, ms = L.timed(warmup, warmup + steps)
+    alg = float(L.alg[warmup:].mean())
+    wts = float(L.wts[warmup:].mean())
+    achieved = alg / (ms * 1e-3) / 1e9
+    return {"workload": wl["text"], "kernel": L.kernels, "launches": steps, "kernel_us": round(ms * 1e3, 3),
+            "weight_bytes_per_call": wts, "algorithmic_bytes_per_call": alg,
+            "gbs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(wl["burst"] * steps / wall, 1)}
+
+
+def host_info():
+    """The GPU box's host as the CPU baseline sees it: nproc, the affinity set,
+    lscpu's model / cores / threads, and the thread share this pool allows."""
+    info = {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "Thread(s) per core", "Core(s) per socket", "Socket(s)", "CPU(s)",
+                             "L3 cache"):
+                info["lscpu_" + k.strip().lower().replace("(s)", "s").replace(" ", "_")] = v.strip()
+    except (OSError, ValueError):
+        pass
+    # One GPU's share of the box's CPUs: worker pools stay within 16 threads.
+    info["share"] = min(info["affinity"], 16)
+    return info
+
+
+NATIVE_H = 2560
+NATIVE_LAYERS = 8
+NATIVE_EXPERTS = 80   # experts 0..79 carry data (fr_native_fixture), as in the reference's fixture
+
+
+def native_routes(passes):
+    """The reference bench's routing (src/bench.c:279-284) over the filled
+    experts: layer = pass % L, experts base..base+9 with base = (pass / L) * 41,
+    here modulo the 80 filled experts and 8 filled layers."""
+    out = []
+    for p in range(passes):
+        base = (p // NATIVE_LAYERS) * 41 % NATIVE_EXPERTS
+        out.append((p % NATIVE_LAYERS, np.array([(base + e) % NATIVE_EXPERTS for e in range(10)], np.uint16)))
+    return out
+
+
+def native_inputs():
+    """The reference bench's request values (src/bench.c:347-351): routed gates
+    0.0625, shared 0.5, x[d] = ((37 d) % 257 - 128) / 128."""
+    g = np.full(11, 0.0625, np.float32)
+    g[10] = 0.5
+    x = np.array([((d * 37) % 257 - 128) / 128 for d in range(NATIVE_H)], np.float32)
+    return g, x
+
+
+def cpu_reference_leg(fa, lib, eng, passes=1024):
+    """CPU baseline: the reference's own AVX2 backend (backends/avx2.c, the
+    fr_avx2 vtable) compiled from its sources into oracle/_ref, swept over the
+    reference's worker choices {1, cores/2, cores-1, cores, logical}
+    (backends/avx2.c:747) within this box's thread share and prefetch {0, 2},
+    each point timed the reference's way (512 warm-ups, 256 samples, p50/p99).
+    The shape is the reference's own: H = 2560 (src/model.h:16), native units
+    (Q4_K gate/up, MXFP4 down, Q8_0 shared), 10 routed + the shared expert,
+    20 owned blocks, layers rotating over 8 filled layers. The same bytes and
+    requests then run through fr_hip_run on the GPU with the same protocol.
+    Bytes per call follow the reference's byte model (src/bench.c:158-162)."""
     import oracle
-    from fixtures import slice_view, sparse_unit
     import vtable
     if not os.path.exists(oracle.REF_PATH):
         return None
     ref = C.CDLL(oracle.REF_PATH, mode=C.RTLD_GLOBAL)
-    vt = vtable.Backend.in_dll(ref, "fr_avx2")
-    ref.fr_avx2_set_tuning(C.c_uint(SLICES), C.c_uint(1), C.c_uint(workers), C.c_uint(0))
-    if ref.fr_avx2_configure(C.c_uint(SLICES), C.c_uint(1)) != 0:
-        return None
-    H = vtable.HIDDEN
-    lay = oracle.layout(H, oracle.FMT_NATIVE)
-    rng = np.random.default_rng(SEED + 9)
-    calls = 48
-    routes = [rng.choice(512, 10, replace=False).astype(np.uint16) for _ in range(calls)]
-    used = sorted(set(int(e) for r in routes for e in r))
+    ref.fr_native_fixture.argtypes = [C.c_void_p, C.c_uint, C.c_uint32]
+    avx2 = vtable.Backend.in_dll(ref, "fr_avx2")
+    lay = oracle.layout(NATIVE_H, oracle.FMT_NATIVE)
+    t0 = time.perf_counter()
     units = []
     for b in range(SLICES):
-        u = sparse_unit(lay)
-        for e in used:
-            slice_view(u, lay, 0, e)[:] = oracle.synth_slice(lay, SEED, b, 0, e)
+        u = np.zeros(lay.block, np.uint8)
+        for layer in range(NATIVE_LAYERS):
+            ref.fr_native_fixture(u.ctypes.data, layer, 7 + 1009 * b + 31 * layer)
         units.append(u)
-    for b in range(SLICES):
-        if vt.load(b, units[b].ctypes.data, lay.block) != 0:
-            raise RuntimeError("fr_avx2 load failed")
+    log(f"cpu leg: {SLICES} native units x {NATIVE_LAYERS} layers filled in {time.perf_counter() - t0:.1f} s")
+    g, x = native_inputs()
+    routes = native_routes(passes)
     reqs = []
-    for r in routes:
+    for layer, experts in routes:
         q = vtable.Req()
-        q.layer, q.burst = 0, 1
+        q.layer, q.burst = layer, 1
         for j in range(10):
-            q.expert[0][j] = int(r[j])
-        g = softmax_gates(rng, 1)[0]
+            q.expert[0][j] = int(experts[j])
         for j in range(11):
             q.gate[0][j] = float(g[j])
-        xs = rng.standard_normal(H).astype(np.float32)
-        C.memmove(q.x[0], xs.ctypes.data, 4 * H)
+        C.memmove(q.x[0], x.ctypes.data, 4 * NATIVE_H)
         reqs.append(q)
+    call_bytes = SLICES * (10 * lay.slice + lay.shared_slice)
     part = vtable.Part()
-    for q in reqs[:4]:
-        if vt.run(C.byref(q), C.byref(part)) != 0:
+
+    def call(i):
+        if avx2.run(C.byref(reqs[i]), C.byref(part)) != 0:
             raise RuntimeError("fr_avx2 run failed")
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        if vt.run(C.byref(reqs[n % calls]), C.byref(part)) != 0:
-            raise RuntimeError("fr_avx2 run failed")
-        n += 1
-    seconds = time.perf_counter() - t0
-    for b in range(SLICES):
-        vt.unload(b)
+
+    info = host_info()
+    tpc = 1
+    try:
+        tpc = max(1, int(info.get("lscpu_threads_per_core", "1")))
+    except ValueError:
+        pass
+    logical = info["share"]
+    cores = max(1, logical // tpc)
+    choices = []
+    for w in (1, max(1, cores // 2), max(1, cores - 1), cores, logical):
+        if w not in choices:
+            choices.append(w)
+    sweep, best = [], None
+    for workers in choices:
+        for prefetch in (0, 2):
+            ref.fr_avx2_set_tuning(C.c_uint(SLICES), C.c_uint(1), C.c_uint(workers), C.c_uint(prefetch))
+            if ref.fr_avx2_configure(C.c_uint(SLICES), C.c_uint(1)) != 0:
+                raise RuntimeError("fr_avx2_configure failed")
+            for b in range(SLICES):
+                if avx2.load(b, units[b].ctypes.data, lay.block) != 0:
+                    raise RuntimeError("fr_avx2 load failed")
+            us = time_run_calls(call, len(reqs), 512, 256)
+            for b in range(SLICES):
+                avx2.unload(b)
+            p50, p99 = percentiles(us)
+            row = {"workers": workers, "prefetch": prefetch, "p50_us": round(p50, 2), "p99_us": round(p99, 2),
+                   "gbs_at_p50": round(call_bytes / (p50 * 1e-6) / 1e9, 2)}
+            log(f"avx2 workers={workers:3d} prefetch={prefetch} p50 {p50:9.2f} us p99 {p99:9.2f} us "
+                f"{row['gbs_at_p50']:8.2f} GB/s")
+            sweep.append(row)
+            if best is None or p50 < best["p50_us"]:
+                best = row
     ref.fr_avx2_close()
-    return {"value": n * 10 * SLICES * lay.slice / seconds / 1e9, "unit": "GB/s", "cores": workers,
-            "kind": "reference",
-            "sample": f"{n} calls of a 10-of-512, 20-slice native layer share at H={H} (the reference's fixed "
-                      f"width; Q4_K gate/up, MXFP4 down) through backends/avx2.c built from the reference sources, "
-                      f"{workers} worker threads, {seconds:.1f} s",
-            "us_per_call": seconds / n * 1e6}
+
+    # The same units and requests on the GPU through fr_hip_run.
+    t0 = time.perf_counter()
+    for b in range(SLICES):
+        fa.check(eng.reserve(b, NATIVE_H, fa.FMT_NATIVE), "fr_hip_reserve")
+        for layer in range(NATIVE_LAYERS):
+            for e in list(range(NATIVE_EXPERTS)) + [512]:
+                fa.check(eng.refresh(b, units[b], layer, e), "fr_hip_refresh")
+    log(f"gpu same shape: slices copied in {time.perf_counter() - t0:.1f} s")
+    gpu_reqs = [(layer, experts.reshape(1, 10), g.reshape(1, 11), x.reshape(1, NATIVE_H)) for layer, experts in routes]
+    prepared = [fa.make_request(*r, fa.MODE_F32) for r in gpu_reqs]
+    y = np.zeros((8, NATIVE_H), np.float32)
+    yp = fa.fptr(y)
+
+    def gcall(i):
+        rc = lib.fr_hip_run(C.byref(prepared[i][0]), yp)
+        if rc != fa.OK:
+            raise RuntimeError(f"fr_hip_run failed with {rc}")
+
+    us = time_run_calls(gcall, len(prepared), 512, 1024)
+    for b in range(SLICES):
+        eng.release(b)
+    gp50, gp99 = percentiles(us)
+    return {
+        "value": best["gbs_at_p50"], "unit": "GB/s", "cores": best["workers"], "kind": "reference",
+        "sample": f"backends/avx2.c built from the reference sources (oracle/_ref): {NATIVE_H}-wide native layer "
+                  f"share (Q4_K gate/up, MXFP4 down, Q8_0 shared), 10 routed + shared x {SLICES} blocks, "
+                  f"{NATIVE_LAYERS} layers rotating; per point 512 warm-ups + 256 timed run() calls, "
+                  f"{call_bytes} B per call (src/bench.c:158-162); best of the worker/prefetch sweep",
+        "p50_us": best["p50_us"], "p99_us": best["p99_us"], "prefetch": best["prefetch"],
+        "host": info, "sweep": sweep,
+        "gpu_same_shape": {"p50_us": round(gp50, 2), "p99_us": round(gp99, 2),
+                           "gbs_at_p50": round(call_bytes / (gp50 * 1e-6) / 1e9, 2),
+                           "vs_cpu_p50": round(best["p50_us"] / gp50, 2),
+                           "note": "fr_hip_run on the same units and requests, 512 warm-ups + 1024 samples"},
+    }
+
+
+def achievable_leg(eng, lib, plans):
+    """Achievable HBM read rate for the headline calls: the streaming probe
+    over the same scattered slices and over a contiguous buffer of the same
+    size (best of a short sweep of pieces, threads and depth)."""
+    sweep = [("scattered", p, t, d) for p in (1, 2) for t in (512, 1024) for d in (2, 4)]
+    sweep += [("contiguous", g, t, d) for g in (512, 1024) for t in (512, 1024) for d in (2, 4)]
+    rows, best, total = stream_ceiling(eng, lib, plans, sweep)
+    return {k: {"gbs": v["gbs"], "us": v["us"], "workgroups": v["workgroups"], "threads": v["threads"],
+                "depth": v["depth"]} for k, v in best.items()}, total
 
 
 def main():
@@ -534,10 +785,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="q4k", choices=sorted(WORKLOADS) + ["prefill", "stream"])
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--workload", default="q4k", choices=sorted(WORKLOADS) + ["prefill", "stream", "run"])
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--run-calls", type=int, default=200)
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configs' legs")
     ap.add_argument("--copy-kernel", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -558,10 +809,12 @@ def main():
     if args.warmup is None:
         args.warmup = 200
 
-    import torch
+    import torch  # noqa: F401  (before the library: one HIP runtime)
     import fronk_amd as fa
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
 
-    wl = WORKLOADS[args.workload]
+    key = "q4k" if args.workload == "run" else args.workload
+    wl = WORKLOADS[key]
     fmt = getattr(fa, wl["fmt"])
     burst = wl["burst"]
     lib = fa.lib()
@@ -571,98 +824,88 @@ def main():
         fa.check(eng.synthetic(b, HIDDEN, fmt, LAYERS, SEED), "fr_hip_synthetic")
     log(f"resident: {SLICES} blocks x {LAYERS} layers generated in {time.perf_counter() - t0:.1f} s")
 
+    if args.workload == "run":
+        # run() alone, the reference's way: for kernel traces of run() calls.
+        reqs = make_requests(1024, burst, wl["routing"], SEED + 1)
+        wts = float(np.mean([algorithmic_bytes(fa, fmt, r[1], r[2])[0] for r in reqs]))
+        rec = run_leg(fa, lib, reqs, wts)
+        for b in range(SLICES):
+            eng.release(b)
+        print(json.dumps({"workload": wl["text"], "run": rec}), flush=True)
+        return
+
     n = args.warmup + args.steps
     reqs = make_requests(n, burst, wl["routing"], SEED + 1)
-    cap = lib.fr_hip_plan_bytes(burst, HIDDEN)
-    stride = (cap + 255) // 256 * 256
-    host = np.zeros((n, stride), np.uint8)
-    alg = np.zeros(n)
-    wts = np.zeros(n)
-    grid = 0
-    for i, (layer, experts, gates, x) in enumerate(reqs):
-        plan, grid = eng.plan(layer, experts, gates, x, fa.MODE_F32)
-        host[i, :plan.size] = plan
-        wts[i], alg[i] = algorithmic_bytes(fa, fmt, experts, gates)
-    dev = torch.from_numpy(host).to("cuda")
-    stream = torch.cuda.Stream()
-    torch.cuda.synchronize()
-    hptr = host.ctypes.data
-    dptr = dev.data_ptr()
-    sptr = C.c_void_p(stream.cuda_stream)
-    launch = lib.fr_hip_launch
-
-    def enqueue(i):
-        rc = launch(C.c_void_p(hptr + i * stride), C.c_void_p(dptr + i * stride), sptr)
-        if rc != fa.OK:
-            raise RuntimeError(f"fr_hip_launch failed with {rc}")
-
+    L = Launches(fa, lib, eng, fmt, reqs)
     for i in range(args.warmup):
-        enqueue(i)
-    stream.synchronize()
-    torch.cuda.synchronize()
-
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    with torch.cuda.stream(stream):
-        ev0.record(stream)
-        for i in range(args.warmup, n):
-            enqueue(i)
-        ev1.record(stream)
-    stream.synchronize()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kernel_ms = ev0.elapsed_time(ev1) / args.steps
-
-    status = C.c_uint(0)
-    fa.check(lib.fr_hip_last_output(sptr, None, 0, C.byref(status)), "fr_hip_last_output")
-    if status.value:
-        raise RuntimeError(f"layer kernel reported status {status.value}")
-
+        L.enqueue(i)
+    L.stream.synchronize()
+    wall, kernel_ms = L.timed(args.warmup, n)
     timed = slice(args.warmup, n)
     ms_per_step = wall * 1e3 / args.steps
-    weight_gbs = wts[timed].sum() / wall / 1e9
-    alg_per_launch = float(alg[timed].mean())
+    weight_gbs = L.wts[timed].sum() / wall / 1e9
+    alg_per_launch = float(L.alg[timed].mean())
 
     # Roofline: algorithmic bytes over the launch's own time, from the HIP
     # events around the timed region on the launch stream. A single-token
     # Q4_K launch is decode_kernel followed by decode_reduce (its fixed-order
     # partial sum); their rocprofv3 averages add up to this figure. The split
-    # between them comes from a second pass with events between the kernels
-    # (the extra markers add a little to each).
+    # between them comes from a second pass with events between the kernels.
     achieved = alg_per_launch / (kernel_ms * 1e-3) / 1e9
-    nt = min(args.steps, 500)
-    fa.check(lib.fr_hip_timing(nt), "fr_hip_timing")
-    for i in range(args.warmup, args.warmup + nt):
-        enqueue(i)
-    main_ms, total_ms, counted = C.c_double(), C.c_double(), C.c_uint()
-    fa.check(lib.fr_hip_timing_read(C.byref(main_ms), C.byref(total_ms), C.byref(counted)), "fr_hip_timing_read")
-    main_us = main_ms.value * 1e3 / counted.value
-    launch_us = total_ms.value * 1e3 / counted.value
+    main_us, launch_us = L.split(args.warmup, min(args.steps, 500))
+    log(f"headline: {kernel_ms * 1e3:.3f} us per launch, {achieved:.1f} GB/s")
 
-    # run() wall time: plan build, H2D, launch, D2H and narrowing per call.
-    run_us = []
-    for layer, experts, gates, x in reqs[:args.run_calls]:
-        t1 = time.perf_counter()
-        rc, _ = eng.run(layer, experts, gates, x, fa.MODE_F32)
-        run_us.append((time.perf_counter() - t1) * 1e6)
-        if rc != fa.OK:
-            raise RuntimeError(f"fr_hip_run failed with {rc}")
-    run_us = np.array(run_us)
+    ceiling, ceiling_bytes = achievable_leg(eng, lib, [L.host[i, :] for i in range(args.warmup, args.warmup + 8)])
+    run_rec = run_leg(fa, lib, reqs[:1024], float(L.wts[:1024].mean()))
+    log(f"run(): p50 {run_rec['p50_us']} us p99 {run_rec['p99_us']} us")
 
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"decode_{args.workload}_traffic.json")
+    tfile = os.path.join(ROOT, "profiles", f"decode_{key}_traffic.json")
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
 
-    cpu = avx2 = None
+    scalar = None
     if not args.no_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "tests"))
-        cpu = cpu_baseline(fa, eng, fmt, reqs[args.warmup:], args.cpu_seconds)
-        avx2 = avx2_reference_baseline(min(args.cpu_seconds, 6.0))
+        scalar = cpu_baseline(fa, eng, fmt, reqs[args.warmup:], args.cpu_seconds)
 
-    for b in range(SLICES):
-        eng.release(b)
+    extra = {}
+    if not args.no_extra and key == "q4k":
+        extra["config4_mtp4"] = decode_leg(fa, lib, eng, "mtp4", 300, 50, SEED + 4)
+        for b in range(1, SLICES):
+            eng.release(b)
+        one = decode_leg(fa, lib, eng, "q4k", 300, 50, SEED + 6, blocks=1)
+        one["workload"] = ("config 1, latency: one owned Q4_K slice (block 0 only) x the 10 routed experts every "
+                           "request carries, hidden 4096, 1 token")
+        r1 = make_requests(1024, 1, "uniform", SEED + 7)
+        one["run"] = run_leg(fa, lib, r1, 10 * slice_sizes(fa, fa.FMT_Q4KT)[0])
+        extra["config1_latency"] = one
+        eng.release(0)
+        for name, k in (("config3a_q8", "q8"), ("config3b_mxfp4", "mxfp4"), ("native_h4096", "native")):
+            f = getattr(fa, WORKLOADS[k]["fmt"])
+            for b in range(SLICES):
+                fa.check(eng.synthetic(b, HIDDEN, f, LAYERS, SEED), "fr_hip_synthetic")
+            extra[name] = decode_leg(fa, lib, eng, k, 300, 50, SEED + 8)
+            for b in range(SLICES):
+                eng.release(b)
+        m, _ = prefill_leg(fa, lib, eng, 2, 1)
+        for b in range(SLICES):
+            eng.release(b)
+        extra["config5_prefill"] = {
+            "workload": PREFILL_TEXT, "chunks": 2, "chunk_ms": round(m["chunk_ms"], 3),
+            "layer_us": round(m["chunk_ms"] * 1e3 / PREFILL_LAYERS, 2),
+            "weight_bytes_per_chunk": m["weights"], "gbs": round(m["achieved"], 1),
+            "frac": round(m["achieved"] / HBM_PEAK_GBS, 4),
+            "tokens_per_s_per_layer": round(PREFILL_TOKENS / (m["chunk_ms"] * 1e-3 / PREFILL_LAYERS), 1),
+            "mfma_tflops_fp32_equiv": round(m["tflops"], 2)}
+        for k2, v in extra.items():
+            log(f"{k2}: {v.get('kernel_us', v.get('chunk_ms'))} {v.get('gbs')} GB/s")
+    else:
+        for b in range(SLICES):
+            eng.release(b)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_reference_leg(fa, lib, eng)
 
     out = {
         "metric": METRIC,
@@ -685,16 +928,20 @@ def main():
         "kernel_us": round(kernel_ms * 1e3, 3),
         "kernel_split_us": {"main": round(main_us, 3), "rest": round(launch_us - main_us, 3),
                             "note": "events between the kernels of each launch, second pass"},
-        "weight_bytes_per_call": float(wts[timed].mean()),
-        "grid": grid,
-        "run_wall_us": {"p50": round(float(np.percentile(run_us, 50)), 2),
-                        "p99": round(float(np.percentile(run_us, 99)), 2)},
-        "run_wall_gbs": round(float(wts[:args.run_calls].mean() / (np.median(run_us) * 1e-6) / 1e9), 2),
+        "weight_bytes_per_call": float(L.wts[timed].mean()),
+        "grid": L.grid,
+        "run": run_rec,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": grid_kernels(lib, host[args.warmup])},
+                     "achievable": {"gbs": ceiling["scattered"]["gbs"],
+                                    "frac_of_achievable": round(achieved / ceiling["scattered"]["gbs"], 4),
+                                    "probe": ceiling, "bytes_per_call": ceiling_bytes,
+                                    "note": "streaming probe over the same scattered slices (and a contiguous "
+                                            "buffer of the same size), best of a short sweep"},
+                     "kernel": L.kernels},
         "cpu_baseline": cpu,
-        "cpu_reference_avx2": avx2,
+        "cpu_scalar_port": scalar,
+        "configs": extra,
     }
     print(json.dumps(out), flush=True)
 

@@ -52,6 +52,8 @@ SIGNATURES = {
     "fr_hip_synthetic": (C.c_int, [C.c_uint, C.c_uint, C.c_uint, C.c_uint, C.c_uint64]),
     "fr_hip_release": (C.c_int, [C.c_uint]),
     "fr_hip_unit_bytes": (C.c_uint64, [C.c_uint, C.c_uint]),
+    "fr_hip_capacity": (C.c_int, [C.c_int, C.c_uint, C.c_uint, C.c_uint64, C.POINTER(C.c_uint64),
+                                  C.POINTER(C.c_uint)]),
     "fr_hip_run": (C.c_int, [C.POINTER(Request), C.POINTER(C.c_float)]),
     "fr_hip_plan_bytes": (C.c_size_t, [C.c_uint, C.c_uint]),
     "fr_hip_plan": (C.c_int, [C.POINTER(Request), C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t),
@@ -113,6 +115,13 @@ def check(rc, what):
 
 def unit_bytes(hidden, fmt):
     return lib().fr_hip_unit_bytes(hidden, fmt)
+
+
+def capacity(hidden, fmt, reserve=0, device=0):
+    """(rc, free HBM bytes, units of (hidden, fmt) the device holds)."""
+    free, blocks = C.c_uint64(0), C.c_uint(0)
+    rc = lib().fr_hip_capacity(device, hidden, fmt, reserve, C.byref(free), C.byref(blocks))
+    return rc, free.value, blocks.value
 
 
 def make_request(layer, experts, gates, x, mode=MODE_F32):

@@ -3731,6 +3731,33 @@ uint64_t fr_hip_unit_bytes(unsigned hidden, unsigned format) {
   return layout_of(hidden, format, l) ? l.block : 0;
 }
 
+int fr_hip_capacity(int device, unsigned hidden, unsigned format, uint64_t reserve, uint64_t* free_bytes,
+                    unsigned* blocks) {
+  if (!free_bytes || !blocks) return FR_HIP_INVALID;
+  Layout l;
+  if (!layout_of(hidden, format, l)) return FR_HIP_INVALID;
+  int rc = fr_hip_probe(device, nullptr, 0);
+  if (rc) return rc;
+  int previous = 0;
+  CK(hipGetDevice(&previous));
+  CK(hipSetDevice(device));
+  size_t avail = 0, total = 0;
+  const hipError_t e = hipMemGetInfo(&avail, &total);
+  CK(hipSetDevice(previous));
+  if (e != hipSuccess) return FR_HIP_IO;
+  // Units this engine already holds on the device count as available: the
+  // figure is the device's capacity for units, not what is left of it.
+  uint64_t held = 0;
+  if (g_open && E.device == device)
+    for (int b = 0; b < kBlocks; ++b)
+      if (E.block[b]) held += E.lay[b].block;
+  const uint64_t usable = (uint64_t)avail + held;
+  const uint64_t n = usable > reserve ? (usable - reserve) / l.block : 0;
+  *free_bytes = (uint64_t)avail;
+  *blocks = n > (uint64_t)kBlocks ? (unsigned)kBlocks : (unsigned)n;
+  return FR_HIP_OK;
+}
+
 static int open_engine(int device);
 
 int fr_hip_open(int device) {

@@ -90,6 +90,14 @@ int fr_hip_synthetic(unsigned block, unsigned hidden, unsigned format, unsigned 
 int fr_hip_release(unsigned block);
 /* Unit bytes of a (hidden, format) pair, 0 if unsupported. */
 uint64_t fr_hip_unit_bytes(unsigned hidden, unsigned format);
+/* The device's capacity for units, for the node's share: selection_capacity
+ * (src/selection.c:227-244) counts host memory only, while this backend
+ * keeps every loaded unit in HBM. Returns in *blocks how many units of
+ * (hidden, format) the device holds in its free memory plus the units this
+ * engine already holds there, less `reserve` bytes, capped at 20 blocks;
+ * *free_bytes is the device's free memory now. No open engine needed. */
+int fr_hip_capacity(int device, unsigned hidden, unsigned format, uint64_t reserve, uint64_t *free_bytes,
+                    unsigned *blocks);
 
 /* The hot path (run: src/backend.h:63, backends/ref.c:57-98): H2D of x and
  * the launch plan, ONE kernel launch over every (expert, owned slice) pair,

@@ -40,3 +40,13 @@ def test_calls_before_open_are_state_errors():
     assert lib.fr_hip_release(0) == fa.STATE
     assert lib.fr_hip_release(20) == fa.INVALID
     assert lib.fr_hip_reserve(0, 4096, fa.FMT_Q4KT) in (fa.STATE, fa.OK)
+
+
+def test_capacity_argument_checks():
+    lib = fa.lib()
+    n = C.c_uint(0)
+    f = C.c_uint64(0)
+    assert lib.fr_hip_capacity(0, 2560, fa.FMT_NATIVE, 0, None, C.byref(n)) == fa.INVALID
+    assert lib.fr_hip_capacity(0, 1000, fa.FMT_NATIVE, 0, C.byref(f), C.byref(n)) == fa.INVALID
+    rc, free, blocks = fa.capacity(2560, fa.FMT_NATIVE, device=99)
+    assert rc == fa.UNSUPPORTED
