@@ -144,6 +144,13 @@ __device__ __forceinline__ bool mx_block_bad(uint32_t e, const uint4& q) {
   const uint32_t ge4 = ((q.x & (q.x >> 1)) | (q.y & (q.y >> 1)) | (q.z & (q.z >> 1)) | (q.w & (q.w >> 1))) & 0x22222222u;
   return e == 255u || (e == 254u && ge2 != 0u) || (e == 253u && ge4 != 0u);
 }
+// mx_block_bad behind a wave-wide screen for the hot loops: only exponents
+// 253..255 can make a block bad, so the code test runs (for the whole wave)
+// only when some lane holds such an exponent.
+__device__ __forceinline__ bool mx_blocks_bad(uint32_t e0, const uint4& q0, uint32_t e1, const uint4& q1) {
+  if (__builtin_expect(__ballot((e0 > e1 ? e0 : e1) >= 253u) == 0, 1)) return false;
+  return mx_block_bad(e0, q0) || mx_block_bad(e1, q1);
+}
 
 // Two OCP E2M1 codes (byte b of v: low nibble first) -> floats times
 // `scale`, with the gfx950 conversion instruction. The products are exact
@@ -441,7 +448,7 @@ __device__ __forceinline__ bool raw_scales(const LaneRaw& r, int c, float s[2], 
     s[0] = e8m0(r.h.x & 0xff);
     s[1] = e8m0((r.h.x >> 8) & 0xff);
     m[0] = m[1] = 0.f;
-    return !mx_block_bad(r.h.x & 0xff, r.q[0]) && !mx_block_bad((r.h.x >> 8) & 0xff, r.q[1]);
+    return !mx_blocks_bad(r.h.x & 0xff, r.q[0], (r.h.x >> 8) & 0xff, r.q[1]);
   } else {  // Q8_0, Q4_0: two fp16 scales
     s[0] = half_to_float(r.h.x & 0xffff);
     s[1] = half_to_float(r.h.x >> 16);
@@ -2073,7 +2080,7 @@ __device__ __forceinline__ void rows_down(const RowsDown& R, const float* hs, fl
     float sc;
     if (DN == TMXFP4) {
       const uint32_t e = (word(R.sc, o >> 2) >> (8 * (o & 3))) & 0xffu;
-      if (valid && mx_block_bad(e, R.q0[o])) bad |= kErrScale;
+      if (valid && mx_blocks_bad(e, R.q0[o], 0u, R.q0[o])) bad |= kErrScale;
       sc = e8m0(e);
     } else {
       const uint32_t hb = (word(R.sc, o >> 1) >> (16 * (o & 1))) & 0xffffu;
