@@ -527,7 +527,7 @@ class Launches:
     """A workload's launch plans resident in HBM and enqueued with fr_hip_launch
     on one stream."""
 
-    def __init__(self, fa, lib, eng, fmt, reqs, blocks=SLICES):
+    def __init__(self, fa, lib, eng, fmt, reqs, blocks=SLICES, mode=None):
         import torch
         self.fa, self.lib = fa, lib
         n = len(reqs)
@@ -539,7 +539,7 @@ class Launches:
         self.wts = np.zeros(n)
         self.grid = 0
         for i, (layer, experts, gates, x) in enumerate(reqs):
-            plan, self.grid = eng.plan(layer, experts, gates, x, fa.MODE_F32)
+            plan, self.grid = eng.plan(layer, experts, gates, x, fa.MODE_F32 if mode is None else mode)
             self.host[i, :plan.size] = plan
             self.wts[i], self.alg[i] = algorithmic_bytes(fa, fmt, experts, gates, blocks)
         self.dev = torch.from_numpy(self.host).to("cuda")
@@ -589,13 +589,14 @@ class Launches:
         return main_ms.value * 1e3 / counted.value, total_ms.value * 1e3 / counted.value
 
 
-def decode_leg(fa, lib, eng, key, steps, warmup, seed, blocks=SLICES):
+def decode_leg(fa, lib, eng, key, steps, warmup, seed, blocks=SLICES, mode=None):
     """One decode workload with its `blocks` owned slices already resident:
-    `warmup` then `steps` pipelined launches. Returns the extra-key record."""
+    `warmup` then `steps` pipelined launches (F32 unless `mode`). Returns the
+    extra-key record."""
     wl = WORKLOADS[key]
     fmt = getattr(fa, wl["fmt"])
     reqs = make_requests(warmup + steps, wl["burst"], wl["routing"], seed)
-    L = Launches(fa, lib, eng, fmt, reqs, blocks)
+    L = Launches(fa, lib, eng, fmt, reqs, blocks, mode)
     for i in range(warmup):
         L.enqueue(i)
     wall, ms = L.timed(warmup, warmup + steps)
@@ -871,6 +872,10 @@ def main():
     extra = {}
     if not args.no_extra and key == "q4k":
         extra["config4_mtp4"] = decode_leg(fa, lib, eng, "mtp4", 300, 50, SEED + 4)
+        q8 = decode_leg(fa, lib, eng, "q4k", 100, 20, SEED + 5, mode=fa.MODE_Q8)
+        q8["workload"] = ("config 2 in the ref-q8 arithmetic (the hip-q8 table: x and h through "
+                          "fr_q8_activation, fp64 sums)")
+        extra["config2_ref_q8"] = q8
         for b in range(1, SLICES):
             eng.release(b)
         one = decode_leg(fa, lib, eng, "q4k", 300, 50, SEED + 6, blocks=1)

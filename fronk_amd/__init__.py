@@ -74,6 +74,7 @@ SIGNATURES = {
     "fr_hip_debug_dequant": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_dequant_down": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_quantize": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.POINTER(C.c_float)]),
+    "fr_hip_debug_quantize64": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_read": (C.c_int, [C.c_uint, C.c_uint64, C.c_void_p, C.c_uint64]),
 }
 
@@ -240,8 +241,11 @@ class Engine:
                                              fptr(out))
         return rc, out
 
-    def quantize(self, x):
+    def quantize(self, x, regs=False):
+        """fr_q8_activation on the device: the group form, or with `regs` the
+        register form of the single-token Q8 path."""
         x = np.ascontiguousarray(x, np.float32)
         out = np.zeros_like(x)
-        rc = lib().fr_hip_debug_quantize(fptr(x), x.size, fptr(out))
+        fn = lib().fr_hip_debug_quantize64 if regs else lib().fr_hip_debug_quantize
+        rc = fn(fptr(x), x.size, fptr(out))
         return rc, out

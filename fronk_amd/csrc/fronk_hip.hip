@@ -3023,6 +3023,19 @@ __global__ void debug_quantize(float* x, uint32_t groups) {
   if (g < groups) q8_group(x + 64 * g, 64);
 }
 
+// The register form: one 64-value group per thread through q8_regs64.
+__global__ void debug_quantize_regs(float* x, uint32_t groups) {
+  uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  float4 v[16];
+  float4* p = reinterpret_cast<float4*>(x + 64 * (size_t)g);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = p[i];
+  q8_regs64(v);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) p[i] = v[i];
+}
+
 __global__ void debug_quantize32(float* x, uint32_t groups) {
   uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g < groups) q8_group(x + 32 * g, 32);
@@ -4298,14 +4311,15 @@ int fr_hip_debug_dequant_down(unsigned format, const void* down, unsigned hidden
   return status ? FR_HIP_NUMERIC : FR_HIP_OK;
 }
 
-int fr_hip_debug_quantize(const float* x, unsigned n, float* out) {
+static int debug_quantize_run(const float* x, unsigned n, float* out, bool regs) {
   if (!g_open) return FR_HIP_STATE;
-  if (!x || !out || !n || (n % 64 && n != 32)) return FR_HIP_INVALID;
+  if (!x || !out || !n || (n % 64 && (regs || n != 32))) return FR_HIP_INVALID;
   CK(hipSetDevice(E.device));
   float* d = nullptr;
   CK(hipMalloc(&d, n * sizeof(float)));
   CK(hipMemcpy(d, x, n * sizeof(float), hipMemcpyHostToDevice));
-  if (n == 32) hipLaunchKernelGGL(debug_quantize32, dim3(1), dim3(64), 0, E.stream, d, 1u);
+  if (regs) hipLaunchKernelGGL(debug_quantize_regs, dim3((n / 64 + 63) / 64), dim3(64), 0, E.stream, d, n / 64);
+  else if (n == 32) hipLaunchKernelGGL(debug_quantize32, dim3(1), dim3(64), 0, E.stream, d, 1u);
   else hipLaunchKernelGGL(debug_quantize, dim3((n / 64 + 63) / 64), dim3(64), 0, E.stream, d, n / 64);
   CK(hipGetLastError());
   CK(hipStreamSynchronize(E.stream));
@@ -4313,5 +4327,8 @@ int fr_hip_debug_quantize(const float* x, unsigned n, float* out) {
   (void)hipFree(d);
   return FR_HIP_OK;
 }
+
+int fr_hip_debug_quantize(const float* x, unsigned n, float* out) { return debug_quantize_run(x, n, out, false); }
+int fr_hip_debug_quantize64(const float* x, unsigned n, float* out) { return debug_quantize_run(x, n, out, true); }
 
 }  // extern "C"

@@ -22,6 +22,10 @@
  *   self_test  FR_STATE when a block is loaded; the golden corpus, then the
  *           native self-test (backends/avx2.c:773-777).
  *   fr_hip_backend_close  the bench's close hook (src/bench.c:265-278).
+ * A second table, "hip-q8", is this backend with the ref-q8 arithmetic
+ * (backends/ref.c:66,85: x and h through fr_q8_activation, fp64 sums), the
+ * counterpart of the reference's ref / ref-q8 pair (backends/ref.c:124-125).
+ * Both tables share the device and the loaded blocks.
  * During self_test, load only reserves device memory and run copies the
  * slices a request references from the borrowed bytes first: the corpus
  * fixtures are sparse multi-GB units, and the native self-test corrupts the
@@ -128,13 +132,13 @@ static int refresh_referenced(const fr_req *r) {
     return FR_OK;
 }
 
-static int run(const fr_req *r, fr_part *out) {
+static int run_mode(const fr_req *r, fr_part *out, unsigned mode) {
     if (!out) return FR_INVALID;
     int rc = validate(r);
     if (rc) return rc;
     if (!loaded()) return FR_STATE;
     if (coherent && (rc = refresh_referenced(r))) return rc;
-    fr_hip_request q = {r->layer, r->burst, FR_HIDDEN, FR_HIP_MODE_F32, &r->expert[0][0], &r->gate[0][0], &r->x[0][0]};
+    fr_hip_request q = {r->layer, r->burst, FR_HIDDEN, mode, &r->expert[0][0], &r->gate[0][0], &r->x[0][0]};
     rc = fr_hip_run(&q, &result[0][0]);
     if (rc) return rc;
     out->layer = r->layer;
@@ -144,18 +148,25 @@ static int run(const fr_req *r, fr_part *out) {
     return FR_OK;
 }
 
-static int bench(int burst_max, fr_costmodel *out) { return fr_bench_execute_backend(&fr_hip, burst_max, out); }
+static int run(const fr_req *r, fr_part *out) { return run_mode(r, out, FR_HIP_MODE_F32); }
+static int run_q8(const fr_req *r, fr_part *out) { return run_mode(r, out, FR_HIP_MODE_Q8); }
 
-static int self_test(const char *dir) {
+static int bench(int burst_max, fr_costmodel *out) { return fr_bench_execute_backend(&fr_hip, burst_max, out); }
+static int bench_q8(int burst_max, fr_costmodel *out) { return fr_bench_execute_backend(&fr_hip_q8, burst_max, out); }
+
+static int check(const fr_backend *b, const char *dir) {
     if (loaded()) return FR_STATE;
     coherent = 1;
-    int rc = fr_vectors_check(&fr_hip, dir, &fr_backend_tolerance, NULL);
-    if (!rc) rc = fr_native_self_test(&fr_hip);
+    int rc = fr_vectors_check(b, dir, &fr_backend_tolerance, NULL);
+    if (!rc) rc = fr_native_self_test(b);
     coherent = 0;
     return rc;
 }
+static int self_test(const char *dir) { return check(&fr_hip, dir); }
+static int self_test_q8(const char *dir) { return check(&fr_hip_q8, dir); }
 
 const fr_backend fr_hip = {"hip", probe, load, unload, run, bench, self_test};
+const fr_backend fr_hip_q8 = {"hip-q8", probe, load, unload, run_q8, bench_q8, self_test_q8};
 
 /* The bench's backend_close hook (src/bench.c:265-278), like fr_avx2_close
  * (backends/avx2.c:718): FR_STATE while a block is loaded, otherwise release

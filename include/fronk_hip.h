@@ -205,6 +205,10 @@ int fr_hip_debug_dequant(unsigned type, const void *row, unsigned n, float *out)
  * (element (d, n) = weight of neuron n for output d) for every down format. */
 int fr_hip_debug_dequant_down(unsigned format, const void *down, unsigned hidden, float *out);
 int fr_hip_debug_quantize(const float *x, unsigned n, float *out);
+/* The same quantizer in its register form (q8_regs64: one 64-value group held
+ * in one lane's registers), which the single-token Q8 path applies to x;
+ * n a multiple of 64. */
+int fr_hip_debug_quantize64(const float *x, unsigned n, float *out);
 /* Copy `len` re-tiled device bytes of a block, from byte `offset`. */
 int fr_hip_debug_read(unsigned block, uint64_t offset, void *out, uint64_t len);
 

@@ -119,11 +119,12 @@ def test_quantize_bit_exact(eng):
     ties[256] = 2.0 ** -125
     cases.append(ties)
     for x in cases:
-        rc, got = eng.quantize(x)
-        assert rc == fa.OK
         rc, want = oracle.q8_activation(x)
         assert rc == 0
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        for regs in (False, True):   # q8_group and q8_regs64
+            rc, got = eng.quantize(x, regs)
+            assert rc == fa.OK
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), regs
     # The 32-value hidden-slice form.
     for x in [rng.standard_normal(32).astype(np.float32) * 1e4, ties[:32].copy()]:
         rc, got = eng.quantize(x)

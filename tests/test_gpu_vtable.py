@@ -22,3 +22,12 @@ def test_probe_finds_gfx950():
 def test_reference_self_test():
     print("hip self_test: golden corpus, then native self-test", flush=True)
     assert vt.backend().self_test(vt.GOLDEN.encode()) == vt.OK
+
+
+def test_reference_self_test_q8():
+    """The "hip-q8" table (ref-q8 arithmetic) through the same harness: the
+    corpus within the backend tolerance, the native self-test against ref."""
+    q8 = vt.backend("fr_hip_q8")
+    assert q8.name == b"hip-q8"
+    print("hip-q8 self_test: golden corpus, then native self-test", flush=True)
+    assert q8.self_test(vt.GOLDEN.encode()) == vt.OK

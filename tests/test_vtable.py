@@ -28,6 +28,23 @@ def test_name_and_table():
         assert C.cast(getattr(m, f), C.c_void_p).value == C.cast(getattr(b, f), C.c_void_p).value
 
 
+def test_q8_table_shares_the_backend():
+    """"hip-q8" differs from "hip" only in run, bench and self_test (the
+    ref-q8 arithmetic); probe, load and unload are the same functions."""
+    b, q = vt.backend(), vt.backend("fr_hip_q8")
+    assert q.name == b"hip-q8"
+    for f in ("probe", "load", "unload"):
+        assert C.cast(getattr(q, f), C.c_void_p).value == C.cast(getattr(b, f), C.c_void_p).value
+    for f in ("run", "bench", "self_test"):
+        assert C.cast(getattr(q, f), C.c_void_p).value != C.cast(getattr(b, f), C.c_void_p).value
+    out = vt.Part()
+    req = vt.Req()
+    req.layer, req.burst = 0, 1
+    for j in range(10):
+        req.expert[0][j] = j
+    assert q.run(C.byref(req), C.byref(out)) == vt.STATE   # valid request, nothing loaded
+
+
 def test_backend_close_without_blocks():
     """The bench's close hook (src/bench.c:265-278) succeeds, and is
     repeatable, when no block is loaded."""

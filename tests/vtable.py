@@ -39,7 +39,7 @@ class Backend(C.Structure):       # fr_backend (src/backend.h:52-67)
                 ("run", RunFn), ("bench", BenchFn), ("self_test", SelfTestFn)]
 
 
-_vt = None
+_vt = {}
 _lib = None
 
 
@@ -57,9 +57,9 @@ def library():
     return _lib
 
 
-def backend():
-    """The fr_hip vtable."""
-    global _vt
-    if _vt is None:
-        _vt = Backend.in_dll(library(), "fr_hip")
-    return _vt
+def backend(symbol="fr_hip"):
+    """The fr_hip vtable (or fr_hip_q8, the same backend with ref-q8
+    arithmetic)."""
+    if symbol not in _vt:
+        _vt[symbol] = Backend.in_dll(library(), symbol)
+    return _vt[symbol]
