@@ -1537,13 +1537,19 @@ __device__ __forceinline__ float header_pass(const uint4& h, unsigned sb, unsign
                                              DecodeLds& L, uint32_t& bad) {
   if (half_bad(h.x) || half_bad(h.x >> 16)) bad |= kErrScale;
   const float d = half_to_float(h.x & 0xffff), dm = half_to_float(h.x >> 16);
+  // q4k_scale_min for all eight sub-blocks at once, one value per byte:
+  // sub-blocks 0..3 are the low six bits of bytes 0..3 (scales) and 4..7
+  // (mins); sub-blocks 4..7 take the low (scales) or high (mins) nibble of
+  // bytes 8..11 with the top two bits of bytes 0..3 or 4..7 above it.
+  const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, mi_lo = h.z & 0x3F3F3F3Fu;
+  const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+  const uint32_t mi_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
   float mins = 0.f;
 #pragma unroll
   for (int g = 0; g < 8; ++g) {
-    uint32_t sc, mi;
-    q4k_scale_min(h.y, h.z, h.w, (uint32_t)g, sc, mi);
-    L.dsc[wave][8 * sbl + g][lane] = d * (float)sc;
-    mins += (dm * (float)mi) * L.xs[t][8 * sb + g];   // t: the x slot
+    const float sc = ub(g < 4 ? sc_lo : sc_hi, g & 3), mi = ub(g < 4 ? mi_lo : mi_hi, g & 3);
+    L.dsc[wave][8 * sbl + g][lane] = d * sc;
+    mins += (dm * mi) * L.xs[t][8 * sb + g];   // t: the x slot
   }
   return mins;
 }
