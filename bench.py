@@ -301,7 +301,7 @@ PREFILL_TOKENS = 512
 MFMA_F32_PEAK_TFLOPS = 157.3
 PREFILL_TEXT = ("Resident node prefill: 48 layers x 512 experts x 640 intermediate x hidden 4096, all Q4_K "
                 "(down transposed, 108.7 GB in HBM); a chunk of 512 tokens, top-10 of 512 uniform per token per "
-                "layer, through fr_hip_run_batch (fp32 matrix cores)")
+                "layer, through fr_hip_run_batch (f16 and bf16 matrix cores on exactly split operands, fp32 accumulation)")
 
 
 def prefill_requests(rng, layers, tokens):
