@@ -263,7 +263,7 @@ def cpu_baseline(fa, eng, fmt, reqs, budget_s):
     from fixtures import host_units
     lay = oracle.layout(HIDDEN, fmt)
     done, seconds, wbytes = 0, 0.0, 0
-    worst = [0.0, 0.0]
+    worst = [0.0, 0.0, 0.0, 0.0]   # rel. L2, normalized max, absolute max-abs, max |y_ref|
     for layer, experts, gates, x in reqs:
         units = host_units(lay, SEED, layer, experts)
         req = oracle.Req()
@@ -281,7 +281,9 @@ def cpu_baseline(fa, eng, fmt, reqs, budget_s):
             raise RuntimeError(f"fr_hip_run failed with {rc}")
         for t in range(req.burst):
             rc, err = oracle.compare(ref[t], y[t])
-            worst = [max(worst[0], err[0]), max(worst[1], err[1])]
+            worst = [max(worst[0], err[0]), max(worst[1], err[1]),
+                     max(worst[2], float(np.max(np.abs(y[t].astype(np.float64) - ref[t])))),
+                     max(worst[3], float(np.max(np.abs(ref[t]))))]
         wbytes += algorithmic_bytes(fa, fmt, experts, gates)[0]
         done += 1
         del units
@@ -292,7 +294,8 @@ def cpu_baseline(fa, eng, fmt, reqs, budget_s):
         "sample": f"{done} calls of this workload through the oracle's scalar restatement of ref "
                   f"(backends/ref.c:57-98), 1 thread, {seconds:.1f} s",
         "tokens_per_s": done * reqs[0][1].shape[0] / seconds,
-        "gpu_vs_oracle": {"rel_l2_max": worst[0], "normalized_max": worst[1], "calls": done},
+        "gpu_vs_oracle": {"rel_l2_max": worst[0], "normalized_max": worst[1], "abs_max": worst[2],
+                          "ref_abs_max": worst[3], "calls": done},
     }
 
 
@@ -322,7 +325,7 @@ def prefill_cpu_baseline(fa, y0, req, budget_s):
     from fixtures import host_units, oracle_request
     lay = oracle.layout(HIDDEN, fa.FMT_Q4KT)
     layer, experts, gates, x = req
-    done, seconds, wbytes, worst = 0, 0.0, 0, [0.0, 0.0]
+    done, seconds, wbytes, worst = 0, 0.0, 0, [0.0, 0.0, 0.0, 0.0]
     for t0 in range(0, experts.shape[0], 8):
         sl = slice(t0, t0 + 8)
         units = host_units(lay, SEED, layer, experts[sl])
@@ -333,7 +336,9 @@ def prefill_cpu_baseline(fa, y0, req, budget_s):
             raise RuntimeError(f"oracle ref_run failed with {rc}")
         for t in range(ref.shape[0]):
             rc, err = oracle.compare(ref[t], y0[t0 + t])
-            worst = [max(worst[0], err[0]), max(worst[1], err[1])]
+            worst = [max(worst[0], err[0]), max(worst[1], err[1]),
+                     max(worst[2], float(np.max(np.abs(y0[t0 + t].astype(np.float64) - ref[t])))),
+                     max(worst[3], float(np.max(np.abs(ref[t]))))]
         wbytes += len(set(experts[sl].ravel().tolist())) * SLICES * lay.slice
         done += ref.shape[0]
         del units
@@ -344,7 +349,8 @@ def prefill_cpu_baseline(fa, y0, req, budget_s):
         "sample": f"{done} tokens of layer 0 in bursts of 8 through the oracle's scalar restatement of ref "
                   f"(backends/ref.c:57-98), 1 thread, {seconds:.1f} s",
         "tokens_per_s": done / seconds,
-        "gpu_vs_oracle": {"rel_l2_max": worst[0], "normalized_max": worst[1], "tokens": done},
+        "gpu_vs_oracle": {"rel_l2_max": worst[0], "normalized_max": worst[1], "abs_max": worst[2],
+                          "ref_abs_max": worst[3], "tokens": done},
     }
 
 

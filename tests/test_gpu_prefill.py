@@ -136,6 +136,29 @@ def test_prefill_512_tokens_properties(eng):
     check_close(run_bursts(eng, layer, experts[:16], gates[:16], x[:16]), y[:16], fa.MODE_F32, "prefill vs run")
 
 
+def test_prefill_48_layers_resident(eng):
+    """The resident node of the prefill workload: 48 layers of 20 owned
+    blocks in HBM (108.7 GB), a 512-token chunk on the last layer, whose
+    slices sit at the top of each block's 5.4 GB. Sampled rows against the
+    oracle; every row finite; a repeat is bit-identical."""
+    hidden, tokens, layer = 4096, 512, 47
+    lay = oracle.layout(hidden, fa.FMT_Q4KT)
+    print("prefill: 20 blocks x 48 layers resident", flush=True)
+    load(eng, hidden, range(20), layers=48)
+    try:
+        rng = np.random.default_rng(4847)
+        experts, gates, x = chunk(rng, tokens, hidden)
+        y = run_ok(eng, layer, experts, gates, x)
+        assert np.isfinite(y).all()
+        assert np.array_equal(run_ok(eng, layer, experts, gates, x).view(np.uint32), y.view(np.uint32))
+        sample = np.arange(5, tokens, 73)
+        ref = oracle_rows(lay, range(20), layer, experts[sample], gates[sample], x[sample])
+        check_close(ref, y[sample], fa.MODE_F32, "prefill layer 47 of 48")
+    finally:
+        for b in range(20):
+            eng.release(b)
+
+
 def test_prefill_error_paths(eng):
     hidden = 4096
     load(eng, hidden, (0, 1))
