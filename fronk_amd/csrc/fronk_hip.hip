@@ -1847,6 +1847,399 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
   if (bad) flag(status, bad);
 }
 
+// ------------------------------------------------- decode kernel, ref-q8
+//
+// The ref-q8 arithmetic (backends/ref.c:66,85: x quantized per 64 and h per
+// 32 by fr_q8_activation, src/q4.c:37-61; dots, SiLU and the gated sum in
+// double) on decode_kernel's work list and tiles: Q4_K gate/up with the
+// transposed Q4_K down, T <= 8.
+//
+// A quantized value is q = (float)(k*s), k an integer in [-127, 127] and s
+// the group's scale. k*s needs up to 31 bits, but its rounding error is a
+// multiple of u = 2^(floor(log2 s) - 23) (the last bit of s; 2^-149 for a
+// subnormal s) of at most 64u, so q = s*k + u*r exactly with k and r signed
+// bytes. x is staged as these two digits, and the same int8 matrix products
+// as decode_kernel's give exact integer dots of each row with k and with r
+// per 32-value sub-block. Everything after them is double: each dot times
+// d*sc times its digit's weight is exact before the sum, the min term uses
+// the exact sum of the sub-block's values, so a and u differ from the
+// reference's double dots only in the order of the additions. That holds
+// where the reference's float weight (d*sc)*q - dmin*mi (src/native.c:14-22)
+// is exact, which is the case when the fp16 exponents of d and dmin differ
+// by -7..3; a super-block header outside that range sets kErrInexact, and
+// fr_hip_run then runs the request on layer_kernel, which decodes every
+// weight as the reference does.
+//
+// h = SiLU(a)*u as in ref (a and u narrowed to float, the sigmoid in
+// double), quantized per 32 (the unit's 32 neurons), so the down follows
+// the fourth round: the four rounds' down bytes stay in registers, and the
+// down is double FMAs over the nibbles (as q*2^-9 from the FP8 conversion,
+// exact). The unit's partial gate*dot is stored in double; decode_reduce
+// sums a token's partials in double in the reference's order.
+constexpr uint32_t kErrInexact = 8;   // a weight the reference rounds in float (ref-q8 decode only)
+
+struct DecodeQ8Table {                 // one wavefront's down coefficients of one round
+  double D[2][8][8];                   // [super-block][group][neuron] d*sc*h
+  double M[2][8][8];                   // dmin*mi*h
+};
+struct DecodeQ8Lds {
+  int8_t xd[2][4][kSubBlocks][32];     // [x slot][digit][sub-block][value]: k, r, 0, 0
+  float xw[2][kSubBlocks][4];          // [x slot][sub-block][digit]: s, u, 0, 0
+  double xs[2][kSubBlocks];            // exact sum of each sub-block's quantized values
+  float dsc[kDecodeWaves][16][64];     // [wave][sub-block of its super-blocks][row] d*sc
+  double rowp[2][kDecodeWaves][64];    // [unit parity][wave][row] scaled integer dots
+  double minp[2][kDecodeWaves][64];    // [unit parity][wave][row] min terms
+  float h[kDecodeWaves][32];           // the unit's h, then quantized (each wavefront's own copy)
+  uint4 dh[kDecodeWaves][16];
+  DecodeQ8Table table[kDecodeWaves];
+};
+static_assert(sizeof(DecodeQ8Lds) <= 160 * 1024, "ref-q8 decode LDS");
+
+// The reference's float weight is exact for every scale, min and quant of a
+// header whose d and dmin exponents differ by -7..3 (either one zero is exact
+// too); subnormals count as exponent -14.
+__device__ __forceinline__ bool q4k_weights_exact(uint32_t dm) {
+  const int ed = max((int)((dm >> 10) & 31u), 1), em = max((int)((dm >> 26) & 31u), 1);
+  const bool zero = (dm & 0x7fffu) == 0 || (dm & 0x7fff0000u) == 0;
+  return zero || (ed - em <= 3 && em - ed <= 7);
+}
+
+// fr_q8_activation of x (src/q4.c:37-61) and its two-digit staging: thread
+// t holds values 8(t%4)..+7 of sub-block t/4; the eight threads of a 64-value
+// group agree on its largest magnitude.
+__device__ __forceinline__ void stage_x_q8(const float4 (&v4)[2], unsigned slot, unsigned nsub, DecodeQ8Lds& L,
+                                           uint32_t& bad) {
+  const unsigned tid = threadIdx.x, s = tid >> 2, q = tid & 3;
+  const float v[8] = {v4[0].x, v4[0].y, v4[0].z, v4[0].w, v4[1].x, v4[1].y, v4[1].z, v4[1].w};
+  float m = 0.f;
+  uint32_t fin = 1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    m = fmaxf(m, fabsf(v[i]));
+    fin &= isfinite(v[i]) ? 1u : 0u;
+  }
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    m = fmaxf(m, __shfl_xor(m, o));
+    fin &= (uint32_t)__shfl_xor((int)fin, o);
+  }
+  if (!fin && s < nsub) bad |= kErrRange;   // fr_q8_activation's FR_NUMERIC
+  const float scale = m / 127.0f, inv = 127.0f / m;
+  const bool zero = scale == 0.f || !fin, finite_inv = isfinite(inv);
+  int es = 0;
+  (void)frexpf(scale, &es);                 // scale in [2^(es-1), 2^es)
+  const int ue = max(es - 24, -149);
+  const double ud = ldexp(1.0, ue);
+  uint32_t w[2][2] = {{0u, 0u}, {0u, 0u}};
+  double sum = 0.0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float r = finite_inv ? v[i] * inv : (v[i] / m) * 127.0f;
+    r = fminf(fmaxf(rintf(r), -127.f), 127.f);
+    const double back = fmin(fmax((double)r * (double)scale, -(double)FLT_MAX), (double)FLT_MAX);
+    const float xq = zero ? 0.f : (float)back;
+    const int k = zero ? 0 : (int)r;
+    const int rem = (int)(((double)xq - (double)k * (double)scale) / ud);   // exact: a multiple of u
+    if (rem < -127 || rem > 127) bad |= kErrRange;                          // only where k*s passes FLT_MAX
+    w[0][i >> 2] |= (uint32_t)(k & 255) << (8 * (i & 3));
+    w[1][i >> 2] |= (uint32_t)(rem & 255) << (8 * (i & 3));
+    sum += (double)xq;                      // exact: multiples of u below 2^37 u
+  }
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  if (s < nsub) {
+    *reinterpret_cast<uint2*>(&L.xd[slot][0][s][8 * q]) = make_uint2(w[0][0], w[0][1]);
+    *reinterpret_cast<uint2*>(&L.xd[slot][1][s][8 * q]) = make_uint2(w[1][0], w[1][1]);
+    *reinterpret_cast<uint2*>(&L.xd[slot][2][s][8 * q]) = make_uint2(0u, 0u);
+    *reinterpret_cast<uint2*>(&L.xd[slot][3][s][8 * q]) = make_uint2(0u, 0u);
+    if (q == 0) {
+      *reinterpret_cast<float4*>(&L.xw[slot][s][0]) = make_float4(zero ? 0.f : scale, zero ? 0.f : (float)ud, 0.f, 0.f);
+      L.xs[slot][s] = sum;
+    }
+  }
+}
+
+// Headers of super-block sb into the d*sc table (as decode_kernel's header
+// pass); the min term over the super-block in double, exact per sub-block.
+__device__ __forceinline__ double header_pass_q8(const uint4& h, unsigned sb, unsigned sbl, unsigned t, int wave,
+                                                 int lane, DecodeQ8Lds& L, uint32_t& bad) {
+  if (half_bad(h.x) || half_bad(h.x >> 16)) bad |= kErrScale;
+  if (!q4k_weights_exact(h.x)) bad |= kErrInexact;
+  const float d = half_to_float(h.x & 0xffff), dm = half_to_float(h.x >> 16);
+  const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, mi_lo = h.z & 0x3F3F3F3Fu;
+  const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+  const uint32_t mi_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+  double mins = 0.0;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const float sc = ub(g < 4 ? sc_lo : sc_hi, g & 3), mi = ub(g < 4 ? mi_lo : mi_hi, g & 3);
+    L.dsc[wave][8 * sbl + g][lane] = d * sc;
+    mins += (double)(dm * mi) * L.xs[t][8 * sb + g];
+  }
+  return mins;
+}
+
+// x operands as decode_kernel's (digits 2 and 3 are zero), each column's
+// weight from the staged table.
+__device__ __forceinline__ void x_operands_q8(unsigned t, unsigned sb, int lane, const DecodeQ8Lds& L, i32x4 (&b)[4],
+                                              double (&fx)[2]) {
+  const unsigned kg = (unsigned)lane >> 4, j = (unsigned)lane & 15, js = j >> 2, jd = j & 3;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const unsigned G = (unsigned)m >> 1, hh = (unsigned)m & 1;
+    const i32x4 z = {0, 0, 0, 0};
+    b[m] = js == kg ? *reinterpret_cast<const i32x4*>(&L.xd[t][jd][8 * sb + 4 * G + kg][16 * hh]) : z;
+  }
+#pragma unroll
+  for (int G = 0; G < 2; ++G) fx[G] = (double)L.xw[t][8 * sb + 4 * G + js][jd];
+}
+
+__device__ __forceinline__ void rb_products_q8(const uint4 (&q)[2], const i32x4 (&b)[4], const double (&fx)[2],
+                                               unsigned sbl, unsigned rb, int wave, int lane, const DecodeQ8Lds& L,
+                                               double (&acc)[4]) {
+  const unsigned kg = (unsigned)lane >> 4, js = ((unsigned)lane & 15) >> 2;
+#pragma unroll
+  for (int G = 0; G < 2; ++G) {
+    const uint4 w = q[G];
+    i32x4 c = {0, 0, 0, 0};
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const uint32_t w0 = hh ? w.z : w.x, w1 = hh ? w.w : w.y;
+      const i32x4 a = {(int)nib_lo(w0), (int)nib_hi(w0), (int)nib_lo(w1), (int)nib_hi(w1)};
+      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[2 * G + hh], c, 0, 0, 0);
+    }
+    const float4 ds = *reinterpret_cast<const float4*>(&L.dsc[wave][8 * sbl + 4 * G + js][16 * rb + 4 * kg]);
+    acc[0] = fma((double)c[0], (double)ds.x * fx[G], acc[0]);
+    acc[1] = fma((double)c[1], (double)ds.y * fx[G], acc[1]);
+    acc[2] = fma((double)c[2], (double)ds.z * fx[G], acc[2]);
+    acc[3] = fma((double)c[3], (double)ds.w * fx[G], acc[3]);
+  }
+}
+
+__device__ __forceinline__ double row_sum_d(double v) {
+  v += dpp_d<kQuadXor1>(v);
+  v += dpp_d<kQuadXor2>(v);
+  v += dpp_d<kRowRor4>(v);
+  v += dpp_d<kRowRor8>(v);
+  return v;
+}
+
+// Down projection of round r (neurons 8r..8r+7, quantized h in hs[0..7]) in
+// double: coefficients, then 8 outputs per lane added into y.
+__device__ __forceinline__ void down_round_q8(const DecodeDnBytes& R, const float* hs, int wave, int lane,
+                                              unsigned nsb, DecodeQ8Lds& L, double (&y)[8], uint32_t& bad) {
+  if (lane < 16) L.dh[wave][lane] = R.dh;
+  DecodeQ8Table& T = L.table[wave];
+  {
+    const unsigned ts = (unsigned)lane >> 5, tg = ((unsigned)lane >> 2) & 7, n0 = 2 * ((unsigned)lane & 3);
+    const bool tvalid = 2 * (unsigned)wave + ts < nsb;
+    double Dv[2], Mv[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint4 hdr = L.dh[wave][8 * ts + n0 + q];
+      bool ok;
+      float D, M;
+      hdr_dm(hdr, tg, D, M, ok);
+      if (tvalid && !ok) bad |= kErrScale;
+      if (tvalid && !q4k_weights_exact(hdr.x)) bad |= kErrInexact;
+      const double hv = (double)hs[n0 + q];
+      Dv[q] = (double)D * hv * (double)kFp8Nibble;   // exact: the nibbles below are q * 2^-9
+      Mv[q] = (double)M * hv;
+    }
+    *reinterpret_cast<double2*>(&T.D[ts][tg][n0]) = make_double2(Dv[0], Dv[1]);
+    *reinterpret_cast<double2*>(&T.M[ts][tg][n0]) = make_double2(Mv[0], Mv[1]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  const unsigned sbl = (unsigned)lane >> 5, j = (unsigned)lane & 31, g = j >> 2;
+  if (2 * (unsigned)wave + sbl < nsb) {
+    const double* cd = &T.D[sbl][g][0];
+    const double* cm = &T.M[sbl][g][0];
+    double coef[8], msum = 0.0;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      coef[n] = cd[n];
+      msum += cm[n];
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const uint4 dq = R.dq[half];
+      double s4[4] = {-msum, -msum, -msum, -msum};
+#pragma unroll
+      for (int wd = 0; wd < 4; ++wd) {
+        const uint32_t v = word(dq, wd);
+        const uint32_t lo = nib_lo(v), hi = nib_hi(v);
+        const float2 la = nib_pair<false>(lo), lb = nib_pair<true>(lo), ha = nib_pair<false>(hi), hb = nib_pair<true>(hi);
+        const double ca = coef[2 * wd], cb = coef[2 * wd + 1];
+        s4[0] = fma((double)la.x, ca, s4[0]);
+        s4[1] = fma((double)ha.x, ca, s4[1]);
+        s4[2] = fma((double)la.y, ca, s4[2]);
+        s4[3] = fma((double)ha.y, ca, s4[3]);
+        s4[0] = fma((double)lb.x, cb, s4[0]);
+        s4[1] = fma((double)hb.x, cb, s4[1]);
+        s4[2] = fma((double)lb.y, cb, s4[2]);
+        s4[3] = fma((double)hb.y, cb, s4[3]);
+      }
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) y[4 * half + cc] += s4[cc];
+    }
+  }
+  __builtin_amdgcn_wave_barrier();   // the table and headers are read before the next round writes them
+}
+
+// The unit's partial gate*dot in double, at decode_kernel's positions.
+__device__ __forceinline__ void store_partial_q8(double* wgpart, unsigned stride, unsigned unit, int wave, int lane,
+                                                 float gate, double (&y)[8]) {
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    double* p = wgpart + partial_index(unit, 4 * (128 * wave + 64 * hh + lane), stride);
+    *reinterpret_cast<double2*>(p) = make_double2((double)gate * y[4 * hh], (double)gate * y[4 * hh + 1]);
+    *reinterpret_cast<double2*>(p + 2) = make_double2((double)gate * y[4 * hh + 2], (double)gate * y[4 * hh + 3]);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = 0.0;
+}
+
+// fr_q8_activation of the unit's 32 h, held by lanes 0..31 of every wavefront.
+__device__ __forceinline__ void quantize_h32(float* h, int lane) {
+  const float v = lane < 32 ? h[lane] : 0.f;
+  float m = fabsf(v);
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  const float scale = m / 127.0f, inv = 127.0f / m;
+  float r = isfinite(inv) ? v * inv : (v / m) * 127.0f;
+  r = fminf(fmaxf(rintf(r), -127.f), 127.f);
+  const double back = fmin(fmax((double)r * (double)scale, -(double)FLT_MAX), (double)FLT_MAX);
+  const float hq = scale == 0.f ? 0.f : (float)back;
+  __builtin_amdgcn_wave_barrier();
+  if (lane < 32) h[lane] = hq;
+  __builtin_amdgcn_wave_barrier();
+}
+
+__global__ __launch_bounds__(kDecodeThreads) void decode_q8_kernel(const uint8_t* __restrict__ plan, Scratch S) {
+  const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
+  uint32_t* status = decode_status(S);
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
+  const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden)), nsb = hidden / 256, nsub = hidden / 32;
+  const unsigned np = plan_field(PH, offsetof(PlanHeader, npairs)), tpw = plan_field(PH, offsetof(PlanHeader, tpw));
+  const unsigned burst = plan_field(PH, offsetof(PlanHeader, burst));
+  const uint32_t* upart = reinterpret_cast<const uint32_t*>(plan + plan_field(PH, offsetof(PlanHeader, groups_off)) +
+                                                          burst * sizeof(DecodeToken));
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __shared__ __align__(16) DecodeQ8Lds L;
+  double* wgpart = reinterpret_cast<double*>(S.wgpart);
+  const float* xg = reinterpret_cast<const float*>(plan + plan_field(PH, offsetof(PlanHeader, x_off)));
+  const unsigned xs0 = 32 * ((unsigned)tid >> 2) + 8 * ((unsigned)tid & 3);
+  const bool xin = ((unsigned)tid >> 2) < nsub;
+  const unsigned sb0 = 2 * (unsigned)wave, sb1 = sb0 + 1;
+  const bool has0 = sb0 < nsb, has1 = sb1 < nsb;
+  const unsigned lb0 = min(sb0, nsb - 1), lb1 = min(sb1, nsb - 1);
+  const uint32_t dq_off = 4608 * min(2 * (unsigned)wave + ((unsigned)lane >> 5), nsb - 1) + 32 * ((unsigned)lane & 31);
+  const uint32_t dh_off =
+      4608 * min(2 * (unsigned)wave + (((unsigned)lane & 15) >> 3), nsb - 1) + 4096 + 16 * ((unsigned)lane & 7);
+  uint32_t bad = 0;
+
+  unsigned p = blockIdx.x * tpw;
+  const unsigned pend = min(p + tpw, np);
+  PairBuf B = pair_buf(pairs + p);
+  float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  if (xin) {
+    const float* xt = xg + (size_t)B.token * hidden + xs0;
+    xv[0] = *reinterpret_cast<const float4*>(xt);
+    xv[1] = *reinterpret_cast<const float4*>(xt + 4);
+  }
+  uint4 h0 = load_hdr(B, lb0, lane), h1 = load_hdr(B, lb1, lane);
+  DecodeNib N[4];
+  DecodeDnBytes D[4];
+  load_nib(B, 0, lb0, lb1, lane, N[0]);
+  load_dn(B, 0, dq_off, dh_off, D[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  stage_x_q8(xv, 0, nsub, L, bad);
+  __syncthreads();   // x is in LDS
+
+  double y[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  const unsigned kg = (unsigned)lane >> 4, jcol = (unsigned)lane & 15;
+  // As decode_kernel's unit loop, with every down after round 3 (h is
+  // quantized over all 32 neurons); the next unit's first bytes are
+  // requested during round 3 except its round-0 down bytes, requested after
+  // this unit's downs have read D[0].
+  for (unsigned k = 0;; ++k) {
+    const unsigned q = p + 1, par = k & 1, t = par;
+    const bool more = q < pend;
+    const PairBuf Bn = pair_buf(pairs + (more ? q : p), more);
+    load_nib(B, 1, lb0, lb1, lane, N[1]);
+    load_dn(B, 1, dq_off, dh_off, D[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 b0[4], b1[4];
+    double fx0[2], fx1[2];
+    x_operands_q8(t, sb0, lane, L, b0, fx0);
+    x_operands_q8(t, sb1, lane, L, b1, fx1);
+    {
+      double mp = 0.0;
+      if (has0) mp += header_pass_q8(h0, sb0, 0, t, wave, lane, L, bad);
+      if (has1) mp += header_pass_q8(h1, sb1, 1, t, wave, lane, L, bad);
+      L.minp[par][wave][lane] = mp;
+    }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const DecodeNib& Nc = N[rb];
+      __builtin_amdgcn_sched_barrier(0);
+      if (rb == 1 || rb == 2) {
+        load_nib(B, rb + 1, lb0, lb1, lane, N[rb + 1]);
+        load_dn(B, rb + 1, dq_off, dh_off, D[rb + 1]);
+      } else if (rb == 3) {
+        if (xin) {
+          const float* xt = xg + (size_t)Bn.token * hidden + xs0;
+          xv[0] = *reinterpret_cast<const float4*>(xt);
+          xv[1] = *reinterpret_cast<const float4*>(xt + 4);
+        }
+        h0 = load_hdr(Bn, lb0, lane);
+        h1 = load_hdr(Bn, lb1, lane);
+        load_nib(Bn, 0, lb0, lb1, lane, N[0]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      double acc[4] = {0.0, 0.0, 0.0, 0.0};
+      if (has0) rb_products_q8(Nc.q[0], b0, fx0, 0, rb, wave, lane, L, acc);
+      if (has1) rb_products_q8(Nc.q[1], b1, fx1, 1, rb, wave, lane, L, acc);
+      {
+        const double r0 = row_sum_d(acc[0]), r1 = row_sum_d(acc[1]), r2 = row_sum_d(acc[2]), r3 = row_sum_d(acc[3]);
+        if (jcol == 0) {
+          double* rp = &L.rowp[par][wave][16 * rb + 4 * kg];
+          *reinterpret_cast<double2*>(rp) = make_double2(r0, r1);
+          *reinterpret_cast<double2*>(rp + 2) = make_double2(r2, r3);
+        }
+      }
+      __syncthreads();   // every wavefront's sums of row-block rb are in LDS
+      if (lane < 8) {
+        const unsigned rg = 16 * rb + (unsigned)lane, ru = rg + 8;
+        double a = 0.0, u = 0.0;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+          a += L.rowp[par][w][rg] - L.minp[par][w][rg];
+          u += L.rowp[par][w][ru] - L.minp[par][w][ru];
+        }
+        // backends/ref.c:80-83: a and u narrowed to float, then SiLU in double.
+        uint32_t hb = 0;
+        const float af = narrow_dot(a), uf = narrow_dot(u);
+        const float hv = silu_mul(af, uf, hb);
+        if (wave == 0) bad |= hb;
+        L.h[wave][8 * rb + lane] = hv;
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    quantize_h32(L.h[wave], lane);   // backends/ref.c:85
+#pragma unroll
+    for (int r = 0; r < 4; ++r) down_round_q8(D[r], &L.h[wave][8 * r], wave, lane, nsb, L, y, bad);
+    load_dn(Bn, 0, dq_off, dh_off, D[0]);
+    store_partial_q8(wgpart, S.ustride, plan_read(upart + p), wave, lane, B.gate, y);
+    if (!more) break;
+    stage_x_q8(xv, par ^ 1, nsub, L, bad);
+    __syncthreads();   // the next unit's x is in LDS
+    p = q;
+    B = Bn;
+  }
+  if (bad) flag(status, bad);
+}
+
 // Position p of a decode partial -> output column (see above).
 __device__ __forceinline__ unsigned decode_column(unsigned p) {
   const unsigned w = p >> 9, hh = (p >> 8) & 1, l = (p >> 2) & 63, cc = p & 3;
@@ -1871,6 +2264,8 @@ __device__ __forceinline__ double xor_d(double v, int m) {
   const int hi = __shfl_xor((int)(uint32_t)((uint64_t)__double_as_longlong(v) >> 32), m);
   return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
 }
+// kDouble: the unit partials are doubles (decode_q8_kernel's).
+template <bool kDouble>
 __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
   const DecodeToken tk = reinterpret_cast<const DecodeToken*>(plan + H.groups_off)[blockIdx.y];
@@ -1884,20 +2279,40 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
   const unsigned tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane & 3;
   const unsigned ps = 16 * wave + (lane >> 2);
   const unsigned p0 = kReducePositions * blockIdx.x + 4 * q;
-  float4 r[kReduceDepth];
-#pragma unroll
-  for (unsigned k = 0; k < kReduceDepth; ++k) {
-    const unsigned g = ps + kReduceLanes * k;
-    r[k] = g < tk.count ? *reinterpret_cast<const float4*>(S.wgpart + partial_index(tk.first + g, p0, S.ustride))
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
   double v[4] = {0.0, 0.0, 0.0, 0.0};
+  if constexpr (kDouble) {
+    const double* part = reinterpret_cast<const double*>(S.wgpart);
+    double2 r[kReduceDepth][2];
 #pragma unroll
-  for (unsigned k = 0; k < kReduceDepth; ++k) {
-    v[0] += (double)r[k].x;
-    v[1] += (double)r[k].y;
-    v[2] += (double)r[k].z;
-    v[3] += (double)r[k].w;
+    for (unsigned k = 0; k < kReduceDepth; ++k) {
+      const unsigned g = ps + kReduceLanes * k;
+      const double2 z = make_double2(0.0, 0.0);
+      const double2* src = reinterpret_cast<const double2*>(part + partial_index(tk.first + g, p0, S.ustride));
+      r[k][0] = g < tk.count ? src[0] : z;
+      r[k][1] = g < tk.count ? src[1] : z;
+    }
+#pragma unroll
+    for (unsigned k = 0; k < kReduceDepth; ++k) {
+      v[0] += r[k][0].x;
+      v[1] += r[k][0].y;
+      v[2] += r[k][1].x;
+      v[3] += r[k][1].y;
+    }
+  } else {
+    float4 r[kReduceDepth];
+#pragma unroll
+    for (unsigned k = 0; k < kReduceDepth; ++k) {
+      const unsigned g = ps + kReduceLanes * k;
+      r[k] = g < tk.count ? *reinterpret_cast<const float4*>(S.wgpart + partial_index(tk.first + g, p0, S.ustride))
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (unsigned k = 0; k < kReduceDepth; ++k) {
+      v[0] += (double)r[k].x;
+      v[1] += (double)r[k].y;
+      v[2] += (double)r[k].z;
+      v[3] += (double)r[k].w;
+    }
   }
 #pragma unroll
   for (int m = 4; m < 64; m <<= 1)
@@ -3160,7 +3575,7 @@ struct Engine {
   size_t partial_bytes = 0;
   uint32_t* out = nullptr;        // [2][out_words]
   uint32_t out_words = 0;
-  float* wgpart = nullptr;        // [kMaxPairs][kMaxHidden]
+  float* wgpart = nullptr;        // [kMaxPairs][kMaxHidden] of float, or of double for ref-q8 plans
   uint32_t* bar = nullptr;        // [2]
   float* static_scratch = nullptr;   // device address of `scratch` on this engine's device
   // fr_hip_run's decode-path outputs in mapped pinned host memory (the host
@@ -3351,8 +3766,10 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   // and their summation order do not depend on the rest of the burst.
   // F32 and every pair one of the row-format pairs (shared expert included):
   // decode_rows_kernel, on the same work list.
-  const bool base = r->mode == MODE_F32 && np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
-  bool q4kt = base, rows = base;
+  // ref-q8 requests take the Q4_K-T decode kernel too (decode_q8_kernel).
+  const bool fits = np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
+  const bool base = r->mode == MODE_F32 && fits;
+  bool q4kt = (r->mode == MODE_F32 || r->mode == MODE_Q8) && fits, rows = base;
   // The row-format kernel is instantiated per unit format: every loaded
   // block must have the first one's routed and shared formats.
   int first = 0;
@@ -3361,7 +3778,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   rows = rows && combo != kNoCombo;
   for (int b = 0; rows && b < kBlocks; ++b)
     rows = !E.block[b] || rows_combo(E.lay[b]) == combo;
-  for (uint32_t i = 0; base && i < np; ++i) q4kt = q4kt && pairs[i].gu == TQ4_KM && pairs[i].dn == TQ4_KT;
+  for (uint32_t i = 0; q4kt && i < np; ++i) q4kt = pairs[i].gu == TQ4_KM && pairs[i].dn == TQ4_KT;
   for (int s2 = 0; q4kt && s2 < nu; ++s2) q4kt = ids[s2] != kShared;
   uint32_t nunits = 0;
   for (uint32_t t = 0; t < T; ++t) nunits += (10u + (r->gate[t * 11 + 10] != 0.f ? 1u : 0u)) * (uint32_t)nloaded;
@@ -3448,7 +3865,9 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
 bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, const Scratch& S, hipStream_t stream,
                    hipEvent_t mid) {
   const dim3 g(grid), b(kDecodeThreads);
-  if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, b, 0, stream, dev_plan, S);
+  const bool q8 = H.mode == MODE_Q8;   // decode_q8_kernel (KIND_DECODE only), double partials
+  if (H.kind == KIND_DECODE && q8) hipLaunchKernelGGL(decode_q8_kernel, g, b, 0, stream, dev_plan, S);
+  else if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, b, 0, stream, dev_plan, S);
   else switch (H.pad) {   // (routed formats, shared formats) of the units the request has
     case COMBO_NATIVE:
       hipLaunchKernelGGL((decode_rows_kernel<TQ4_K, TMXFP4, TQ4_K, TMXFP4>), g, b, 0, stream, dev_plan, S);
@@ -3471,8 +3890,12 @@ bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, 
       break;
   }
   if (mid && hipEventRecord(mid, stream) != hipSuccess) return false;
-  hipLaunchKernelGGL(decode_reduce, dim3(kMaxHidden / kReducePositions, H.burst), dim3(kReduceThreads), 0, stream,
-                     dev_plan, S);
+  if (q8)
+    hipLaunchKernelGGL(decode_reduce<true>, dim3(kMaxHidden / kReducePositions, H.burst), dim3(kReduceThreads), 0,
+                       stream, dev_plan, S);
+  else
+    hipLaunchKernelGGL(decode_reduce<false>, dim3(kMaxHidden / kReducePositions, H.burst), dim3(kReduceThreads), 0,
+                       stream, dev_plan, S);
   return true;
 }
 
@@ -3812,7 +4235,7 @@ static int open_engine(int device) {
   CK(hipMalloc(&E.partial, E.partial_bytes));
   E.out_words = 4 + kMaxBurst * kMaxHidden;
   CK(hipMalloc(&E.out, 2 * (size_t)E.out_words * sizeof(uint32_t)));
-  CK(hipMalloc(&E.wgpart, (size_t)kMaxPairs * kMaxHidden * sizeof(float)));
+  CK(hipMalloc(&E.wgpart, (size_t)kMaxPairs * kMaxHidden * sizeof(double)));   // ref-q8 partials are doubles
   CK(hipMalloc(&E.bar, 2 * sizeof(uint32_t)));
   CK(hipMemset(E.bar, 0, 2 * sizeof(uint32_t)));
   // The static scratch array's address on this device (the name is a host
@@ -4060,6 +4483,7 @@ int fr_hip_launch_static(const void* host_plan, const void* device_plan, float* 
   // Plans this variant runs: one token, decode kernels, units within the
   // static scratch.
   if (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS) return FR_HIP_UNSUPPORTED;
+  if (H.mode != MODE_F32) return FR_HIP_UNSUPPORTED;   // the static array holds float partials
   if (H.burst != 1 || H.npairs > kStaticUnits || !H.hidden || H.hidden > (unsigned)kMaxHidden) return FR_HIP_UNSUPPORTED;
   if (!H.grid || H.grid > (unsigned)kDecodeGridMax || H.grid > H.npairs || H.ngroups != H.burst) return FR_HIP_INVALID;
   if (H.kind == KIND_DECODE_ROWS && (H.pad & ~kComboShared) > COMBO_Q4_0) return FR_HIP_INVALID;
@@ -4084,13 +4508,15 @@ int fr_hip_last_output(void* stream, float* y, size_t count, unsigned* status) {
   return fetch_output(stream ? static_cast<hipStream_t>(stream) : E.stream, count, y, status);
 }
 
-int fr_hip_run(const fr_hip_request* req, float* y) {
-  if (!g_open) return FR_HIP_STATE;
-  if (!req || !y) return FR_HIP_INVALID;
-  CK(hipSetDevice(E.device));
+// One run() call's launch; `layer` forces the layer kernel (the plan is
+// built with the decode kernels switched off).
+int run_once(const fr_hip_request* req, float* y, bool layer, unsigned* status_out) {
   size_t used = 0;
   unsigned grid = 0;
+  const bool no_decode = E.no_decode;
+  E.no_decode = no_decode || layer;
   int rc = build_plan(req, E.plan_host, E.plan_cap, &used, &grid);
+  E.no_decode = no_decode;
   if (rc) return rc;
   const PlanHeader& H = *reinterpret_cast<const PlanHeader*>(E.plan_host);
   // The plan (with x) is staged into device memory by a copy kernel, then
@@ -4117,10 +4543,24 @@ int fr_hip_run(const fr_hip_request* req, float* y) {
     if (rc) return rc;
   }
   ++E.sample.runs;
-  if (status & kErrTimeout) return FR_HIP_IO;
-  if (status) return FR_HIP_NUMERIC;
-  // y is written only on success: untouched on failure.
+  *status_out = status;
+  if (status) return FR_HIP_OK;
   memcpy(y, decode ? E.hy_host : reinterpret_cast<const float*>(E.out_host + 4), count * sizeof(float));
+  return FR_HIP_OK;
+}
+
+int fr_hip_run(const fr_hip_request* req, float* y) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!req || !y) return FR_HIP_INVALID;
+  CK(hipSetDevice(E.device));
+  unsigned status = 0;
+  int rc = run_once(req, y, false, &status);
+  // A ref-q8 decode launch that met a weight the reference rounds in float
+  // (and nothing else) is run again on the layer kernel.
+  if (!rc && status == kErrInexact) rc = run_once(req, y, true, &status);
+  if (rc) return rc;
+  if (status & kErrTimeout) return FR_HIP_IO;
+  if (status) return FR_HIP_NUMERIC;   // y is written only on success: untouched on failure
   return FR_HIP_OK;
 }
 

@@ -35,7 +35,9 @@ enum { FR_HIP_FMT_LEGACY = 0, FR_HIP_FMT_NATIVE = 1, FR_HIP_FMT_Q4KT = 2,
  * F64: fp32 activations, exactly decoded weights, fp64 dot products: the
  *      arithmetic of `ref` (backends/ref.c:57-98) up to summation order.
  * Q8:  `ref-q8` (backends/ref.c:125): x and each slice's h quantized by the
- *      reference quantizer (src/q4.c:37-61), bit-exact, with fp64 dots. */
+ *      reference quantizer (src/q4.c:37-61), bit-exact, with fp64 dots (on
+ *      all-Q4_K units: exact integer dots of x's two int8 digits, summed in
+ *      fp64). */
 enum { FR_HIP_MODE_F32 = 0, FR_HIP_MODE_F64 = 1, FR_HIP_MODE_Q8 = 2 };
 
 /* ggml type ids accepted by the debug decoders (src/native.h:8). */
@@ -99,9 +101,13 @@ uint64_t fr_hip_unit_bytes(unsigned hidden, unsigned format);
 int fr_hip_capacity(int device, unsigned hidden, unsigned format, uint64_t reserve, uint64_t *free_bytes,
                     unsigned *blocks);
 
-/* The hot path (run: src/backend.h:63, backends/ref.c:57-98): H2D of x and
- * the launch plan, ONE kernel launch over every (expert, owned slice) pair,
- * D2H of y. y receives burst*hidden floats only on success. Request
+/* The hot path (run: src/backend.h:63, backends/ref.c:57-98): the plan
+ * (routing, gates, x) built on the host and staged into device memory by a
+ * copy kernel, one launch over every (expert, owned slice) pair (the decode
+ * kernel and its fixed-order reduction, or the layer kernel), y and status
+ * back through mapped host memory, one stream wait. A Q8 request whose
+ * all-Q4_K units meet a weight the reference rounds in float is repeated on
+ * the layer kernel. y receives burst*hidden floats only on success. Request
  * validation is the caller's (backends/ref.c:41-56); this checks shapes. */
 int fr_hip_run(const fr_hip_request *req, float *y);
 
@@ -126,7 +132,7 @@ int fr_hip_last_output(void *stream, float *y, size_t count, unsigned *status);
  * Runs plans of one token whose units take the decode kernels
  * (decode_kernel or decode_rows_kernel, then the fixed-order reduction):
  * up to 224 units, i.e. 10 routed experts and the shared one over 20
- * blocks; anything else returns FR_HIP_UNSUPPORTED. Enqueued on `stream`
+ * blocks, in F32 mode; anything else returns FR_HIP_UNSUPPORTED. Enqueued on `stream`
  * (NULL = the library stream); when it completes, *device_status is 0 and
  * device_y holds the hidden outputs, or *device_status has the error bits
  * (FR_NUMERIC cases; device_y is then unspecified). Calls that overlap on

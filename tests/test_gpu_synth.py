@@ -236,3 +236,104 @@ def test_decode_burst_rows_equal_single_token_runs(eng, burst):
     finally:
         for b in range(20):
             eng.release(b)
+
+
+def q8_plan(eng, experts, gates, x):
+    plan, grid = eng.plan(0, experts, gates, x, fa.MODE_Q8)
+    head = np.frombuffer(plan[:80].tobytes(), np.uint32)
+    return int(head[16]), int(head[2]), grid   # kind, mode, grid
+
+
+@pytest.mark.parametrize("hidden", [4096, 2560])
+def test_ref_q8_decode_kernel(eng, hidden):
+    """ref-q8 requests on all-Q4_K units run on decode_q8_kernel: x as two
+    exact int8 digits per value, the matrix-core dots, everything after them
+    in double. A single token and a Zipf burst against the oracle's ref-q8
+    at the Q8 bar (1e-9), against the same requests on layer_kernel's Q8 mode,
+    a bit-identical repeat, and every burst row bit-identical to its token
+    run alone."""
+    lay = oracle.layout(hidden, fa.FMT_Q4KT)
+    seed = 8080 + hidden
+    rng = np.random.default_rng(hidden + 1)
+    for b in range(20):
+        assert eng.synthetic(b, hidden, fa.FMT_Q4KT, 1, seed) == fa.OK
+    try:
+        single = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+        burst = zipf_routes(rng, 4)
+        used = sorted(set(np.concatenate([single.ravel(), burst.ravel()]).tolist()))
+        units = []
+        for b in range(20):
+            u = sparse_unit(lay)
+            for e in used:
+                slice_view(u, lay, 0, e)[:] = oracle.synth_slice(lay, seed, b, 0, e)
+            units.append(u)
+        for experts in (single, burst):
+            T = experts.shape[0]
+            gates = np.zeros((T, 11), np.float32)
+            gates[:, :10] = softmax_gates(rng, T)
+            x = rng.standard_normal((T, hidden)).astype(np.float32)
+            x[0, :64] *= 1e-37   # a group whose scale is subnormal
+            kind, mode, grid = q8_plan(eng, experts, gates, x)
+            assert kind == fa.KIND_DECODE and mode == fa.MODE_Q8, (kind, mode)
+            print(f"ref-q8 decode hidden={hidden} T={T} grid={grid}", flush=True)
+            rc, y = eng.run(0, experts, gates, x, fa.MODE_Q8)
+            assert rc == fa.OK
+            rc, ref = oracle.ref_run(units, fa.FMT_Q4KT, True, oracle_request(0, experts, gates, x))
+            assert rc == 0
+            check_close(ref, y, fa.MODE_Q8, ("ref-q8 decode", hidden, T))
+            rc, again = eng.run(0, experts, gates, x, fa.MODE_Q8)
+            assert rc == fa.OK and np.array_equal(y.view(np.uint32), again.view(np.uint32))
+            eng.route(fa.ROUTE_NO_DECODE)
+            try:
+                print(f"ref-q8 layer kernel hidden={hidden} T={T}", flush=True)
+                rc, yl = eng.run(0, experts, gates, x, fa.MODE_Q8)
+            finally:
+                eng.route(0)
+            assert rc == fa.OK
+            check_close(yl, y, fa.MODE_Q8, ("ref-q8 decode vs layer kernel", hidden, T))
+            for t in range(T if T > 1 else 0):
+                rc, y1 = eng.run(0, experts[t:t + 1], gates[t:t + 1], x[t:t + 1], fa.MODE_Q8)
+                assert rc == fa.OK
+                assert np.array_equal(y1[0].view(np.uint32), y[t].view(np.uint32)), f"token {t} differs alone"
+    finally:
+        for b in range(20):
+            eng.release(b)
+
+
+def test_ref_q8_inexact_weights_run_on_layer_kernel(eng):
+    """A super-block whose d and dmin exponents are far apart has float
+    weights the reference rounds (src/native.c:22); the decode kernel flags
+    it and run() repeats the request on layer_kernel, which decodes every
+    weight as the reference does: the result meets the oracle at the Q8 bar,
+    after two launches."""
+    hidden, seed = 4096, 9090
+    lay = oracle.layout(hidden, fa.FMT_Q4KT)
+    rng = np.random.default_rng(9)
+    for b in range(20):
+        assert eng.synthetic(b, hidden, fa.FMT_Q4KT, 1, seed) == fa.OK
+    try:
+        experts = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+        units = []
+        for b in range(20):
+            u = sparse_unit(lay)
+            for e in experts.ravel():
+                slice_view(u, lay, 0, int(e))[:] = oracle.synth_slice(lay, seed, b, 0, int(e))
+            units.append(u)
+        e0 = int(experts[0, 0])
+        view = slice_view(units[3], lay, 0, e0)
+        view[0:4] = np.frombuffer(np.array([0x3FFF, 0x03FF], np.uint16).tobytes(), np.uint8)   # d 1.999, dmin subnormal
+        assert eng.refresh(3, units[3], 0, e0) == fa.OK
+        gates = np.zeros((1, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, 1)
+        x = rng.standard_normal((1, hidden)).astype(np.float32)
+        before = eng.sample().runs
+        print("ref-q8 inexact header", flush=True)
+        rc, y = eng.run(0, experts, gates, x, fa.MODE_Q8)
+        assert rc == fa.OK
+        assert eng.sample().runs - before == 2
+        rc, ref = oracle.ref_run(units, fa.FMT_Q4KT, True, oracle_request(0, experts, gates, x))
+        assert rc == 0
+        check_close(ref, y, fa.MODE_Q8, "ref-q8 inexact header")
+    finally:
+        for b in range(20):
+            eng.release(b)
