@@ -900,6 +900,11 @@ def main():
             for b in range(SLICES):
                 fa.check(eng.synthetic(b, HIDDEN, f, LAYERS, SEED), "fr_hip_synthetic")
             extra[name] = decode_leg(fa, lib, eng, k, 300, 50, SEED + 8)
+            if k == "native":   # the reference's own unit format in the ref-q8 arithmetic (hip-q8)
+                nq8 = decode_leg(fa, lib, eng, k, 100, 20, SEED + 9, mode=fa.MODE_Q8)
+                nq8["workload"] = ("native units (Q4_K gate/up, MXFP4 down) at hidden 4096 in the ref-q8 "
+                                   "arithmetic (the hip-q8 table), 10 of 512 x 20 slices, 1 token")
+                extra["native_ref_q8"] = nq8
             for b in range(SLICES):
                 eng.release(b)
         m, _ = prefill_leg(fa, lib, eng, 2, 1)

@@ -1907,7 +1907,10 @@ __device__ __forceinline__ bool q4k_weights_exact(uint32_t dm) {
 // fr_q8_activation of x (src/q4.c:37-61) and its two-digit staging: thread
 // t holds values 8(t%4)..+7 of sub-block t/4; the eight threads of a 64-value
 // group agree on its largest magnitude.
-__device__ __forceinline__ void stage_x_q8(const float4 (&v4)[2], unsigned slot, unsigned nsub, DecodeQ8Lds& L,
+// With kLanes the digits go to the row-format kernel's lane-major layout
+// (as stage_x's), each sub-block's weights and exact sum to its tables.
+template <class Lds, bool kLanes = false>
+__device__ __forceinline__ void stage_x_q8(const float4 (&v4)[2], unsigned slot, unsigned nsub, Lds& L,
                                            uint32_t& bad) {
   const unsigned tid = threadIdx.x, s = tid >> 2, q = tid & 3;
   const float v[8] = {v4[0].x, v4[0].y, v4[0].z, v4[0].w, v4[1].x, v4[1].y, v4[1].z, v4[1].w};
@@ -1948,13 +1951,24 @@ __device__ __forceinline__ void stage_x_q8(const float4 (&v4)[2], unsigned slot,
   sum += __shfl_xor(sum, 1);
   sum += __shfl_xor(sum, 2);
   if (s < nsub) {
-    *reinterpret_cast<uint2*>(&L.xd[slot][0][s][8 * q]) = make_uint2(w[0][0], w[0][1]);
-    *reinterpret_cast<uint2*>(&L.xd[slot][1][s][8 * q]) = make_uint2(w[1][0], w[1][1]);
-    *reinterpret_cast<uint2*>(&L.xd[slot][2][s][8 * q]) = make_uint2(0u, 0u);
-    *reinterpret_cast<uint2*>(&L.xd[slot][3][s][8 * q]) = make_uint2(0u, 0u);
-    if (q == 0) {
-      *reinterpret_cast<float4*>(&L.xw[slot][s][0]) = make_float4(zero ? 0.f : scale, zero ? 0.f : (float)ud, 0.f, 0.f);
-      L.xs[slot][s] = sum;
+    const float ws = zero ? 0.f : scale, wu = zero ? 0.f : (float)ud;
+    if constexpr (kLanes) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
+        *reinterpret_cast<uint2*>(&L.xl[d][s & 1][q >> 1][s >> 1][2 * (q & 1)]) = make_uint2(w[d][0], w[d][1]);
+      if (q == 0) {
+        *reinterpret_cast<float2*>(&L.xw[s][0]) = make_float2(ws, wu);
+        L.xsd[s] = sum;
+      }
+    } else {
+      *reinterpret_cast<uint2*>(&L.xd[slot][0][s][8 * q]) = make_uint2(w[0][0], w[0][1]);
+      *reinterpret_cast<uint2*>(&L.xd[slot][1][s][8 * q]) = make_uint2(w[1][0], w[1][1]);
+      *reinterpret_cast<uint2*>(&L.xd[slot][2][s][8 * q]) = make_uint2(0u, 0u);
+      *reinterpret_cast<uint2*>(&L.xd[slot][3][s][8 * q]) = make_uint2(0u, 0u);
+      if (q == 0) {
+        *reinterpret_cast<float4*>(&L.xw[slot][s][0]) = make_float4(ws, wu, 0.f, 0.f);
+        L.xs[slot][s] = sum;
+      }
     }
   }
 }
@@ -2385,6 +2399,8 @@ struct RowsLds {
   int xl[4][2][2][kSubBlocks / 2][4];   // x of the unit's token as int8 digits, lane-major (stage_x)
   float xf[1][kSubBlocks];              // 2^e of each 32-value sub-block
   float xs[1][kSubBlocks];           // fp32 sum of each sub-block
+  float xw[kSubBlocks][2];              // ref-q8: the two digits' weights s, u of each sub-block
+  double xsd[kSubBlocks];               // ref-q8: exact sum of each sub-block's quantized values
   float h[kNeurons];
 };
 
@@ -2693,6 +2709,255 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rows_kernel(const uint8
     if (GA == GB && DA == DB) bad |= rows_unit<GA, DA>(S.wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
     else if (gu == GA && dn == DA) bad |= rows_unit<GA, DA>(S.wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
     else bad |= rows_unit<GB, DB>(S.wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
+  }
+  if (bad) flag(status, bad);
+}
+
+// ------------------------------------------------- row formats, ref-q8
+//
+// decode_rows_kernel's units in the ref-q8 arithmetic (see decode_q8_kernel)
+// for the integer gate/up formats: the reference's native units (Q4_K
+// gate/up, MXFP4 down, Q8_0 shared expert), all-Q8_0 and legacy Q4_0. x is
+// staged as its two exact int8 digits (k, r), the v_dot4 dots per sub-block
+// are exact integers, and everything after them is double: each lane's part
+// of a row, the wave-wide sums, SiLU as ref forms it, h quantized over the
+// unit's 32 neurons, the down (every MXFP4, Q8_0 and Q4_0 weight is exact in
+// float) and the stored partial gate*dot.
+
+struct LaneDigitsQ8 {
+  int q[2][8];   // digits k, r of the sub-block, dword i = values 4i..4i+3
+  float s, u;    // their weights
+  double sum;    // exact sum of the sub-block's quantized values
+};
+
+template <int J>
+__device__ __forceinline__ void load_digits_q8(const RowsLds& L, int c, LaneDigitsQ8& X) {
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int4 v = *reinterpret_cast<const int4*>(&L.xl[d][J][k][c][0]);
+      X.q[d][4 * k] = v.x;
+      X.q[d][4 * k + 1] = v.y;
+      X.q[d][4 * k + 2] = v.z;
+      X.q[d][4 * k + 3] = v.w;
+    }
+  const float2 w = *reinterpret_cast<const float2*>(&L.xw[2 * c + J][0]);
+  X.s = w.x;
+  X.u = w.y;
+  X.sum = L.xsd[2 * c + J];
+}
+
+// The lane's part of a row dot over sub-block 2c + J in double (scales as
+// lane_dot_digits; sc and mn are exact floats).
+template <int type, int J>
+__device__ __forceinline__ double lane_dot_digits_q8(const LaneRaw& r, const float* sc, const float* mn,
+                                                     const LaneDigitsQ8& X) {
+  int acc[2] = {0, 0};
+  if (type == TQ8_0) {
+#pragma unroll
+    for (int p = 2 * J; p < 2 * J + 2; ++p)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int w = (int)word(r.q[p], i);
+#pragma unroll
+        for (int d = 0; d < 2; ++d) acc[d] = __builtin_amdgcn_sdot4(w, X.q[d][4 * (p & 1) + i], acc[d], false);
+      }
+  } else if (type == TQ4_K) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t v = word(r.q[i >> 2], i & 3);
+      const int n = (int)(J ? nib_hi(v) : nib_lo(v));
+#pragma unroll
+      for (int d = 0; d < 2; ++d) acc[d] = __builtin_amdgcn_sdot4(n, X.q[d][i], acc[d], false);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v = word(r.q[J], i);
+      const int lo = (int)nib_lo(v), hi = (int)nib_hi(v);
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        acc[d] = __builtin_amdgcn_sdot4(lo, X.q[d][i], acc[d], false);
+        acc[d] = __builtin_amdgcn_sdot4(hi, X.q[d][4 + i], acc[d], false);
+      }
+    }
+  }
+  const double qx = (double)acc[0] * (double)X.s + (double)acc[1] * (double)X.u;   // sum of q * x, exact terms
+  if (type == TQ4_K) return (double)sc[J] * qx - (double)mn[J] * X.sum;
+  if (type == TQ4_0) return (double)sc[J] * (qx - 8.0 * X.sum);
+  return (double)sc[J] * qx;
+}
+
+// dot[i] = sum_n W[c0+i][n] * h[n] in double for the thread's 8 outputs
+// (backends/ref.c:86-92 with h quantized; the gate is applied at the store).
+template <int DN>
+__device__ __forceinline__ void rows_down_q8(const RowsDown& R, const float* hs, bool valid, double (&y)[8],
+                                             uint32_t& bad) {
+  const float4* h4 = reinterpret_cast<const float4*>(hs);
+  double hsum = 0.0;
+  if (DN == TQ4_0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hsum += ((double)h4[i].x + (double)h4[i].y) + ((double)h4[i].z + (double)h4[i].w);
+  }
+#pragma unroll
+  for (int o = 0; o < 8; ++o) {
+    float sc;
+    if (DN == TMXFP4) {
+      const uint32_t e = (word(R.sc, o >> 2) >> (8 * (o & 3))) & 0xffu;
+      if (valid && mx_blocks_bad(e, R.q0[o], 0u, R.q0[o])) bad |= kErrScale;
+      sc = e8m0(e);
+    } else {
+      const uint32_t hb = (word(R.sc, o >> 1) >> (16 * (o & 1))) & 0xffffu;
+      if (valid && half_bad(hb)) bad |= kErrScale;
+      sc = half_to_float(hb);
+    }
+    double sum = 0.0;
+    if (DN == TQ8_0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t v = word(i < 4 ? R.q0[o] : R.q1[o], i & 3);
+        const float4 h = h4[i];
+        sum = fma((double)(int8_t)v, (double)h.x, sum);
+        sum = fma((double)(int8_t)(v >> 8), (double)h.y, sum);
+        sum = fma((double)(int8_t)(v >> 16), (double)h.z, sum);
+        sum = fma((double)(int8_t)(v >> 24), (double)h.w, sum);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t v = word(R.q0[o], i);
+        const float4 a = h4[i], b = h4[4 + i];
+        if (DN == TMXFP4) {
+          const float2 e0 = fp4_pair(v, 1.0f, 0), e1 = fp4_pair(v, 1.0f, 1), e2 = fp4_pair(v, 1.0f, 2),
+                       e3 = fp4_pair(v, 1.0f, 3);
+          sum = fma((double)e0.x, (double)a.x, sum);
+          sum = fma((double)e1.x, (double)a.y, sum);
+          sum = fma((double)e2.x, (double)a.z, sum);
+          sum = fma((double)e3.x, (double)a.w, sum);
+          sum = fma((double)e0.y, (double)b.x, sum);
+          sum = fma((double)e1.y, (double)b.y, sum);
+          sum = fma((double)e2.y, (double)b.z, sum);
+          sum = fma((double)e3.y, (double)b.w, sum);
+        } else {
+          const uint32_t lo = nib_lo(v), hi = nib_hi(v);
+          sum = fma((double)ub(lo, 0), (double)a.x, sum);
+          sum = fma((double)ub(lo, 1), (double)a.y, sum);
+          sum = fma((double)ub(lo, 2), (double)a.z, sum);
+          sum = fma((double)ub(lo, 3), (double)a.w, sum);
+          sum = fma((double)ub(hi, 0), (double)b.x, sum);
+          sum = fma((double)ub(hi, 1), (double)b.y, sum);
+          sum = fma((double)ub(hi, 2), (double)b.z, sum);
+          sum = fma((double)ub(hi, 3), (double)b.w, sum);
+        }
+      }
+      if (DN == TQ4_0) sum -= 8.0 * hsum;
+    }
+    y[o] = valid ? (double)sc * sum : 0.0;
+  }
+}
+
+template <int GU, int DN>
+__device__ __forceinline__ uint32_t rows_unit_q8(double* wgpart, unsigned ustride, unsigned unit, const PairDesc* P,
+                                                 const float* xg, unsigned hidden, int wave, int lane, RowsLds& L) {
+  static_assert(GU != TMXFP4, "ref-q8 row units dot in integers");
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(P);
+  const uint64_t slice = ((uint64_t)uniform(plan_read(w + 1)) << 32) | uniform(plan_read(w));
+  const uint32_t proj = uniform(plan_read(w + 2));
+  const uint32_t token = uniform(plan_read(w + 3)) >> 24;
+  const float gate = __uint_as_float(uniform(plan_read(reinterpret_cast<const uint32_t*>(P->gate))));
+  const int nch = (int)(hidden / 64);
+  const unsigned nsub = hidden / 32;
+  const bool active = lane < nch;
+  const int c = active ? lane : 0;
+  const unsigned n0 = kRowsWaveNeurons * (unsigned)wave;
+  const unsigned cw = 256 * (2 * (unsigned)wave + ((unsigned)lane >> 5)) + 8 * ((unsigned)lane & 31);
+  const bool dvalid = cw < hidden;
+  const unsigned c0 = dvalid ? cw : 0;
+  const uint8_t* down = reinterpret_cast<const uint8_t*>(slice) + 2 * (size_t)proj;
+  const float* xt = xg + (size_t)token * hidden;
+  uint32_t bad = 0;
+
+  float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  const unsigned tid = threadIdx.x;
+  if ((tid >> 2) < nsub) {
+    const float4* xs = reinterpret_cast<const float4*>(xt + 32 * (tid >> 2) + 8 * (tid & 3));
+    xv[0] = xs[0];
+    xv[1] = xs[1];
+  }
+  LaneRaw raw[2 * kRowsWaveNeurons];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int i = 0; i < kRowsWaveNeurons; ++i) load_gu_row<GU>(slice, proj, k, n0 + i, nch, c, raw[kRowsWaveNeurons * k + i]);
+  RowsDown R;
+  stage_x_q8<RowsLds, true>(xv, 0, nsub, L, bad);
+  __syncthreads();   // x's digits are in LDS
+  double part[2 * kRowsWaveNeurons];
+  LaneDigitsQ8 X;
+  load_digits_q8<0>(L, c, X);
+#pragma unroll
+  for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
+    float sc[2], mn[2];
+    const bool ok = raw_scales<GU>(raw[r], c, sc, mn);
+    if (active && !ok) bad |= kErrScale;
+    if (GU == TQ4_K && active && !q4k_weights_exact(raw[r].h.x)) bad |= kErrInexact;
+    part[r] = lane_dot_digits_q8<GU, 0>(raw[r], sc, mn, X);
+  }
+  rows_load_down<DN>(down, hidden, c0, R);
+  load_digits_q8<1>(L, c, X);
+  double dot[2 * kRowsWaveNeurons];
+#pragma unroll
+  for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
+    float sc[2], mn[2];
+    (void)raw_scales<GU>(raw[r], c, sc, mn);
+    part[r] += lane_dot_digits_q8<GU, 1>(raw[r], sc, mn, X);
+    dot[r] = wave_total(active ? part[r] : 0.0);
+  }
+  if (lane < kRowsWaveNeurons) {
+    double a = dot[0], u = dot[kRowsWaveNeurons];
+#pragma unroll
+    for (int i = 1; i < kRowsWaveNeurons; ++i)
+      if (lane == i) {
+        a = dot[i];
+        u = dot[kRowsWaveNeurons + i];
+      }
+    L.h[n0 + lane] = silu_mul(narrow_dot(a), narrow_dot(u), bad);   // backends/ref.c:80-83
+  }
+  __syncthreads();   // the unit's 32 h are in LDS
+  if (wave == 0) quantize_h32(L.h, lane);   // backends/ref.c:85
+  __syncthreads();   // quantized
+  double y[8];
+  rows_down_q8<DN>(R, L.h, dvalid, y, bad);
+  store_partial_q8(wgpart, ustride, unit, wave, lane, gate, y);
+  __syncthreads();   // h is read before the next unit writes it
+  return bad;
+}
+
+template <int GA, int DA, int GB, int DB>
+__global__ __launch_bounds__(kDecodeThreads) void decode_rows_q8_kernel(const uint8_t* __restrict__ plan, Scratch S) {
+  const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
+  uint32_t* status = decode_status(S);
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
+  const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden));
+  const unsigned np = plan_field(PH, offsetof(PlanHeader, npairs)), tpw = plan_field(PH, offsetof(PlanHeader, tpw));
+  const unsigned burst = plan_field(PH, offsetof(PlanHeader, burst));
+  const uint32_t* upart = reinterpret_cast<const uint32_t*>(plan + plan_field(PH, offsetof(PlanHeader, groups_off)) +
+                                                          burst * sizeof(DecodeToken));
+  const float* xg = reinterpret_cast<const float*>(plan + plan_field(PH, offsetof(PlanHeader, x_off)));
+  double* wgpart = reinterpret_cast<double*>(S.wgpart);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __shared__ __align__(16) RowsLds L;
+  uint32_t bad = 0;
+  const unsigned pend = min((blockIdx.x + 1) * tpw, np);
+  for (unsigned p = blockIdx.x * tpw; p < pend; ++p) {
+    const PairDesc* P = pairs + p;
+    const uint32_t w3 = uniform(plan_read(reinterpret_cast<const uint32_t*>(P) + 3));
+    const uint32_t gu = w3 & 0xffu, dn = (w3 >> 8) & 0xffu;
+    const unsigned unit = plan_read(upart + p);
+    if (GA == GB && DA == DB) bad |= rows_unit_q8<GA, DA>(wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
+    else if (gu == GA && dn == DA) bad |= rows_unit_q8<GA, DA>(wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
+    else bad |= rows_unit_q8<GB, DB>(wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
   }
   if (bad) flag(status, bad);
 }
@@ -3765,17 +4030,20 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   // blocks ascending (the single-token pair order), so that a token's units
   // and their summation order do not depend on the rest of the burst.
   // F32 and every pair one of the row-format pairs (shared expert included):
-  // decode_rows_kernel, on the same work list.
-  // ref-q8 requests take the Q4_K-T decode kernel too (decode_q8_kernel).
+  // decode_rows_kernel, on the same work list. ref-q8 requests take the same
+  // two routes (decode_q8_kernel, decode_rows_q8_kernel), the row formats
+  // only where gate/up dots in integers (not MXFP4).
   const bool fits = np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
-  const bool base = r->mode == MODE_F32 && fits;
-  bool q4kt = (r->mode == MODE_F32 || r->mode == MODE_Q8) && fits, rows = base;
+  const bool f32q8 = (r->mode == MODE_F32 || r->mode == MODE_Q8) && fits;
+  bool q4kt = f32q8, rows = f32q8;
   // The row-format kernel is instantiated per unit format: every loaded
   // block must have the first one's routed and shared formats.
   int first = 0;
   while (!E.block[first]) ++first;
   const uint32_t combo = rows_combo(E.lay[first]);
   rows = rows && combo != kNoCombo;
+  // ref-q8 row units need integer gate/up dots (decode_rows_q8_kernel).
+  if (r->mode == MODE_Q8) rows = rows && (combo == COMBO_NATIVE || combo == COMBO_Q8 || combo == COMBO_Q4_0);
   for (int b = 0; rows && b < kBlocks; ++b)
     rows = !E.block[b] || rows_combo(E.lay[b]) == combo;
   for (uint32_t i = 0; q4kt && i < np; ++i) q4kt = pairs[i].gu == TQ4_KM && pairs[i].dn == TQ4_KT;
@@ -3865,9 +4133,24 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
 bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, const Scratch& S, hipStream_t stream,
                    hipEvent_t mid) {
   const dim3 g(grid), b(kDecodeThreads);
-  const bool q8 = H.mode == MODE_Q8;   // decode_q8_kernel (KIND_DECODE only), double partials
+  const bool q8 = H.mode == MODE_Q8;   // decode_q8_kernel or decode_rows_q8_kernel, double partials
   if (H.kind == KIND_DECODE && q8) hipLaunchKernelGGL(decode_q8_kernel, g, b, 0, stream, dev_plan, S);
   else if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, b, 0, stream, dev_plan, S);
+  else if (q8) switch (H.pad) {   // the integer gate/up formats only (build_plan)
+    case COMBO_NATIVE:
+      hipLaunchKernelGGL((decode_rows_q8_kernel<TQ4_K, TMXFP4, TQ4_K, TMXFP4>), g, b, 0, stream, dev_plan, S);
+      break;
+    case COMBO_NATIVE | kComboShared:
+      hipLaunchKernelGGL((decode_rows_q8_kernel<TQ4_K, TMXFP4, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
+      break;
+    case COMBO_Q8:
+    case COMBO_Q8 | kComboShared:
+      hipLaunchKernelGGL((decode_rows_q8_kernel<TQ8_0, TQ8_0, TQ8_0, TQ8_0>), g, b, 0, stream, dev_plan, S);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_rows_q8_kernel<TQ4_0, TQ4_0, TQ4_0, TQ4_0>), g, b, 0, stream, dev_plan, S);
+      break;
+  }
   else switch (H.pad) {   // (routed formats, shared formats) of the units the request has
     case COMBO_NATIVE:
       hipLaunchKernelGGL((decode_rows_kernel<TQ4_K, TMXFP4, TQ4_K, TMXFP4>), g, b, 0, stream, dev_plan, S);

@@ -139,3 +139,77 @@ def test_rows_unit_list_overflow_falls_back_to_layer_kernel(eng):
     finally:
         for b in range(20):
             eng.release(b)
+
+
+def q8_plan(eng, experts, gates, x):
+    plan, grid = eng.plan(0, experts, gates, x, fa.MODE_Q8)
+    head = np.frombuffer(plan[:80].tobytes(), np.uint32)
+    return int(head[16]), int(head[2]), grid   # kind, mode, grid
+
+
+@pytest.mark.parametrize("fmt,hidden,burst,shared_tokens", [
+    (fa.FMT_NATIVE, 4096, 1, ()), (fa.FMT_NATIVE, 2560, 1, (0,)), (fa.FMT_Q8, 4096, 1, (0,)),
+    (fa.FMT_NATIVE, 4096, 4, (1, 3)), (fa.FMT_Q8, 2560, 3, ())])
+def test_rows_ref_q8(eng, fmt, hidden, burst, shared_tokens):
+    """ref-q8 requests on row-format units with integer gate/up dots run on
+    decode_rows_q8_kernel (x as two exact int8 digits, double after the
+    integer dots): against the oracle's ref-q8 at the Q8 bar (1e-9), against
+    layer_kernel's Q8 mode, bit for bit run to run, and every burst row bit
+    for bit against its token run alone."""
+    lay = oracle.layout(hidden, fmt)
+    seed = 6100 + 10 * fmt + hidden + burst
+    rng = np.random.default_rng(seed)
+    for b in range(20):
+        assert eng.synthetic(b, hidden, fmt, 1, seed) == fa.OK
+    try:
+        experts = zipf_routes(rng, burst) if burst > 1 else rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+        gates = np.zeros((burst, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, burst)
+        for t in shared_tokens:
+            gates[t, 10] = 0.5
+        x = rng.standard_normal((burst, hidden)).astype(np.float32)
+        kind, mode, grid = q8_plan(eng, experts, gates, x)
+        assert kind == KIND_DECODE_ROWS and mode == fa.MODE_Q8, (kind, mode)
+        print(f"rows ref-q8 fmt={fmt} hidden={hidden} burst={burst} shared={shared_tokens} grid={grid}", flush=True)
+        rc, y = eng.run(0, experts, gates, x, fa.MODE_Q8)
+        assert rc == fa.OK
+        rc, ref = oracle.ref_run(host_units(lay, seed, experts, bool(shared_tokens)), fmt, True,
+                                 oracle_request(0, experts, gates, x))
+        assert rc == 0
+        check_close(ref, y, fa.MODE_Q8, ("rows ref-q8", fmt, hidden, burst))
+        rc, again = eng.run(0, experts, gates, x, fa.MODE_Q8)
+        assert rc == fa.OK and np.array_equal(y.view(np.uint32), again.view(np.uint32))
+        eng.route(fa.ROUTE_NO_DECODE)
+        try:
+            print(f"rows ref-q8 on the layer kernel fmt={fmt}", flush=True)
+            rc, y_lay = eng.run(0, experts, gates, x, fa.MODE_Q8)
+        finally:
+            eng.route(0)
+        assert rc == fa.OK
+        check_close(y_lay, y, fa.MODE_Q8, ("rows ref-q8 vs layer", fmt, hidden, burst))
+        for t in range(burst if burst > 1 else 0):
+            rc, y1 = eng.run(0, experts[t:t + 1], gates[t:t + 1], x[t:t + 1], fa.MODE_Q8)
+            assert rc == fa.OK
+            assert np.array_equal(y1[0].view(np.uint32), y[t].view(np.uint32)), f"token {t} differs alone"
+    finally:
+        for b in range(20):
+            eng.release(b)
+
+
+def test_rows_ref_q8_mxfp4_takes_the_layer_kernel(eng):
+    """MXFP4 gate/up rows dot in fp32: ref-q8 requests over them stay on the
+    layer kernel's fp64 Q8 mode."""
+    hidden, fmt, seed = 4096, fa.FMT_MXFP4, 61
+    for b in range(2):
+        assert eng.synthetic(b, hidden, fmt, 1, seed) == fa.OK
+    try:
+        rng = np.random.default_rng(2)
+        experts = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+        gates = np.zeros((1, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, 1)
+        x = rng.standard_normal((1, hidden)).astype(np.float32)
+        kind, mode, _ = q8_plan(eng, experts, gates, x)
+        assert kind == 0 and mode == fa.MODE_Q8
+    finally:
+        for b in range(2):
+            eng.release(b)
