@@ -118,8 +118,8 @@ def grid_kernels(lib, plan):
     """The kernels one launch of this plan runs (plan header fields `kind` and `mode`)."""
     head = np.frombuffer(plan[:80].tobytes(), np.uint32)
     kind, mode = int(head[16]), int(head[2])
-    if kind == 1 and mode == 2:
-        return "decode_q8_kernel + decode_reduce"
+    if mode == 2 and kind in (1, 2):
+        return ("decode_q8_kernel" if kind == 1 else "decode_rows_q8_kernel") + " + decode_reduce"
     return {1: "decode_kernel + decode_reduce", 2: "decode_rows_kernel + decode_reduce"}.get(kind, "layer_kernel")
 
 
