@@ -66,10 +66,15 @@ def test_native_fixture_deterministic_and_burst_invariant(eng, native2560):
     assert same == 8
 
 
-def test_native_error_paths(eng, native2560):
+@pytest.mark.parametrize("mode", [fa.MODE_F32, fa.MODE_Q8])
+def test_native_error_paths(eng, native2560, mode):
+    """x at FLT_MAX, a non-finite Q4_K d, an E8M0 255 down scale and a
+    non-finite shared-expert Q8_0 scale each give FR_NUMERIC (the F32 and
+    the ref-q8 row-format decode kernels), and the restored units run."""
     lay, data, gates, x, blocks = native2560
     experts = np.arange(10).reshape(1, 10)
-    rc, y = eng.run(47, experts, gates[:1], np.full((1, 2560), np.finfo(np.float32).max, np.float32))
+    print(f"native error paths mode={mode}", flush=True)
+    rc, y = eng.run(47, experts, gates[:1], np.full((1, 2560), np.finfo(np.float32).max, np.float32), mode)
     assert rc == fa.NUMERIC
     for off, val in [(oracle.slice_offset(lay, 47, 0) + 1, 0x7C),
                      (oracle.slice_offset(lay, 47, 0) + 2 * lay.proj, 255),
@@ -78,9 +83,9 @@ def test_native_error_paths(eng, native2560):
         data[off] = val
         layer, expert = 47, (512 if off >= oracle.slice_offset(lay, 47, 512) else 0)
         assert eng.refresh(19, data, layer, expert) == fa.OK
-        rc, _ = eng.run(47, experts, gates[:1], x[:1])
+        rc, _ = eng.run(47, experts, gates[:1], x[:1], mode)
         assert rc == fa.NUMERIC, off
         data[off] = saved
         assert eng.refresh(19, data, layer, expert) == fa.OK
-    rc, _ = eng.run(47, experts, gates[:1], x[:1])
+    rc, _ = eng.run(47, experts, gates[:1], x[:1], mode)
     assert rc == fa.OK

@@ -337,3 +337,39 @@ def test_ref_q8_inexact_weights_run_on_layer_kernel(eng):
     finally:
         for b in range(20):
             eng.release(b)
+
+
+def test_ref_q8_decode_error_paths(eng):
+    """decode_q8_kernel: a non-finite gate/up d, a non-finite down d and x at
+    FLT_MAX give FR_NUMERIC with y untouched; the restored slice runs."""
+    hidden, seed = 4096, 3131
+    lay = oracle.layout(hidden, fa.FMT_Q4KT)
+    rng = np.random.default_rng(31)
+    for b in range(2):
+        assert eng.synthetic(b, hidden, fa.FMT_Q4KT, 1, seed) == fa.OK
+    try:
+        experts = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+        gates = np.zeros((1, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, 1)
+        x = rng.standard_normal((1, hidden)).astype(np.float32)
+        e0 = int(experts[0, 3])
+        unit = sparse_unit(lay)
+        view = slice_view(unit, lay, 0, e0)
+        view[:] = oracle.synth_slice(lay, seed, 1, 0, e0)
+        good = view.copy()
+        print("ref-q8 decode error paths", flush=True)
+        rc, y = eng.run(0, experts, gates, np.full((1, hidden), np.finfo(np.float32).max, np.float32), fa.MODE_Q8)
+        assert rc == fa.NUMERIC
+        for off in (1, 2 * lay.proj + 1):   # high byte of a gate row's d, of a down row's d: 0x7C -> inf
+            view[:] = good
+            view[off] = 0x7C
+            assert eng.refresh(1, unit, 0, e0) == fa.OK
+            rc, y = eng.run(0, experts, gates, x, fa.MODE_Q8)
+            assert rc == fa.NUMERIC and not y.any(), off
+        view[:] = good
+        assert eng.refresh(1, unit, 0, e0) == fa.OK
+        rc, y = eng.run(0, experts, gates, x, fa.MODE_Q8)
+        assert rc == fa.OK and np.isfinite(y).all()
+    finally:
+        for b in range(2):
+            eng.release(b)
