@@ -3960,80 +3960,26 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
       masks[s] |= (uint8_t)(1u << t);
       gates[s][t] = g;
     }
-  // Pairs, partitioned by down format so each group is homogeneous.
+  // Route first, from the loaded blocks' layouts, so that a decode plan is
+  // built alone (x copied once). F32, routed experts only (no shared gate),
+  // every pair Q4_K with the transposed down: the decode kernel. Its work
+  // list is rebuilt as (token, pair) units, token-major, each token's experts
+  // in request order and blocks ascending (the single-token pair order), so
+  // that a token's units and their summation order do not depend on the
+  // rest of the burst. F32 and every pair one of the row-format pairs (shared
+  // expert included): decode_rows_kernel, on the same work list. ref-q8
+  // requests take the same two routes (decode_q8_kernel,
+  // decode_rows_q8_kernel), the row formats only where gate/up dots in
+  // integers (not MXFP4).
   PlanHeader* H = reinterpret_cast<PlanHeader*>(out);
   memset(H, 0, sizeof(*H));
-  PairDesc* pairs = reinterpret_cast<PairDesc*>(out + sizeof(PlanHeader));
-  uint32_t np = 0;
-  uint8_t classes[4] = {TQ4_KT, TMXFP4, TQ4_0, TQ8_0};
-  GroupDesc groups[kMaxPairs];
-  uint32_t ng = 0, gmax = 1;
-  uint64_t wbytes = 0;
-  for (uint8_t cls : classes) {
-    uint32_t start = np;
-    for (int s = 0; s < nu; ++s)
-      for (int b = 0; b < kBlocks; ++b) {
-        if (!E.block[b]) continue;
-        const Layout& l = E.lay[b];
-        bool shared = ids[s] == kShared;
-        uint8_t dn = (uint8_t)(shared ? l.shared_dn : l.dn);
-        if (dn != cls) continue;
-        PairDesc& P = pairs[np++];
-        memset(&P, 0, sizeof(P));
-        P.slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer + (uint64_t)ids[s] * l.slice);
-        P.proj = (uint32_t)(shared ? l.shared_proj : l.proj);
-        P.gu = (uint8_t)(shared ? l.shared_gu : l.gu);
-        P.dn = dn;
-        P.tmask = masks[s];
-        for (uint32_t t = 0; t < T; ++t) P.gate[t] = gates[s][t];
-        wbytes += shared ? l.shared_slice : l.slice;
-      }
-    uint32_t gp = group_pairs(cls);
-    for (uint32_t f = start; f < np; f += gp) {
-      GroupDesc& G = groups[ng++];
-      memset(&G, 0, sizeof(G));
-      G.first = (uint16_t)f;
-      G.count = (uint16_t)(np - f < gp ? np - f : gp);
-      G.dn = cls;
-      if (G.count > gmax) gmax = G.count;
-    }
-  }
-  const uint32_t nn = kTaskNeurons;
-  H->hidden = hidden;
-  H->burst = T;
-  H->mode = r->mode;
-  H->npairs = np;
-  H->ngroups = ng;
-  H->nranges = hidden / kCols;
-  H->nn = nn;
-  H->ntA = np * (kNeurons / nn);
-  H->ntB = ng * H->nranges;
-  // Phase A stages activations in tiles of 1 (single token) or 4 tokens.
-  const uint32_t tchunk = T == 1 ? 1 : (T < 4 ? T : 4);
-  H->tchunk = tchunk;
-  H->gmax = gmax;
   H->pairs_off = sizeof(PlanHeader);
-  H->groups_off = H->pairs_off + np * sizeof(PairDesc);
-  memcpy(out + H->groups_off, groups, ng * sizeof(GroupDesc));
-  H->x_off = (uint32_t)((H->groups_off + ng * sizeof(GroupDesc) + 255) & ~255u);
-  memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
-  H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
-  size_t ldsA = T == 1 ? 0 : (size_t)tchunk * hidden * sizeof(float);
-  size_t wstride = 2 * 8 * kTabStride + T * 8 * kTabStride;
-  size_t ldsB = (size_t)gmax * T * kNeurons * sizeof(float) + kWaves * wstride * sizeof(float) +
-                kWaves * kCols * sizeof(double);
-  H->lds = (uint32_t)(ldsA > ldsB ? ldsA : ldsB);
-  if (H->lds > (uint32_t)kLdsLimit) return FR_HIP_UNSUPPORTED;
-  // F32, routed experts only (no shared gate), every pair Q4_K with the
-  // transposed down: the decode kernel. Its work list is rebuilt as (token,
-  // pair) units, token-major, each token's experts in request order and
-  // blocks ascending (the single-token pair order), so that a token's units
-  // and their summation order do not depend on the rest of the burst.
-  // F32 and every pair one of the row-format pairs (shared expert included):
-  // decode_rows_kernel, on the same work list. ref-q8 requests take the same
-  // two routes (decode_q8_kernel, decode_rows_q8_kernel), the row formats
-  // only where gate/up dots in integers (not MXFP4).
-  const bool fits = np > 0 && hidden <= (uint32_t)kMaxHidden && E.cus > 0;
+  PairDesc* pairs = reinterpret_cast<PairDesc*>(out + sizeof(PlanHeader));
+  uint64_t wbytes = 0;   // the request's weight bytes: each (expert, block) slice once
+  for (int s2 = 0; s2 < nu; ++s2)
+    for (int b = 0; b < kBlocks; ++b)
+      if (E.block[b]) wbytes += ids[s2] == kShared ? E.lay[b].shared_slice : E.lay[b].slice;
+  const bool fits = hidden <= (uint32_t)kMaxHidden && E.cus > 0;
   const bool f32q8 = (r->mode == MODE_F32 || r->mode == MODE_Q8) && fits;
   bool q4kt = f32q8, rows = f32q8;
   // The row-format kernel is instantiated per unit format: every loaded
@@ -4046,11 +3992,13 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   if (r->mode == MODE_Q8) rows = rows && (combo == COMBO_NATIVE || combo == COMBO_Q8 || combo == COMBO_Q4_0);
   for (int b = 0; rows && b < kBlocks; ++b)
     rows = !E.block[b] || rows_combo(E.lay[b]) == combo;
-  for (uint32_t i = 0; q4kt && i < np; ++i) q4kt = pairs[i].gu == TQ4_KM && pairs[i].dn == TQ4_KT;
+  for (int b = 0; q4kt && b < kBlocks; ++b)
+    q4kt = !E.block[b] || (E.lay[b].gu == TQ4_KM && E.lay[b].dn == TQ4_KT);
   for (int s2 = 0; q4kt && s2 < nu; ++s2) q4kt = ids[s2] != kShared;
   uint32_t nunits = 0;
   for (uint32_t t = 0; t < T; ++t) nunits += (10u + (r->gate[t * 11 + 10] != 0.f ? 1u : 0u)) * (uint32_t)nloaded;
   const bool decode = (q4kt || rows) && nunits <= (uint32_t)kMaxPairs;
+  uint32_t np = 0;
   if (decode && !E.no_decode) {
     // Units are (token, pair). Their partials are numbered token-major in the
     // reference's order (token, routed expert in request order, ascending
@@ -4067,26 +4015,37 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
                                                   T * sizeof(DecodeToken));
     uint32_t w = 0;
     for (int s2 = 0; s2 < nu; ++s2) {
+      const bool shared = ids[s2] == kShared;
+      // The expert's place in each of its tokens' lists (the shared expert
+      // follows the 10 routed), found once for all blocks.
+      uint8_t place[kMaxBurst] = {};
+      for (uint32_t t = 0; t < T; ++t) {
+        if (!(masks[s2] >> t & 1u)) continue;
+        int e = 10;
+        if (!shared) {
+          e = 0;
+          while (r->expert[t * 10 + e] != ids[s2]) ++e;
+        }
+        place[t] = (uint8_t)e;
+      }
       int brank = 0;
       for (int b = 0; b < kBlocks; ++b) {
         if (!E.block[b]) continue;
         const Layout& l = E.lay[b];
-        const bool shared = ids[s2] == kShared;
+        const uint64_t slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer +
+                                                     (uint64_t)ids[s2] * l.slice);
         for (uint32_t t = 0; t < T; ++t) {
           if (!(masks[s2] >> t & 1u)) continue;
-          int e = 0;   // the expert's place in the token's list; the shared expert follows the 10 routed
-          if (shared) e = 10;
-          else
-            while (r->expert[t * 10 + e] != ids[s2]) ++e;
+          const int e = place[t];
           PairDesc& U = pairs[w];
-          memset(&U, 0, sizeof(U));
-          U.slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer + (uint64_t)ids[s2] * l.slice);
+          U.slice = slice;
           U.proj = (uint32_t)(shared ? l.shared_proj : l.proj);
           U.gu = (uint8_t)(shared ? l.shared_gu : l.gu);
           U.dn = (uint8_t)(shared ? l.shared_dn : l.dn);
           U.tmask = (uint8_t)(1u << t);
           U.pad = (uint8_t)t;
           U.gate[0] = r->gate[t * 11 + e];
+          for (int k = 1; k < kMaxBurst; ++k) U.gate[k] = 0.f;
           upart[w++] = tok[t].first + (uint32_t)e * (uint32_t)nloaded + (uint32_t)brank;
         }
         ++brank;
@@ -4094,6 +4053,9 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     }
     if (w != nunits) return FR_HIP_INVALID;   // every token routes 10 distinct experts
     if (w > (uint32_t)kMaxPairs) return FR_HIP_INVALID;
+    H->hidden = hidden;
+    H->burst = T;
+    H->mode = r->mode;
     H->npairs = nunits;
     H->ngroups = T;
     H->groups_off = H->pairs_off + nunits * sizeof(PairDesc);
@@ -4113,6 +4075,63 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     H->grid = (nunits + ppw - 1) / ppw;
     np = nunits;
   } else {
+    // Pairs, partitioned by down format so each group is homogeneous.
+    uint8_t classes[4] = {TQ4_KT, TMXFP4, TQ4_0, TQ8_0};
+    GroupDesc groups[kMaxPairs];
+    uint32_t ng = 0, gmax = 1;
+    for (uint8_t cls : classes) {
+      uint32_t start = np;
+      for (int s = 0; s < nu; ++s)
+        for (int b = 0; b < kBlocks; ++b) {
+          if (!E.block[b]) continue;
+          const Layout& l = E.lay[b];
+          bool shared = ids[s] == kShared;
+          uint8_t dn = (uint8_t)(shared ? l.shared_dn : l.dn);
+          if (dn != cls) continue;
+          PairDesc& P = pairs[np++];
+          memset(&P, 0, sizeof(P));
+          P.slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer + (uint64_t)ids[s] * l.slice);
+          P.proj = (uint32_t)(shared ? l.shared_proj : l.proj);
+          P.gu = (uint8_t)(shared ? l.shared_gu : l.gu);
+          P.dn = dn;
+          P.tmask = masks[s];
+          for (uint32_t t = 0; t < T; ++t) P.gate[t] = gates[s][t];
+        }
+      uint32_t gp = group_pairs(cls);
+      for (uint32_t f = start; f < np; f += gp) {
+        GroupDesc& G = groups[ng++];
+        memset(&G, 0, sizeof(G));
+        G.first = (uint16_t)f;
+        G.count = (uint16_t)(np - f < gp ? np - f : gp);
+        G.dn = cls;
+        if (G.count > gmax) gmax = G.count;
+      }
+    }
+    const uint32_t nn = kTaskNeurons;
+    H->hidden = hidden;
+    H->burst = T;
+    H->mode = r->mode;
+    H->npairs = np;
+    H->ngroups = ng;
+    H->nranges = hidden / kCols;
+    H->nn = nn;
+    H->ntA = np * (kNeurons / nn);
+    H->ntB = ng * H->nranges;
+    // Phase A stages activations in tiles of 1 (single token) or 4 tokens.
+    const uint32_t tchunk = T == 1 ? 1 : (T < 4 ? T : 4);
+    H->tchunk = tchunk;
+    H->gmax = gmax;
+    H->groups_off = H->pairs_off + np * sizeof(PairDesc);
+    memcpy(out + H->groups_off, groups, ng * sizeof(GroupDesc));
+    H->x_off = (uint32_t)((H->groups_off + ng * sizeof(GroupDesc) + 255) & ~255u);
+    memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
+    H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
+    size_t ldsA = T == 1 ? 0 : (size_t)tchunk * hidden * sizeof(float);
+    size_t wstride = 2 * 8 * kTabStride + T * 8 * kTabStride;
+    size_t ldsB = (size_t)gmax * T * kNeurons * sizeof(float) + kWaves * wstride * sizeof(float) +
+                  kWaves * kCols * sizeof(double);
+    H->lds = (uint32_t)(ldsA > ldsB ? ldsA : ldsB);
+    if (H->lds > (uint32_t)kLdsLimit) return FR_HIP_UNSUPPORTED;
     H->kind = KIND_LAYER;
     H->tpw = 0;
     H->grid = H->ntA + H->ntB;
@@ -4751,8 +4770,9 @@ int fr_hip_launch(const void* host_plan, const void* device_plan, void* stream) 
   if (!g_open) return FR_HIP_STATE;
   if (!host_plan || !device_plan) return FR_HIP_INVALID;
   const PlanHeader& H = *static_cast<const PlanHeader*>(host_plan);
-  if (!H.burst || H.burst > (unsigned)kMaxBurst || !H.ntA || !H.ntB) return FR_HIP_INVALID;
-  if (H.kind == KIND_LAYER ? H.grid != H.ntA + H.ntB : ((H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS) || !H.grid))
+  if (!H.burst || H.burst > (unsigned)kMaxBurst) return FR_HIP_INVALID;
+  if (H.kind == KIND_LAYER ? !H.ntA || !H.ntB || H.grid != H.ntA + H.ntB
+                           : (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS) || !H.grid)
     return FR_HIP_INVALID;
   return launch(static_cast<const uint8_t*>(device_plan), H, H.grid,
                 stream ? static_cast<hipStream_t>(stream) : E.stream);
