@@ -2264,7 +2264,7 @@ __device__ __forceinline__ unsigned decode_column(unsigned p) {
 // blockIdx.y, units [first, first + count) of the plan's token table), in
 // fp64 and a fixed order: lane (q, ps) of wavefront w, ps = 16w + l/4, adds
 // units ps, ps+64, ps+128, ps+192 of positions 16*blockIdx.x + 4q..4q+3 in
-// that order (its four loads are in flight together), a butterfly over the
+// that order (its four loads in flight together), a butterfly over the
 // 16 ps of each wavefront combines them, and wavefront 0 adds the four
 // wavefronts' sums in order. Narrowing follows the reference's overflow rule
 // (backends/ref.c:95); the status word is decode_kernel's. A token's result
@@ -2293,39 +2293,43 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
   const unsigned tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane & 3;
   const unsigned ps = 16 * wave + (lane >> 2);
   const unsigned p0 = kReducePositions * blockIdx.x + 4 * q;
+  // Every load is issued unconditionally (units past the token's last read
+  // its last unit again, and their values are then dropped), so that the
+  // four are in flight together: a load under a lane condition is waited for
+  // before the next one is issued.
   double v[4] = {0.0, 0.0, 0.0, 0.0};
   if constexpr (kDouble) {
     const double* part = reinterpret_cast<const double*>(S.wgpart);
     double2 r[kReduceDepth][2];
 #pragma unroll
     for (unsigned k = 0; k < kReduceDepth; ++k) {
-      const unsigned g = ps + kReduceLanes * k;
-      const double2 z = make_double2(0.0, 0.0);
+      const unsigned g = min(ps + kReduceLanes * k, tk.count - 1);
       const double2* src = reinterpret_cast<const double2*>(part + partial_index(tk.first + g, p0, S.ustride));
-      r[k][0] = g < tk.count ? src[0] : z;
-      r[k][1] = g < tk.count ? src[1] : z;
+      r[k][0] = src[0];
+      r[k][1] = src[1];
     }
 #pragma unroll
     for (unsigned k = 0; k < kReduceDepth; ++k) {
-      v[0] += r[k][0].x;
-      v[1] += r[k][0].y;
-      v[2] += r[k][1].x;
-      v[3] += r[k][1].y;
+      const bool in = ps + kReduceLanes * k < tk.count;
+      v[0] += in ? r[k][0].x : 0.0;
+      v[1] += in ? r[k][0].y : 0.0;
+      v[2] += in ? r[k][1].x : 0.0;
+      v[3] += in ? r[k][1].y : 0.0;
     }
   } else {
     float4 r[kReduceDepth];
 #pragma unroll
     for (unsigned k = 0; k < kReduceDepth; ++k) {
-      const unsigned g = ps + kReduceLanes * k;
-      r[k] = g < tk.count ? *reinterpret_cast<const float4*>(S.wgpart + partial_index(tk.first + g, p0, S.ustride))
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
+      const unsigned g = min(ps + kReduceLanes * k, tk.count - 1);
+      r[k] = *reinterpret_cast<const float4*>(S.wgpart + partial_index(tk.first + g, p0, S.ustride));
     }
 #pragma unroll
     for (unsigned k = 0; k < kReduceDepth; ++k) {
-      v[0] += (double)r[k].x;
-      v[1] += (double)r[k].y;
-      v[2] += (double)r[k].z;
-      v[3] += (double)r[k].w;
+      const bool in = ps + kReduceLanes * k < tk.count;
+      v[0] += in ? (double)r[k].x : 0.0;
+      v[1] += in ? (double)r[k].y : 0.0;
+      v[2] += in ? (double)r[k].z : 0.0;
+      v[3] += in ? (double)r[k].w : 0.0;
     }
   }
 #pragma unroll
