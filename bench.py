@@ -120,7 +120,8 @@ def grid_kernels(lib, plan):
     kind, mode = int(head[16]), int(head[2])
     if mode == 2 and kind in (1, 2):
         return ("decode_q8_kernel" if kind == 1 else "decode_rows_q8_kernel") + " + decode_reduce"
-    return {1: "decode_kernel + decode_reduce", 2: "decode_rows_kernel + decode_reduce"}.get(kind, "layer_kernel")
+    return {1: "decode_kernel + decode_reduce", 2: "decode_rows_kernel + decode_reduce",
+            3: "decode_split_kernel + decode_reduce"}.get(kind, "layer_kernel")
 
 
 def plan_slices(plan):

@@ -18,7 +18,7 @@ Q4_0, Q8_0, Q4_K, MXFP4 = 2, 8, 12, 39
 MAX_BURST, MAX_HIDDEN, BLOCKS = 8, 4096, 20
 ROUTE_NO_DECODE = 2
 # Plan kinds (the kernel a plan runs), plan header word 16.
-KIND_LAYER, KIND_DECODE, KIND_DECODE_ROWS = 0, 1, 2
+KIND_LAYER, KIND_DECODE, KIND_DECODE_ROWS, KIND_DECODE_SPLIT = 0, 1, 2, 3
 
 LIB_PATH = _build.HIP_LIB
 

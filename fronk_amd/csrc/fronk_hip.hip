@@ -93,7 +93,10 @@ static_assert(sizeof(PlanHeader) == 80, "header layout");
 // kernel for all-Q4_K units with the transposed down (F32, routed experts
 // only), whose work list is (token, pair) units, token-major, each with its
 // own partial.
-enum : uint32_t { KIND_LAYER = 0, KIND_DECODE = 1, KIND_DECODE_ROWS = 2 };
+enum : uint32_t { KIND_LAYER = 0, KIND_DECODE = 1, KIND_DECODE_ROWS = 2, KIND_DECODE_SPLIT = 3 };
+// A decode plan's items (work-list entries with a partial each): one per
+// unit, or `split` (2 or 4) per unit for KIND_DECODE_SPLIT.
+constexpr int kMaxDecodeItems = 2048;
 // A decode plan's token table (at groups_off): token t's units.
 struct DecodeToken {
   uint32_t first, count;
@@ -1843,6 +1846,113 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
     __syncthreads();   // the next unit's x is in LDS
     p = q;
     B = Bn;
+  }
+  if (bad) flag(status, bad);
+}
+
+// ------------------------------------------------- decode kernel, split units
+//
+// decode_kernel gives each unit to one workgroup, whose CU streams the
+// unit's 221 KB: when a node owns few blocks a request has few units, most
+// CUs idle, and a call takes as long as a full layer share. Here each unit
+// is split into `split` items of 4/split row-blocks (split 4 for at most 5
+// owned blocks, 2 for at most 11): an item computes its row-blocks' gate/up
+// and h as decode_kernel's rounds do, then the down of those neurons over
+// every output into a partial of its own, and decode_reduce sums a token's
+// items in (unit, item) order. The split depends on the owned blocks only,
+// so a burst row and the same token run alone split the same way and stay
+// bit-identical. All of an item's bytes are requested at once (x, headers,
+// one or two rounds). kRounds: row-blocks per item (1 for split 4, 2 for
+// split 2).
+template <unsigned kRounds>
+__global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const uint8_t* __restrict__ plan, Scratch S) {
+  const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
+  uint32_t* status = decode_status(S);
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
+  const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden)), nsb = hidden / 256, nsub = hidden / 32;
+  const unsigned np = plan_field(PH, offsetof(PlanHeader, npairs)), tpw = plan_field(PH, offsetof(PlanHeader, tpw));
+  const unsigned burst = plan_field(PH, offsetof(PlanHeader, burst));
+  constexpr unsigned split = 4 / kRounds;
+  const uint32_t* upart = reinterpret_cast<const uint32_t*>(plan + plan_field(PH, offsetof(PlanHeader, groups_off)) +
+                                                          burst * sizeof(DecodeToken));
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __shared__ __align__(16) DecodeLds L;
+  const float* xg = reinterpret_cast<const float*>(plan + plan_field(PH, offsetof(PlanHeader, x_off)));
+  const unsigned xs0 = 32 * ((unsigned)tid >> 2) + 8 * ((unsigned)tid & 3);
+  const bool xin = ((unsigned)tid >> 2) < nsub;
+  const unsigned sb0 = 2 * (unsigned)wave, sb1 = sb0 + 1;
+  const bool has0 = sb0 < nsb, has1 = sb1 < nsb;
+  const unsigned lb0 = min(sb0, nsb - 1), lb1 = min(sb1, nsb - 1);
+  const uint32_t dq_off = 4608 * min(2 * (unsigned)wave + ((unsigned)lane >> 5), nsb - 1) + 32 * ((unsigned)lane & 31);
+  const uint32_t dh_off =
+      4608 * min(2 * (unsigned)wave + (((unsigned)lane & 15) >> 3), nsb - 1) + 4096 + 16 * ((unsigned)lane & 7);
+  const unsigned kg = (unsigned)lane >> 4, jcol = (unsigned)lane & 15;
+  uint32_t bad = 0;
+  const unsigned items = np * split, iend = min((blockIdx.x + 1) * tpw, items);
+  for (unsigned it = blockIdx.x * tpw; it < iend; ++it) {
+    const unsigned p = it / split, part = it % split, rb0 = kRounds * part;
+    const PairBuf B = pair_buf(pairs + p);
+    float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+    if (xin) {
+      const float* xt = xg + (size_t)B.token * hidden + xs0;
+      xv[0] = *reinterpret_cast<const float4*>(xt);
+      xv[1] = *reinterpret_cast<const float4*>(xt + 4);
+    }
+    const uint4 h0 = load_hdr(B, lb0, lane), h1 = load_hdr(B, lb1, lane);
+    DecodeNib N[kRounds];
+    DecodeDnBytes D[kRounds];
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r) {
+      load_nib(B, rb0 + r, lb0, lb1, lane, N[r]);
+      load_dn(B, rb0 + r, dq_off, dh_off, D[r]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();   // every wavefront is past the previous item's reads of x, the tables and h
+    stage_x(xv, 0, nsub, true, L, bad);
+    __syncthreads();   // x is in LDS
+    i32x4 b0[4], b1[4];
+    float fx0[2], fx1[2];
+    x_operands(0, sb0, lane, L, b0, fx0);
+    x_operands(0, sb1, lane, L, b1, fx1);
+    {
+      float mp = 0.f;
+      if (has0) mp += header_pass(h0, sb0, 0, 0, wave, lane, L, bad);
+      if (has1) mp += header_pass(h1, sb1, 1, 0, wave, lane, L, bad);
+      L.minp[0][wave][lane] = mp;
+    }
+    float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r) {
+      const unsigned rb = rb0 + r;
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      if (has0) rb_products(N[r].q[0], b0, fx0, 0, rb, wave, lane, L, acc);
+      if (has1) rb_products(N[r].q[1], b1, fx1, 1, rb, wave, lane, L, acc);
+      {
+        float4 v4;
+        v4.x = row_sum(acc[0]);
+        v4.y = row_sum(acc[1]);
+        v4.z = row_sum(acc[2]);
+        v4.w = row_sum(acc[3]);
+        if (jcol == 0) *reinterpret_cast<float4*>(&L.rowp[0][wave][16 * rb + 4 * kg]) = v4;
+      }
+      __syncthreads();   // every wavefront's sums of row-block rb are in LDS
+      if (lane < 8) {
+        const unsigned rg = 16 * rb + (unsigned)lane, ru = rg + 8;
+        float a = 0.f, u = 0.f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+          a += L.rowp[0][w][rg] - L.minp[0][w][rg];
+          u += L.rowp[0][w][ru] - L.minp[0][w][ru];
+        }
+        uint32_t hb = 0;
+        const float gh = B.gate * silu_mul_f32(a, u, hb);
+        if (wave == 0) bad |= hb;
+        L.h[wave][lane] = gh;
+      }
+      __builtin_amdgcn_wave_barrier();
+      down_round(D[r], L.h[wave], wave, lane, nsb, L, y, bad);
+    }
+    store_partial(S.wgpart, S.ustride, plan_read(upart + p) * split + part, wave, lane, y);
   }
   if (bad) flag(status, bad);
 }
@@ -3736,11 +3846,11 @@ __global__ void debug_quantize32(float* x, uint32_t groups) {
 // ------------------------------------------------------ static scratch
 //
 // fr_hip_launch_static's scratch, for callers that cannot allocate: the
-// decode kernels' error word (in a 256-byte first block), then the unit
-// partials of up to kStaticUnits units ([position block][unit][16]). Each
-// GPU the library runs on holds it (3.7 MB) until the process ends. Host
+// decode kernels' error word (in a 256-byte first block), then the
+// partials of up to kStaticUnits items ([position block][item][16]). Each
+// GPU the library runs on holds it (4.2 MB) until the process ends. Host
 // code reaches it only through the address hipGetSymbolAddress returns.
-constexpr uint32_t kStaticUnits = 224;   // one token: 10 routed and the shared expert x 20 blocks
+constexpr uint32_t kStaticUnits = 256;   // one token's items: 11 experts x 20 blocks, or split units of fewer blocks
 constexpr size_t kStaticHead = 64;       // floats before the partials (the error word, padded)
 constexpr size_t kStaticFloats = kStaticHead + (size_t)(kMaxHidden / 16) * kStaticUnits * 16;
 static __device__ __align__(256) float scratch[kStaticFloats];
@@ -3844,7 +3954,7 @@ struct Engine {
   size_t partial_bytes = 0;
   uint32_t* out = nullptr;        // [2][out_words]
   uint32_t out_words = 0;
-  float* wgpart = nullptr;        // [kMaxPairs][kMaxHidden] of float, or of double for ref-q8 plans
+  float* wgpart = nullptr;        // [kMaxDecodeItems][kMaxHidden] of float, or of double for ref-q8 plans
   uint32_t* bar = nullptr;        // [2]
   float* static_scratch = nullptr;   // device address of `scratch` on this engine's device
   // fr_hip_run's decode-path outputs in mapped pinned host memory (the host
@@ -4068,15 +4178,29 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
     H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
     // One workgroup per CU at most, each taking a contiguous chunk of
-    // ceil(units / cap) units of the work list.
+    // ceil(items / cap) items of the work list.
     const uint32_t cap = E.cus < (unsigned)kDecodeGridMax ? E.cus : (unsigned)kDecodeGridMax;
-    const uint32_t ppw = (nunits + cap - 1) / cap;
     H->kind = q4kt ? KIND_DECODE : KIND_DECODE_ROWS;
     bool with_shared = false;
     for (uint32_t t = 0; t < T; ++t) with_shared = with_shared || r->gate[t * 11 + 10] != 0.f;
     H->pad = q4kt ? 0u : combo | (with_shared ? kComboShared : 0u);
+    // F32 all-Q4_K units of a node with few owned blocks are split into
+    // items of fewer row-blocks (decode_split_kernel); the split depends on
+    // the owned blocks only, never on the burst.
+    const uint32_t split = q4kt && r->mode == MODE_F32 ? (nloaded <= 5 ? 4u : nloaded <= 11 ? 2u : 1u) : 1u;
+    if (split > 1) {
+      H->kind = KIND_DECODE_SPLIT;
+      H->pad = split;
+      DecodeToken* table = reinterpret_cast<DecodeToken*>(out + H->groups_off);   // a token's items
+      for (uint32_t t = 0; t < T; ++t) {
+        table[t].first *= split;
+        table[t].count *= split;
+      }
+    }
+    const uint32_t items = nunits * split;
+    const uint32_t ppw = (items + cap - 1) / cap;
     H->tpw = ppw;
-    H->grid = (nunits + ppw - 1) / ppw;
+    H->grid = (items + ppw - 1) / ppw;
     np = nunits;
   } else {
     // Pairs, partitioned by down format so each group is homogeneous.
@@ -4157,7 +4281,9 @@ bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, 
                    hipEvent_t mid) {
   const dim3 g(grid), b(kDecodeThreads);
   const bool q8 = H.mode == MODE_Q8;   // decode_q8_kernel or decode_rows_q8_kernel, double partials
-  if (H.kind == KIND_DECODE && q8) hipLaunchKernelGGL(decode_q8_kernel, g, b, 0, stream, dev_plan, S);
+  if (H.kind == KIND_DECODE_SPLIT && H.pad == 4) hipLaunchKernelGGL(decode_split_kernel<1>, g, b, 0, stream, dev_plan, S);
+  else if (H.kind == KIND_DECODE_SPLIT) hipLaunchKernelGGL(decode_split_kernel<2>, g, b, 0, stream, dev_plan, S);
+  else if (H.kind == KIND_DECODE && q8) hipLaunchKernelGGL(decode_q8_kernel, g, b, 0, stream, dev_plan, S);
   else if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, b, 0, stream, dev_plan, S);
   else if (q8) switch (H.pad) {   // the integer gate/up formats only (build_plan)
     case COMBO_NATIVE:
@@ -4219,8 +4345,12 @@ __global__ __launch_bounds__(64) void stage_plan(const uint4* __restrict__ src, 
 // buffers (fr_hip_run), and the engine's output parity is left as it is.
 int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream, bool host = false) {
   if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
-  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS;
-  if (decode && (grid > (unsigned)kDecodeGridMax || grid > H.npairs || H.ngroups != H.burst)) return FR_HIP_INVALID;
+  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS || H.kind == KIND_DECODE_SPLIT;
+  const unsigned items = H.kind == KIND_DECODE_SPLIT ? H.npairs * H.pad : H.npairs;
+  if (H.kind == KIND_DECODE_SPLIT && H.pad != 2 && H.pad != 4) return FR_HIP_INVALID;
+  if (decode && (grid > (unsigned)kDecodeGridMax || grid > items || items > (unsigned)kMaxDecodeItems ||
+                 H.ngroups != H.burst))
+    return FR_HIP_INVALID;
   if (H.kind == KIND_DECODE_ROWS && (H.pad & ~kComboShared) > COMBO_Q4_0) return FR_HIP_INVALID;
   Scratch S;
   S.done = E.done;
@@ -4232,7 +4362,7 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
   S.bar = E.bar;
   S.out_words = E.out_words;
   S.parity = E.parity;
-  S.ustride = kMaxPairs;
+  S.ustride = kMaxDecodeItems;
   S.ystat = nullptr;
   S.yout = nullptr;
   S.dstat = nullptr;
@@ -4541,7 +4671,7 @@ static int open_engine(int device) {
   CK(hipMalloc(&E.partial, E.partial_bytes));
   E.out_words = 4 + kMaxBurst * kMaxHidden;
   CK(hipMalloc(&E.out, 2 * (size_t)E.out_words * sizeof(uint32_t)));
-  CK(hipMalloc(&E.wgpart, (size_t)kMaxPairs * kMaxHidden * sizeof(double)));   // ref-q8 partials are doubles
+  CK(hipMalloc(&E.wgpart, (size_t)kMaxDecodeItems * kMaxHidden * sizeof(double)));   // ref-q8 partials are doubles
   CK(hipMalloc(&E.bar, 2 * sizeof(uint32_t)));
   CK(hipMemset(E.bar, 0, 2 * sizeof(uint32_t)));
   // The static scratch array's address on this device (the name is a host
@@ -4776,7 +4906,8 @@ int fr_hip_launch(const void* host_plan, const void* device_plan, void* stream) 
   const PlanHeader& H = *static_cast<const PlanHeader*>(host_plan);
   if (!H.burst || H.burst > (unsigned)kMaxBurst) return FR_HIP_INVALID;
   if (H.kind == KIND_LAYER ? !H.ntA || !H.ntB || H.grid != H.ntA + H.ntB
-                           : (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS) || !H.grid)
+                           : (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS && H.kind != KIND_DECODE_SPLIT) ||
+                                 !H.grid)
     return FR_HIP_INVALID;
   return launch(static_cast<const uint8_t*>(device_plan), H, H.grid,
                 stream ? static_cast<hipStream_t>(stream) : E.stream);
@@ -4789,10 +4920,12 @@ int fr_hip_launch_static(const void* host_plan, const void* device_plan, float* 
   const PlanHeader& H = *static_cast<const PlanHeader*>(host_plan);
   // Plans this variant runs: one token, decode kernels, units within the
   // static scratch.
-  if (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS) return FR_HIP_UNSUPPORTED;
+  if (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS && H.kind != KIND_DECODE_SPLIT) return FR_HIP_UNSUPPORTED;
   if (H.mode != MODE_F32) return FR_HIP_UNSUPPORTED;   // the static array holds float partials
-  if (H.burst != 1 || H.npairs > kStaticUnits || !H.hidden || H.hidden > (unsigned)kMaxHidden) return FR_HIP_UNSUPPORTED;
-  if (!H.grid || H.grid > (unsigned)kDecodeGridMax || H.grid > H.npairs || H.ngroups != H.burst) return FR_HIP_INVALID;
+  if (H.kind == KIND_DECODE_SPLIT && H.pad != 2 && H.pad != 4) return FR_HIP_INVALID;
+  const unsigned items = H.kind == KIND_DECODE_SPLIT ? H.npairs * H.pad : H.npairs;
+  if (H.burst != 1 || items > kStaticUnits || !H.hidden || H.hidden > (unsigned)kMaxHidden) return FR_HIP_UNSUPPORTED;
+  if (!H.grid || H.grid > (unsigned)kDecodeGridMax || H.grid > items || H.ngroups != H.burst) return FR_HIP_INVALID;
   if (H.kind == KIND_DECODE_ROWS && (H.pad & ~kComboShared) > COMBO_Q4_0) return FR_HIP_INVALID;
   if (!E.static_scratch) return FR_HIP_STATE;
   CK(hipSetDevice(E.device));
@@ -4836,7 +4969,7 @@ int run_once(const fr_hip_request* req, float* y, bool layer, unsigned* status_o
     hipLaunchKernelGGL(stage_plan, dim3((words + 63) / 64), dim3(64), 0, E.stream, E.plan_mapped,
                        reinterpret_cast<uint4*>(E.plan_dev), words);
   }
-  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS;
+  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS || H.kind == KIND_DECODE_SPLIT;
   rc = launch(E.plan_dev, H, grid, E.stream, decode);
   if (rc) return rc;
   const size_t count = (size_t)H.burst * H.hidden;

@@ -126,13 +126,14 @@ int fr_hip_last_output(void *stream, float *y, size_t count, unsigned *status);
 /* fr_hip_launch for callers that cannot allocate (no reference counterpart):
  * code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc. It calls no allocating routine: the decode kernels' scratch is
- * a static device array of the library (the unit partials of up to 224
- * units, 3.7 MB, held by each GPU the library runs on until the process
+ * a static device array of the library (the partials of up to 256 work
+ * items, 4.2 MB, held by each GPU the library runs on until the process
  * ends), and y and the status word are device memory the caller passes.
  * Runs plans of one token whose units take the decode kernels
- * (decode_kernel or decode_rows_kernel, then the fixed-order reduction):
- * up to 224 units, i.e. 10 routed experts and the shared one over 20
- * blocks, in F32 mode; anything else returns FR_HIP_UNSUPPORTED. Enqueued on `stream`
+ * (decode_kernel, decode_split_kernel or decode_rows_kernel, then the
+ * fixed-order reduction): up to 256 items, which every F32 single-token
+ * plan of up to 20 blocks fits (10 routed experts and the shared one);
+ * anything else returns FR_HIP_UNSUPPORTED. Enqueued on `stream`
  * (NULL = the library stream); when it completes, *device_status is 0 and
  * device_y holds the hidden outputs, or *device_status has the error bits
  * (FR_NUMERIC cases; device_y is then unspecified). Calls that overlap on

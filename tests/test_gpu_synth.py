@@ -373,3 +373,62 @@ def test_ref_q8_decode_error_paths(eng):
     finally:
         for b in range(2):
             eng.release(b)
+
+
+@pytest.mark.parametrize("nblocks,split", [(1, 4), (3, 4), (5, 4), (6, 2), (11, 2), (12, 1)])
+def test_split_units_for_few_blocks(eng, nblocks, split):
+    """A node that owns at most 5 (11) blocks splits each all-Q4_K unit into
+    4 (2) items of fewer row-blocks (decode_split_kernel): a single token
+    against the oracle and the layer kernel, bit for bit run to run, and a
+    4-token burst whose rows are bit-identical to the tokens run alone (the
+    split depends on the owned blocks only)."""
+    hidden, seed = 4096, 5150 + nblocks
+    lay = oracle.layout(hidden, fa.FMT_Q4KT)
+    rng = np.random.default_rng(nblocks)
+    blocks = sorted(rng.choice(20, nblocks, replace=False).tolist())
+    for b in blocks:
+        assert eng.synthetic(b, hidden, fa.FMT_Q4KT, 1, seed) == fa.OK
+    try:
+        burst = zipf_routes(rng, 4)
+        single = burst[:1]
+        units = [None] * 20
+        for b in blocks:
+            u = sparse_unit(lay)
+            for e in set(int(v) for v in burst.ravel()):
+                slice_view(u, lay, 0, e)[:] = oracle.synth_slice(lay, seed, b, 0, e)
+            units[b] = u
+        gates = np.zeros((4, 11), np.float32)
+        gates[:, :10] = softmax_gates(rng, 4)
+        x = rng.standard_normal((4, hidden)).astype(np.float32)
+        plan, grid = eng.plan(0, single, gates[:1], x[:1], fa.MODE_F32)
+        head = np.frombuffer(plan[:80].tobytes(), np.uint32)
+        want = fa.KIND_DECODE if split == 1 else fa.KIND_DECODE_SPLIT
+        assert int(head[16]) == want and (split == 1 or int(head[19]) == split), (head[16], head[19])
+        assert grid == min(256, 10 * nblocks * split) or split == 1, grid
+        print(f"split units: {nblocks} blocks, split {split}, grid {grid}", flush=True)
+        rc, y = eng.run(0, single, gates[:1], x[:1], fa.MODE_F32)
+        assert rc == fa.OK
+        rc, ref = oracle.ref_run(units, fa.FMT_Q4KT, False, oracle_request(0, single, gates[:1], x[:1]))
+        assert rc == 0
+        check_close(ref, y, fa.MODE_F32, ("split", nblocks))
+        rc, again = eng.run(0, single, gates[:1], x[:1], fa.MODE_F32)
+        assert rc == fa.OK and np.array_equal(y.view(np.uint32), again.view(np.uint32))
+        eng.route(fa.ROUTE_NO_DECODE)
+        try:
+            rc, y_lay = eng.run(0, single, gates[:1], x[:1], fa.MODE_F32)
+        finally:
+            eng.route(0)
+        assert rc == fa.OK
+        check_close(ref, y_lay, fa.MODE_F32, ("split vs layer", nblocks))
+        rc, yb = eng.run(0, burst, gates, x, fa.MODE_F32)
+        assert rc == fa.OK
+        rc, refb = oracle.ref_run(units, fa.FMT_Q4KT, False, oracle_request(0, burst, gates, x))
+        assert rc == 0
+        check_close(refb, yb, fa.MODE_F32, ("split burst", nblocks))
+        for t in range(4):
+            rc, y1 = eng.run(0, burst[t:t + 1], gates[t:t + 1], x[t:t + 1], fa.MODE_F32)
+            assert rc == fa.OK
+            assert np.array_equal(y1[0].view(np.uint32), yb[t].view(np.uint32)), f"token {t} differs alone"
+    finally:
+        for b in blocks:
+            eng.release(b)

@@ -3,9 +3,10 @@ graph capture or in loops that forbid hipMalloc). Its unit partials live in
 the library's static device array; y and the status word are the caller's.
 
 Checked against the engine's own launch of the same plan (fr_hip_launch +
-fr_hip_last_output) bit for bit, on two calls in a row, the second with a
-smaller request (half the owned blocks, so half the units), and on the error
-path; plans it does not run return FR_UNSUPPORTED.
+fr_hip_last_output) bit for bit, on calls in a row with fewer owned blocks
+each: 20 (decode_kernel, 200 units), 10 (units split in 2: 200 items) and 3
+(split in 4: 120 items), and on the error path; plans it does not run return
+FR_UNSUPPORTED.
 """
 import ctypes as C
 
@@ -56,7 +57,7 @@ def test_static_launch_matches_engine_launch():
     for b in range(20):
         assert eng.synthetic(b, H, fa.FMT_Q4KT, 1, 4040 + b) == fa.OK
     try:
-        for call, blocks in enumerate((20, 10)):
+        for call, blocks in enumerate((20, 10, 3)):
             for b in range(blocks, 20):
                 eng.release(b)
             experts = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
@@ -64,8 +65,10 @@ def test_static_launch_matches_engine_launch():
             gates[:, :10] = softmax_gates(rng, 1)
             x = rng.standard_normal((1, H)).astype(np.float32)
             plan, grid = eng.plan(0, experts, gates, x, fa.MODE_F32)
-            npairs = int(plan[12:16].view(np.uint32)[0])
+            head = plan[:80].view(np.uint32)
+            npairs = int(head[3])
             assert npairs == 10 * blocks
+            assert int(head[16]) == (fa.KIND_DECODE if blocks > 11 else fa.KIND_DECODE_SPLIT)
             dplan = device_plan(plan)
             print(f"static launch call {call}: {npairs} units, grid {grid}", flush=True)
             rc, ys, st = static_launch(lib, plan, dplan, ydev, sdev, sp)
