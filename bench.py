@@ -120,6 +120,8 @@ def grid_kernels(lib, plan):
     kind, mode = int(head[16]), int(head[2])
     if mode == 2 and kind in (1, 2):
         return ("decode_q8_kernel" if kind == 1 else "decode_rows_q8_kernel") + " + decode_reduce"
+    if mode == 3 and kind == 2:
+        return "decode_rows_q8_kernel (q8_256) + decode_reduce"
     return {1: "decode_kernel + decode_reduce", 2: "decode_rows_kernel + decode_reduce",
             3: "decode_split_kernel + decode_reduce"}.get(kind, "layer_kernel")
 
@@ -906,6 +908,11 @@ def main():
                 nq8["workload"] = ("native units (Q4_K gate/up, MXFP4 down) at hidden 4096 in the ref-q8 "
                                    "arithmetic (the hip-q8 table), 10 of 512 x 20 slices, 1 token")
                 extra["native_ref_q8"] = nq8
+                n256 = decode_leg(fa, lib, eng, k, 100, 20, SEED + 10, mode=fa.MODE_Q8_256)
+                n256["workload"] = ("native units (Q4_K gate/up, MXFP4 down) at hidden 4096 in the AVX2 "
+                                    "backend's arithmetic (the hip-q8-256 table: x per 256 and h per 32 "
+                                    "through quantize8, integer dots), 10 of 512 x 20 slices, 1 token")
+                extra["native_q8_256"] = n256
             for b in range(SLICES):
                 eng.release(b)
         m, _ = prefill_leg(fa, lib, eng, 2, 1)

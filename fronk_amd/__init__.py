@@ -13,7 +13,7 @@ from . import build as _build
 
 OK, INVALID, STATE, NUMERIC, IO, UNSUPPORTED = 0, -1, -2, -3, -4, -5
 FMT_LEGACY, FMT_NATIVE, FMT_Q4KT, FMT_Q8, FMT_MXFP4 = 0, 1, 2, 3, 4
-MODE_F32, MODE_F64, MODE_Q8 = 0, 1, 2
+MODE_F32, MODE_F64, MODE_Q8, MODE_Q8_256 = 0, 1, 2, 3
 Q4_0, Q8_0, Q4_K, MXFP4 = 2, 8, 12, 39
 MAX_BURST, MAX_HIDDEN, BLOCKS = 8, 4096, 20
 ROUTE_NO_DECODE = 2
@@ -75,6 +75,8 @@ SIGNATURES = {
     "fr_hip_debug_dequant_down": (C.c_int, [C.c_uint, C.c_void_p, C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_quantize": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_quantize64": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.POINTER(C.c_float)]),
+    "fr_hip_debug_quantize8": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.c_uint, C.POINTER(C.c_int8),
+                                         C.POINTER(C.c_float), C.POINTER(C.c_int16)]),
     "fr_hip_debug_read": (C.c_int, [C.c_uint, C.c_uint64, C.c_void_p, C.c_uint64]),
 }
 
@@ -249,3 +251,14 @@ class Engine:
         fn = lib().fr_hip_debug_quantize64 if regs else lib().fr_hip_debug_quantize
         rc = fn(fptr(x), x.size, fptr(out))
         return rc, out
+
+    def quantize8(self, x, group):
+        """The q8_256 quantizers on the device (the AVX2 backend's quantize8):
+        (rc, codes, d per group, int16 sums per 32 or None for group 32)."""
+        x = np.ascontiguousarray(x, np.float32)
+        q = np.zeros(x.size, np.int8)
+        d = np.zeros(max(x.size // group, 1), np.float32)
+        s = np.zeros(max(x.size // 32, 1), np.int16)
+        rc = lib().fr_hip_debug_quantize8(fptr(x), x.size, group, q.ctypes.data_as(C.POINTER(C.c_int8)), fptr(d),
+                                          s.ctypes.data_as(C.POINTER(C.c_int16)))
+        return rc, q, d, (s if group == 256 else None)

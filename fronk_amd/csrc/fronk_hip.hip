@@ -64,7 +64,7 @@ enum : uint8_t { TQ4_0 = 2, TQ8_0 = 8, TQ4_K = 12, TMXFP4 = 39, TQ4_KT = 140, TQ
 // TQ4_KM: the routed Q4_K gate/up rows of a pair in matrix-core tiles (see
 // the re-tiled layouts); it decodes as TQ4_K once loaded.
 template <int GU> constexpr int kAs = GU == TQ4_KM ? TQ4_K : GU;
-enum { MODE_F32 = 0, MODE_F64 = 1, MODE_Q8 = 2 };
+enum { MODE_F32 = 0, MODE_F64 = 1, MODE_Q8 = 2, MODE_Q8_256 = 3 };
 
 struct PairDesc {            // one (expert, block) slice of the request
   uint64_t slice;            // device address of the re-tiled slice
@@ -2083,6 +2083,93 @@ __device__ __forceinline__ void stage_x_q8(const float4 (&v4)[2], unsigned slot,
   }
 }
 
+// ------------------------------------------------- q8_256: the AVX2 arithmetic
+//
+// The AVX2 backend's native path quantizes x once per token with quantize8
+// (backends/avx2.c:184-203, group 256 at :633): d = amax/127, inv = amax ?
+// 127/amax : 0, codes by the cvtps conversion of x*inv (round to nearest
+// even; NaN and values outside int32 give INT32_MIN), saturated through
+// int16 to int8, and an int16 sum per 32 of the unsaturated codes (wrapping).
+// Its dots are integer (codes times the 6-bit scales or int8 weights) times
+// one float scale per block, h is SiLU in float (:428) quantized per 32 by
+// the same routine (:434), and the down is integer (codes times h codes)
+// times the block scale, md and the gate (:331-362, :364-390).
+
+// cvtps of one float (backends/avx2.c:193-196).
+__device__ __forceinline__ int cvtps_i32(float r) {
+  return (r != r || !(fabsf(r) < 2147483648.f)) ? INT_MIN : (int)rintf(r);
+}
+// The int8 code of a cvtps result: int32 -> int16 -> int8, saturating.
+__device__ __forceinline__ int sat_i8(int v) { return min(max(v, -128), 127); }
+
+// quantize8 of x per 256 in the row-format kernel's lane-major layout
+// (digit 0 the code, digit 1 zero): thread t holds values 8(t%4)..+7 of
+// sub-block t/4; the 32 threads of a 256-group agree on its largest
+// magnitude. Each sub-block's weight is the group's d, its sum the int16 sum
+// of its codes times d (exact in double).
+template <class Lds>
+__device__ __forceinline__ void stage_x_q256(const float4 (&v4)[2], unsigned nsub, Lds& L, uint32_t& bad) {
+  const unsigned tid = threadIdx.x, s = tid >> 2, q = tid & 3;
+  const float v[8] = {v4[0].x, v4[0].y, v4[0].z, v4[0].w, v4[1].x, v4[1].y, v4[1].z, v4[1].w};
+  float m = 0.f;
+  uint32_t fin = 1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    m = fmaxf(m, fabsf(v[i]));
+    fin &= isfinite(v[i]) ? 1u : 0u;
+  }
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) {
+    m = fmaxf(m, __shfl_xor(m, o));
+    fin &= (uint32_t)__shfl_xor((int)fin, o);
+  }
+  if (!fin && s < nsub) bad |= kErrRange;   // the reference's run rejects a non-finite x first (backends/avx2.c:626)
+  const float d = m / 127.0f, inv = m != 0.f ? 127.0f / m : 0.f;
+  uint32_t w[2] = {0u, 0u}, sum = 0u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = cvtps_i32(v[i] * inv);
+    sum += (uint32_t)c;
+    w[i >> 2] |= (uint32_t)(sat_i8(c) & 255) << (8 * (i & 3));
+  }
+  sum += (uint32_t)__shfl_xor((int)sum, 1);
+  sum += (uint32_t)__shfl_xor((int)sum, 2);
+  if (s < nsub) {
+    *reinterpret_cast<uint2*>(&L.xl[0][s & 1][q >> 1][s >> 1][2 * (q & 1)]) = make_uint2(w[0], w[1]);
+    *reinterpret_cast<uint2*>(&L.xl[1][s & 1][q >> 1][s >> 1][2 * (q & 1)]) = make_uint2(0u, 0u);
+    if (q == 0) {
+      *reinterpret_cast<float2*>(&L.xw[s][0]) = make_float2(d, 0.f);
+      L.xsd[s] = (double)(int16_t)(uint16_t)sum * (double)d;
+    }
+  }
+}
+
+// quantize8 of the unit's 32 h (group 32, no sums), held by lanes 0..31 of
+// the wavefront: h[n] becomes its code, *md the group's d.
+__device__ __forceinline__ void quantize_h32_q256(float* h, float* md, int lane) {
+  const float v = lane < 32 ? h[lane] : 0.f;
+  float m = fabsf(v);
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  const float inv = m != 0.f ? 127.0f / m : 0.f;
+  const float code = (float)sat_i8(cvtps_i32(v * inv));
+  __builtin_amdgcn_wave_barrier();
+  if (lane < 32) h[lane] = code;
+  if (lane == 0) *md = m / 127.0f;
+  __builtin_amdgcn_wave_barrier();
+}
+
+// SiLU(a)*u as the AVX2 native path forms it, a/(1+e^-a)*u in float
+// (backends/avx2.c:428); a non-finite h is its FR_NUMERIC (:433).
+__device__ __forceinline__ float silu_mul_q256(float a, float u, uint32_t& bad) {
+  const float h = a / (1.f + expf(-a)) * u;
+  if (!isfinite(h)) {
+    bad |= kErrRange;
+    return 0.f;
+  }
+  return h;
+}
+
 // Headers of super-block sb into the d*sc table (as decode_kernel's header
 // pass); the min term over the super-block in double, exact per sub-block.
 __device__ __forceinline__ double header_pass_q8(const uint4& h, unsigned sb, unsigned sbl, unsigned t, int wave,
@@ -2516,6 +2603,7 @@ struct RowsLds {
   float xw[kSubBlocks][2];              // ref-q8: the two digits' weights s, u of each sub-block
   double xsd[kSubBlocks];               // ref-q8: exact sum of each sub-block's quantized values
   float h[kNeurons];
+  float hmd;                            // q8_256: the d of the unit's quantized h
 };
 
 // The lane's x digits of sub-block 2c + J (J = 0, 1 of the lane's 64
@@ -2864,7 +2952,7 @@ __device__ __forceinline__ void load_digits_q8(const RowsLds& L, int c, LaneDigi
 
 // The lane's part of a row dot over sub-block 2c + J in double (scales as
 // lane_dot_digits; sc and mn are exact floats).
-template <int type, int J>
+template <int type, int J, int kDigits = 2>
 __device__ __forceinline__ double lane_dot_digits_q8(const LaneRaw& r, const float* sc, const float* mn,
                                                      const LaneDigitsQ8& X) {
   int acc[2] = {0, 0};
@@ -2875,7 +2963,7 @@ __device__ __forceinline__ double lane_dot_digits_q8(const LaneRaw& r, const flo
       for (int i = 0; i < 4; ++i) {
         const int w = (int)word(r.q[p], i);
 #pragma unroll
-        for (int d = 0; d < 2; ++d) acc[d] = __builtin_amdgcn_sdot4(w, X.q[d][4 * (p & 1) + i], acc[d], false);
+        for (int d = 0; d < kDigits; ++d) acc[d] = __builtin_amdgcn_sdot4(w, X.q[d][4 * (p & 1) + i], acc[d], false);
       }
   } else if (type == TQ4_K) {
 #pragma unroll
@@ -2883,7 +2971,7 @@ __device__ __forceinline__ double lane_dot_digits_q8(const LaneRaw& r, const flo
       const uint32_t v = word(r.q[i >> 2], i & 3);
       const int n = (int)(J ? nib_hi(v) : nib_lo(v));
 #pragma unroll
-      for (int d = 0; d < 2; ++d) acc[d] = __builtin_amdgcn_sdot4(n, X.q[d][i], acc[d], false);
+      for (int d = 0; d < kDigits; ++d) acc[d] = __builtin_amdgcn_sdot4(n, X.q[d][i], acc[d], false);
     }
   } else {
 #pragma unroll
@@ -2891,7 +2979,7 @@ __device__ __forceinline__ double lane_dot_digits_q8(const LaneRaw& r, const flo
       const uint32_t v = word(r.q[J], i);
       const int lo = (int)nib_lo(v), hi = (int)nib_hi(v);
 #pragma unroll
-      for (int d = 0; d < 2; ++d) {
+      for (int d = 0; d < kDigits; ++d) {
         acc[d] = __builtin_amdgcn_sdot4(lo, X.q[d][i], acc[d], false);
         acc[d] = __builtin_amdgcn_sdot4(hi, X.q[d][4 + i], acc[d], false);
       }
@@ -2903,11 +2991,12 @@ __device__ __forceinline__ double lane_dot_digits_q8(const LaneRaw& r, const flo
   return (double)sc[J] * qx;
 }
 
-// dot[i] = sum_n W[c0+i][n] * h[n] in double for the thread's 8 outputs
-// (backends/ref.c:86-92 with h quantized; the gate is applied at the store).
+// dot[i] = hscale * sum_n W[c0+i][n] * h[n] in double for the thread's 8
+// outputs (backends/ref.c:86-92 with h quantized, hscale 1; q8_256: h the
+// codes, hscale their d); the gate is applied at the store.
 template <int DN>
-__device__ __forceinline__ void rows_down_q8(const RowsDown& R, const float* hs, bool valid, double (&y)[8],
-                                             uint32_t& bad) {
+__device__ __forceinline__ void rows_down_q8(const RowsDown& R, const float* hs, double hscale, bool valid,
+                                             double (&y)[8], uint32_t& bad) {
   const float4* h4 = reinterpret_cast<const float4*>(hs);
   double hsum = 0.0;
   if (DN == TQ4_0) {
@@ -2967,14 +3056,18 @@ __device__ __forceinline__ void rows_down_q8(const RowsDown& R, const float* hs,
       }
       if (DN == TQ4_0) sum -= 8.0 * hsum;
     }
-    y[o] = valid ? (double)sc * sum : 0.0;
+    y[o] = valid ? (double)sc * sum * hscale : 0.0;
   }
 }
 
-template <int GU, int DN>
+// kQ256: the AVX2 arithmetic (one int8 code per x value, group 256; SiLU in
+// float; h codes and their d), otherwise ref-q8.
+template <int GU, int DN, bool kQ256>
 __device__ __forceinline__ uint32_t rows_unit_q8(double* wgpart, unsigned ustride, unsigned unit, const PairDesc* P,
                                                  const float* xg, unsigned hidden, int wave, int lane, RowsLds& L) {
   static_assert(GU != TMXFP4, "ref-q8 row units dot in integers");
+  static_assert(!kQ256 || GU != TQ4_0, "q8_256 row units are native or Q8_0");
+  constexpr int kDigits = kQ256 ? 1 : 2;
   const uint32_t* w = reinterpret_cast<const uint32_t*>(P);
   const uint64_t slice = ((uint64_t)uniform(plan_read(w + 1)) << 32) | uniform(plan_read(w));
   const uint32_t proj = uniform(plan_read(w + 2));
@@ -3005,7 +3098,8 @@ __device__ __forceinline__ uint32_t rows_unit_q8(double* wgpart, unsigned ustrid
 #pragma unroll
     for (int i = 0; i < kRowsWaveNeurons; ++i) load_gu_row<GU>(slice, proj, k, n0 + i, nch, c, raw[kRowsWaveNeurons * k + i]);
   RowsDown R;
-  stage_x_q8<RowsLds, true>(xv, 0, nsub, L, bad);
+  if constexpr (kQ256) stage_x_q256(xv, nsub, L, bad);
+  else stage_x_q8<RowsLds, true>(xv, 0, nsub, L, bad);
   __syncthreads();   // x's digits are in LDS
   double part[2 * kRowsWaveNeurons];
   LaneDigitsQ8 X;
@@ -3015,8 +3109,8 @@ __device__ __forceinline__ uint32_t rows_unit_q8(double* wgpart, unsigned ustrid
     float sc[2], mn[2];
     const bool ok = raw_scales<GU>(raw[r], c, sc, mn);
     if (active && !ok) bad |= kErrScale;
-    if (GU == TQ4_K && active && !q4k_weights_exact(raw[r].h.x)) bad |= kErrInexact;
-    part[r] = lane_dot_digits_q8<GU, 0>(raw[r], sc, mn, X);
+    if (!kQ256 && GU == TQ4_K && active && !q4k_weights_exact(raw[r].h.x)) bad |= kErrInexact;
+    part[r] = lane_dot_digits_q8<GU, 0, kDigits>(raw[r], sc, mn, X);
   }
   rows_load_down<DN>(down, hidden, c0, R);
   load_digits_q8<1>(L, c, X);
@@ -3025,7 +3119,7 @@ __device__ __forceinline__ uint32_t rows_unit_q8(double* wgpart, unsigned ustrid
   for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
     float sc[2], mn[2];
     (void)raw_scales<GU>(raw[r], c, sc, mn);
-    part[r] += lane_dot_digits_q8<GU, 1>(raw[r], sc, mn, X);
+    part[r] += lane_dot_digits_q8<GU, 1, kDigits>(raw[r], sc, mn, X);
     dot[r] = wave_total(active ? part[r] : 0.0);
   }
   if (lane < kRowsWaveNeurons) {
@@ -3036,19 +3130,23 @@ __device__ __forceinline__ uint32_t rows_unit_q8(double* wgpart, unsigned ustrid
         a = dot[i];
         u = dot[kRowsWaveNeurons + i];
       }
-    L.h[n0 + lane] = silu_mul(narrow_dot(a), narrow_dot(u), bad);   // backends/ref.c:80-83
+    if constexpr (kQ256) L.h[n0 + lane] = silu_mul_q256(narrow_dot(a), narrow_dot(u), bad);
+    else L.h[n0 + lane] = silu_mul(narrow_dot(a), narrow_dot(u), bad);   // backends/ref.c:80-83
   }
   __syncthreads();   // the unit's 32 h are in LDS
-  if (wave == 0) quantize_h32(L.h, lane);   // backends/ref.c:85
+  if (wave == 0) {
+    if constexpr (kQ256) quantize_h32_q256(L.h, &L.hmd, lane);   // backends/avx2.c:434
+    else quantize_h32(L.h, lane);                                // backends/ref.c:85
+  }
   __syncthreads();   // quantized
   double y[8];
-  rows_down_q8<DN>(R, L.h, dvalid, y, bad);
+  rows_down_q8<DN>(R, L.h, kQ256 ? (double)L.hmd : 1.0, dvalid, y, bad);
   store_partial_q8(wgpart, ustride, unit, wave, lane, gate, y);
   __syncthreads();   // h is read before the next unit writes it
   return bad;
 }
 
-template <int GA, int DA, int GB, int DB>
+template <int GA, int DA, int GB, int DB, bool kQ256 = false>
 __global__ __launch_bounds__(kDecodeThreads) void decode_rows_q8_kernel(const uint8_t* __restrict__ plan, Scratch S) {
   const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
   uint32_t* status = decode_status(S);
@@ -3069,9 +3167,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rows_q8_kernel(const ui
     const uint32_t w3 = uniform(plan_read(reinterpret_cast<const uint32_t*>(P) + 3));
     const uint32_t gu = w3 & 0xffu, dn = (w3 >> 8) & 0xffu;
     const unsigned unit = plan_read(upart + p);
-    if (GA == GB && DA == DB) bad |= rows_unit_q8<GA, DA>(wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
-    else if (gu == GA && dn == DA) bad |= rows_unit_q8<GA, DA>(wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
-    else bad |= rows_unit_q8<GB, DB>(wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
+    if (GA == GB && DA == DB) bad |= rows_unit_q8<GA, DA, kQ256>(wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
+    else if (gu == GA && dn == DA) bad |= rows_unit_q8<GA, DA, kQ256>(wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
+    else bad |= rows_unit_q8<GB, DB, kQ256>(wgpart, S.ustride, unit, P, xg, hidden, wave, lane, L);
   }
   if (bad) flag(status, bad);
 }
@@ -3841,6 +3939,46 @@ __global__ void debug_quantize32(float* x, uint32_t groups) {
   if (g < groups) q8_group(x + 32 * g, 32);
 }
 
+// quantize8 of one token's x (group 256) through the q8_256 staging of the
+// row-format kernel, read back from LDS: each value's code, d per 256 and
+// the int16 sum per 32 (hidden <= kMaxHidden, a multiple of 256).
+__global__ __launch_bounds__(kDecodeThreads) void debug_quantize8_x(const float* x, uint32_t hidden, int8_t* q,
+                                                                    float* d, int16_t* s) {
+  __shared__ __align__(16) RowsLds L;
+  const unsigned tid = threadIdx.x, nsub = hidden / 32, sb = tid >> 2, k = tid & 3;
+  float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  if (sb < nsub) {
+    const float4* xs = reinterpret_cast<const float4*>(x + 32 * sb + 8 * k);
+    xv[0] = xs[0];
+    xv[1] = xs[1];
+  }
+  uint32_t bad = 0;
+  stage_x_q256(xv, nsub, L, bad);
+  __syncthreads();
+  if (sb >= nsub) return;
+  const uint2 w = *reinterpret_cast<const uint2*>(&L.xl[0][sb & 1][k >> 1][sb >> 1][2 * (k & 1)]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[32 * sb + 8 * k + i] = (int8_t)((i < 4 ? w.x : w.y) >> (8 * (i & 3)));
+  if (k == 0) {
+    const float dg = L.xw[sb][0];
+    if (sb % 8 == 0) d[sb / 8] = dg;
+    s[sb] = dg == 0.f ? (int16_t)0 : (int16_t)(L.xsd[sb] / (double)dg);   // exact: the sum times d
+  }
+}
+
+// quantize8 of 32 h values (group 32) through the q8_256 h quantizer.
+__global__ __launch_bounds__(64) void debug_quantize8_h(const float* h, int8_t* q, float* d) {
+  __shared__ float hs[32];
+  __shared__ float md;
+  const int lane = threadIdx.x;
+  if (lane < 32) hs[lane] = h[lane];
+  __syncthreads();
+  quantize_h32_q256(hs, &md, lane);
+  __syncthreads();
+  if (lane < 32) q[lane] = (int8_t)hs[lane];
+  if (lane == 0) *d = md;
+}
+
 // ================================================================ host
 
 // ------------------------------------------------------ static scratch
@@ -4044,7 +4182,7 @@ uint32_t rows_combo(const Layout& l) {
 
 int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, unsigned* grid) {
   if (!r || !out || !used || !grid || !r->expert || !r->gate || !r->x) return FR_HIP_INVALID;
-  if (r->burst < 1 || r->burst > (unsigned)kMaxBurst || r->layer >= (unsigned)kLayers || r->mode > 2)
+  if (r->burst < 1 || r->burst > (unsigned)kMaxBurst || r->layer >= (unsigned)kLayers || r->mode > MODE_Q8_256)
     return FR_HIP_INVALID;
   const uint32_t T = r->burst, hidden = r->hidden;
   int nloaded = 0;
@@ -4094,16 +4232,28 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     for (int b = 0; b < kBlocks; ++b)
       if (E.block[b]) wbytes += ids[s2] == kShared ? E.lay[b].shared_slice : E.lay[b].slice;
   const bool fits = hidden <= (uint32_t)kMaxHidden && E.cus > 0;
-  const bool f32q8 = (r->mode == MODE_F32 || r->mode == MODE_Q8) && fits;
-  bool q4kt = f32q8, rows = f32q8;
   // The row-format kernel is instantiated per unit format: every loaded
   // block must have the first one's routed and shared formats.
   int first = 0;
   while (!E.block[first]) ++first;
   const uint32_t combo = rows_combo(E.lay[first]);
+  // q8_256 is the AVX2 backend's arithmetic. With legacy Q4_0 blocks that
+  // backend quantizes x per 64 into fr_q8_activation's codes
+  // (backends/avx2.c:83-100 against src/q4.c:37-61, used when any block is
+  // legacy, :630-633), so those requests run in the ref-q8 arithmetic.
+  uint32_t mode = r->mode;
+  if (mode == MODE_Q8_256) {
+    bool legacy = true;
+    for (int b = 0; b < kBlocks; ++b) legacy = legacy && (!E.block[b] || E.lay[b].gu == TQ4_0);
+    if (legacy) mode = MODE_Q8;
+  }
+  const bool f32q8 = (mode == MODE_F32 || mode == MODE_Q8 || mode == MODE_Q8_256) && fits;
+  bool q4kt = f32q8 && mode != MODE_Q8_256, rows = f32q8;
   rows = rows && combo != kNoCombo;
-  // ref-q8 row units need integer gate/up dots (decode_rows_q8_kernel).
-  if (r->mode == MODE_Q8) rows = rows && (combo == COMBO_NATIVE || combo == COMBO_Q8 || combo == COMBO_Q4_0);
+  // ref-q8 row units need integer gate/up dots (decode_rows_q8_kernel);
+  // q8_256 runs on the native and Q8_0 units, the formats its backend knows.
+  if (mode == MODE_Q8) rows = rows && (combo == COMBO_NATIVE || combo == COMBO_Q8 || combo == COMBO_Q4_0);
+  if (mode == MODE_Q8_256) rows = rows && (combo == COMBO_NATIVE || combo == COMBO_Q8);
   for (int b = 0; rows && b < kBlocks; ++b)
     rows = !E.block[b] || rows_combo(E.lay[b]) == combo;
   for (int b = 0; q4kt && b < kBlocks; ++b)
@@ -4169,7 +4319,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     if (w > (uint32_t)kMaxPairs) return FR_HIP_INVALID;
     H->hidden = hidden;
     H->burst = T;
-    H->mode = r->mode;
+    H->mode = mode;
     H->npairs = nunits;
     H->ngroups = T;
     H->groups_off = H->pairs_off + nunits * sizeof(PairDesc);
@@ -4187,7 +4337,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     // F32 all-Q4_K units of a node with few owned blocks are split into
     // items of fewer row-blocks (decode_split_kernel); the split depends on
     // the owned blocks only, never on the burst.
-    const uint32_t split = q4kt && r->mode == MODE_F32 ? (nloaded <= 5 ? 4u : nloaded <= 11 ? 2u : 1u) : 1u;
+    const uint32_t split = q4kt && mode == MODE_F32 ? (nloaded <= 5 ? 4u : nloaded <= 11 ? 2u : 1u) : 1u;
     if (split > 1) {
       H->kind = KIND_DECODE_SPLIT;
       H->pad = split;
@@ -4202,6 +4352,8 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     H->tpw = ppw;
     H->grid = (items + ppw - 1) / ppw;
     np = nunits;
+  } else if (mode == MODE_Q8_256) {
+    return FR_HIP_UNSUPPORTED;   // the layer kernel has no q8_256 arithmetic
   } else {
     // Pairs, partitioned by down format so each group is homogeneous.
     uint8_t classes[4] = {TQ4_KT, TMXFP4, TQ4_0, TQ8_0};
@@ -4238,7 +4390,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     const uint32_t nn = kTaskNeurons;
     H->hidden = hidden;
     H->burst = T;
-    H->mode = r->mode;
+    H->mode = mode;
     H->npairs = np;
     H->ngroups = ng;
     H->nranges = hidden / kCols;
@@ -4280,11 +4432,23 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
 bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, const Scratch& S, hipStream_t stream,
                    hipEvent_t mid) {
   const dim3 g(grid), b(kDecodeThreads);
-  const bool q8 = H.mode == MODE_Q8;   // decode_q8_kernel or decode_rows_q8_kernel, double partials
+  // decode_q8_kernel or decode_rows_q8_kernel: double partials.
+  const bool q8 = H.mode == MODE_Q8 || H.mode == MODE_Q8_256;
   if (H.kind == KIND_DECODE_SPLIT && H.pad == 4) hipLaunchKernelGGL(decode_split_kernel<1>, g, b, 0, stream, dev_plan, S);
   else if (H.kind == KIND_DECODE_SPLIT) hipLaunchKernelGGL(decode_split_kernel<2>, g, b, 0, stream, dev_plan, S);
   else if (H.kind == KIND_DECODE && q8) hipLaunchKernelGGL(decode_q8_kernel, g, b, 0, stream, dev_plan, S);
   else if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, b, 0, stream, dev_plan, S);
+  else if (H.mode == MODE_Q8_256) switch (H.pad) {   // native or Q8_0 units only (build_plan, launch)
+    case COMBO_NATIVE:
+      hipLaunchKernelGGL((decode_rows_q8_kernel<TQ4_K, TMXFP4, TQ4_K, TMXFP4, true>), g, b, 0, stream, dev_plan, S);
+      break;
+    case COMBO_NATIVE | kComboShared:
+      hipLaunchKernelGGL((decode_rows_q8_kernel<TQ4_K, TMXFP4, TQ8_0, TQ8_0, true>), g, b, 0, stream, dev_plan, S);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_rows_q8_kernel<TQ8_0, TQ8_0, TQ8_0, TQ8_0, true>), g, b, 0, stream, dev_plan, S);
+      break;
+  }
   else if (q8) switch (H.pad) {   // the integer gate/up formats only (build_plan)
     case COMBO_NATIVE:
       hipLaunchKernelGGL((decode_rows_q8_kernel<TQ4_K, TMXFP4, TQ4_K, TMXFP4>), g, b, 0, stream, dev_plan, S);
@@ -4352,6 +4516,10 @@ int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStrea
                  H.ngroups != H.burst))
     return FR_HIP_INVALID;
   if (H.kind == KIND_DECODE_ROWS && (H.pad & ~kComboShared) > COMBO_Q4_0) return FR_HIP_INVALID;
+  if (H.mode > MODE_Q8_256) return FR_HIP_INVALID;
+  if (H.mode == MODE_Q8_256 && (H.kind != KIND_DECODE_ROWS || ((H.pad & ~kComboShared) != COMBO_NATIVE &&
+                                                               (H.pad & ~kComboShared) != COMBO_Q8)))
+    return FR_HIP_INVALID;
   Scratch S;
   S.done = E.done;
   S.fin = E.fin;
@@ -4435,7 +4603,7 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // of token t's e-th expert, the order in which its partials are summed.
 int build_batch(const fr_hip_batch* r, uint8_t* out, size_t cap, size_t* used) {
   if (!r || !out || !used || !r->expert || !r->gate || !r->x) return FR_HIP_INVALID;
-  if (!r->tokens || r->tokens > (unsigned)kMaxBatchTokens || r->layer >= (unsigned)kLayers || r->mode > 2)
+  if (!r->tokens || r->tokens > (unsigned)kMaxBatchTokens || r->layer >= (unsigned)kLayers || r->mode > MODE_Q8_256)
     return FR_HIP_INVALID;
   if (r->mode != MODE_F32) return FR_HIP_UNSUPPORTED;
   const uint32_t T = r->tokens, hidden = r->hidden;
@@ -5215,6 +5383,35 @@ static int debug_quantize_run(const float* x, unsigned n, float* out, bool regs)
 }
 
 int fr_hip_debug_quantize(const float* x, unsigned n, float* out) { return debug_quantize_run(x, n, out, false); }
+
+int fr_hip_debug_quantize8(const float* x, unsigned n, unsigned group, int8_t* q, float* d, int16_t* s) {
+  if (!g_open) return FR_HIP_STATE;
+  const bool xg = group == 256 && n && n % 256 == 0 && n <= (unsigned)kMaxHidden && s;
+  if (!x || !q || !d || !(xg || (group == 32 && n == 32))) return FR_HIP_INVALID;
+  if (hipSetDevice(E.device) != hipSuccess) return FR_HIP_IO;
+  // One buffer: x, then the codes, the scales and the sums.
+  const size_t xb = n * sizeof(float), qb = n, db = n / group * sizeof(float), sb = n / 32 * sizeof(int16_t);
+  const size_t qo = xb, dof = (qo + qb + 15) & ~(size_t)15, so = (dof + db + 15) & ~(size_t)15;
+  uint8_t* buf = nullptr;
+  if (hipMalloc(&buf, so + sb) != hipSuccess) return FR_HIP_IO;
+  int rc = FR_HIP_OK;
+  if (hipMemcpy(buf, x, xb, hipMemcpyHostToDevice) != hipSuccess) rc = FR_HIP_IO;
+  if (!rc) {
+    float* dx = reinterpret_cast<float*>(buf);
+    int8_t* dq = reinterpret_cast<int8_t*>(buf + qo);
+    float* dd = reinterpret_cast<float*>(buf + dof);
+    int16_t* ds = reinterpret_cast<int16_t*>(buf + so);
+    if (xg) hipLaunchKernelGGL(debug_quantize8_x, dim3(1), dim3(kDecodeThreads), 0, E.stream, dx, n, dq, dd, ds);
+    else hipLaunchKernelGGL(debug_quantize8_h, dim3(1), dim3(64), 0, E.stream, dx, dq, dd);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(E.stream) != hipSuccess ||
+        hipMemcpy(q, dq, qb, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(d, dd, db, hipMemcpyDeviceToHost) != hipSuccess ||
+        (xg && hipMemcpy(s, ds, sb, hipMemcpyDeviceToHost) != hipSuccess))
+      rc = FR_HIP_IO;
+  }
+  (void)hipFree(buf);
+  return rc;
+}
 int fr_hip_debug_quantize64(const float* x, unsigned n, float* out) { return debug_quantize_run(x, n, out, true); }
 
 }  // extern "C"

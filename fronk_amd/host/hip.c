@@ -25,7 +25,9 @@
  * A second table, "hip-q8", is this backend with the ref-q8 arithmetic
  * (backends/ref.c:66,85: x and h through fr_q8_activation, fp64 sums), the
  * counterpart of the reference's ref / ref-q8 pair (backends/ref.c:124-125).
- * Both tables share the device and the loaded blocks.
+ * A third, "hip-q8-256", runs the AVX2 backend's arithmetic (x and h through
+ * its quantize8, backends/avx2.c:184-203, integer dots; FR_HIP_MODE_Q8_256).
+ * The tables share the device and the loaded blocks.
  * During self_test, load only reserves device memory and run copies the
  * slices a request references from the borrowed bytes first: the corpus
  * fixtures are sparse multi-GB units, and the native self-test corrupts the
@@ -150,9 +152,13 @@ static int run_mode(const fr_req *r, fr_part *out, unsigned mode) {
 
 static int run(const fr_req *r, fr_part *out) { return run_mode(r, out, FR_HIP_MODE_F32); }
 static int run_q8(const fr_req *r, fr_part *out) { return run_mode(r, out, FR_HIP_MODE_Q8); }
+static int run_q8_256(const fr_req *r, fr_part *out) { return run_mode(r, out, FR_HIP_MODE_Q8_256); }
 
 static int bench(int burst_max, fr_costmodel *out) { return fr_bench_execute_backend(&fr_hip, burst_max, out); }
 static int bench_q8(int burst_max, fr_costmodel *out) { return fr_bench_execute_backend(&fr_hip_q8, burst_max, out); }
+static int bench_q8_256(int burst_max, fr_costmodel *out) {
+    return fr_bench_execute_backend(&fr_hip_q8_256, burst_max, out);
+}
 
 static int check(const fr_backend *b, const char *dir) {
     if (loaded()) return FR_STATE;
@@ -164,9 +170,11 @@ static int check(const fr_backend *b, const char *dir) {
 }
 static int self_test(const char *dir) { return check(&fr_hip, dir); }
 static int self_test_q8(const char *dir) { return check(&fr_hip_q8, dir); }
+static int self_test_q8_256(const char *dir) { return check(&fr_hip_q8_256, dir); }
 
 const fr_backend fr_hip = {"hip", probe, load, unload, run, bench, self_test};
 const fr_backend fr_hip_q8 = {"hip-q8", probe, load, unload, run_q8, bench_q8, self_test_q8};
+const fr_backend fr_hip_q8_256 = {"hip-q8-256", probe, load, unload, run_q8_256, bench_q8_256, self_test_q8_256};
 
 /* The bench's backend_close hook (src/bench.c:265-278), like fr_avx2_close
  * (backends/avx2.c:718): FR_STATE while a block is loaded, otherwise release

@@ -5,7 +5,8 @@
 #include "backend.h"
 
 extern const fr_backend fr_hip;
-extern const fr_backend fr_hip_q8;   /* the same backend with ref-q8 arithmetic */
+extern const fr_backend fr_hip_q8;       /* the same backend with ref-q8 arithmetic */
+extern const fr_backend fr_hip_q8_256;   /* ... with the AVX2 backend's arithmetic */
 /* Release the device when no block is loaded; FR_STATE otherwise. */
 int fr_hip_backend_close(void);
 

@@ -37,8 +37,17 @@ enum { FR_HIP_FMT_LEGACY = 0, FR_HIP_FMT_NATIVE = 1, FR_HIP_FMT_Q4KT = 2,
  * Q8:  `ref-q8` (backends/ref.c:125): x and each slice's h quantized by the
  *      reference quantizer (src/q4.c:37-61), bit-exact, with fp64 dots (on
  *      all-Q4_K units: exact integer dots of x's two int8 digits, summed in
- *      fp64). */
-enum { FR_HIP_MODE_F32 = 0, FR_HIP_MODE_F64 = 1, FR_HIP_MODE_Q8 = 2 };
+ *      fp64).
+ * Q8_256: the AVX2 backend's arithmetic (backends/avx2.c:170-174): x as int8
+ *      codes per 256 by quantize8 (avx2.c:184-203, bit-exact), integer dots
+ *      times one float scale per block, SiLU in float, h as int8 codes per 32
+ *      (quantize8, avx2.c:434), integer down dots times the block scale, the
+ *      codes' d and the gate; sums over units in fp64. Native units (Q4_K
+ *      gate/up, MXFP4 down, Q8_0 shared expert) and all-Q8_0 units;
+ *      requests on legacy Q4_0 blocks run as Q8 (that backend's legacy codes,
+ *      avx2.c:83-100, are fr_q8_activation's); other formats, and requests
+ *      of more than 1,620 (token, pair) units, return FR_HIP_UNSUPPORTED. */
+enum { FR_HIP_MODE_F32 = 0, FR_HIP_MODE_F64 = 1, FR_HIP_MODE_Q8 = 2, FR_HIP_MODE_Q8_256 = 3 };
 
 /* ggml type ids accepted by the debug decoders (src/native.h:8). */
 enum { FR_HIP_Q4_0 = 2, FR_HIP_Q8_0 = 8, FR_HIP_Q4_K = 12, FR_HIP_MXFP4 = 39 };
@@ -216,6 +225,12 @@ int fr_hip_debug_quantize(const float *x, unsigned n, float *out);
  * in one lane's registers), which the single-token Q8 path applies to x;
  * n a multiple of 64. */
 int fr_hip_debug_quantize64(const float *x, unsigned n, float *out);
+/* The Q8_256 quantizers against the AVX2 backend's quantize8
+ * (backends/avx2.c:184-203): group 256 runs the decode kernel's x staging on
+ * one token (n a multiple of 256, at most 4096; codes q[n], d[n/256], int16
+ * sums s[n/32]); group 32 runs its h quantizer (n = 32; q[32], d[1]; s is not
+ * written). */
+int fr_hip_debug_quantize8(const float *x, unsigned n, unsigned group, int8_t *q, float *d, int16_t *s);
 /* Copy `len` re-tiled device bytes of a block, from byte `offset`. */
 int fr_hip_debug_read(unsigned block, uint64_t offset, void *out, uint64_t len);
 

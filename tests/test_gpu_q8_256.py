@@ -1,0 +1,232 @@
+"""FR_HIP_MODE_Q8_256: the AVX2 backend's arithmetic on the GPU.
+
+The AVX2 backend's native path (backends/avx2.c:170-174) quantizes x once per
+token with quantize8 (avx2.c:184-203, groups of 256), forms integer dots times
+one float scale per block, SiLU in float, h quantized per 32 by the same
+routine (avx2.c:434) and integer down dots times the block scale, h's d and
+the gate. Pinned three ways:
+- the device quantizers bit for bit against the oracle's quantize8, itself
+  pinned by closed forms (tests/test_oracle_kats.py);
+- the outputs against the reference's own AVX2 backend (the fr_avx2 vtable
+  compiled from its sources into oracle/_ref) on the same native units and
+  requests at its compiled-in H = 2560, far closer than either is to ref: the
+  two differ only in the order of float additions, libm's expf against the
+  device's, and the rare h code that those move across a rounding boundary;
+- the outputs against the oracle's ref within the backend tolerance the
+  reference holds AVX2 to (src/backend.c:13).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import fronk_amd as fa
+import oracle
+import vtable as vt
+from fixtures import oracle_request, softmax_gates, sparse_unit
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not vt.available(), reason="oracle/_ref or libfr_hip.so not built")]
+
+H = vt.HIDDEN          # the reference library's compiled-in hidden size
+BACKEND_TOL = (0.025, 0.030)   # fr_backend_tolerance (src/backend.c:13): rel. L2, normalized max
+AVX2_TOL = (2e-4, 2e-3)        # GPU against the AVX2 backend itself
+
+
+@pytest.fixture(scope="module")
+def eng():
+    e = fa.Engine(0)
+    yield e
+    for b in range(20):
+        e.release(b)
+
+
+def test_quantize8_bit_exact(eng):
+    """x per 256 through the decode kernel's staging (codes, d, int16 sums)
+    and h per 32 through its h quantizer, against the oracle: RNE ties, zero
+    groups, large and tiny magnitudes, and a group whose multiplier 127/amax
+    overflows (codes -128, sums wrapping to 0)."""
+    rng = np.random.default_rng(256)
+    cases = [rng.standard_normal(4096).astype(np.float32),
+             rng.standard_normal(2560).astype(np.float32) * 1e4,
+             (rng.standard_normal(4096) * 1e-30).astype(np.float32),
+             np.zeros(256, np.float32)]
+    ties = np.zeros(1024, np.float32)
+    ties[:7] = [127, .5, 1.5, 2.5, -.5, -1.5, -2.5]
+    ties[256:258] = [254, 3]
+    ties[512] = np.finfo(np.float32).max
+    ties[768] = 2.0 ** -140          # 127/amax overflows: every code of the group is -128
+    cases.append(ties)
+    for x in cases:
+        q0, d0, s0 = oracle.quantize8(x, 256)
+        rc, q, d, s = eng.quantize8(x, 256)
+        assert rc == fa.OK
+        assert np.array_equal(q, q0) and np.array_equal(d.view(np.uint32), d0.view(np.uint32))
+        assert np.array_equal(s, s0)
+    for x in [rng.standard_normal(32).astype(np.float32) * 3, ties[:32].copy(), np.zeros(32, np.float32),
+              ties[768:800].copy()]:
+        q0, d0, _ = oracle.quantize8(x, 32)
+        rc, q, d, _ = eng.quantize8(x, 32)
+        assert rc == fa.OK
+        assert np.array_equal(q, q0) and d.view(np.uint32)[0] == d0.view(np.uint32)[0]
+    assert eng.quantize8(np.zeros(100, np.float32), 256)[0] == fa.INVALID
+    assert eng.quantize8(np.zeros(64, np.float32), 32)[0] == fa.INVALID
+
+
+def ref_library():
+    ref = C.CDLL(vt.REF_LIB, mode=C.RTLD_GLOBAL)
+    ref.fr_native_fixture.argtypes = [C.c_void_p, C.c_uint, C.c_uint32]
+    ref.fr_avx2_set_tuning.argtypes = [C.c_uint] * 4
+    ref.fr_avx2_configure.argtypes = [C.c_uint, C.c_uint]
+    return ref
+
+
+def native_units(ref, lay, blocks, layer):
+    """Native units filled by the reference's own fixture (src/native.c:62):
+    experts 0..79 and the shared slice of `layer`, a seed per block."""
+    units = [None] * 20
+    for b in blocks:
+        u = sparse_unit(lay)
+        ref.fr_native_fixture(u.ctypes.data, layer, 11 + 101 * b)
+        units[b] = u
+    return units
+
+
+def avx2_run(avx2, layer, experts, gates, x):
+    q = vt.Req()
+    q.layer, q.burst = layer, x.shape[0]
+    for t in range(x.shape[0]):
+        for j in range(10):
+            q.expert[t][j] = int(experts[t, j])
+        for j in range(11):
+            q.gate[t][j] = float(gates[t, j])
+        C.memmove(q.x[t], np.ascontiguousarray(x[t], np.float32).ctypes.data, 4 * H)
+    out = vt.Part()
+    rc = avx2.run(C.byref(q), C.byref(out))
+    return rc, np.ctypeslib.as_array(out.y)[:x.shape[0]].copy()
+
+
+def close(ref, got, tol):
+    worst = (0.0, 0.0)
+    for t in range(ref.shape[0]):
+        rc, err = oracle.compare(ref[t], got[t])
+        assert rc == 0
+        assert err[0] <= tol[0] and err[1] <= tol[1], (t, err)
+        worst = (max(worst[0], err[0]), max(worst[1], err[1]))
+    return worst
+
+
+def requests(rng):
+    """A single token with the shared expert (the reference bench's values,
+    src/bench.c:347-351), one without it, and a 4-token burst over the 80
+    filled experts with softmax gates and x ~ N(0, 1)."""
+    x1 = np.array([((d * 37) % 257 - 128) / 128 for d in range(H)], np.float32).reshape(1, H)
+    g1 = np.full((1, 11), 0.0625, np.float32)
+    g1[0, 10] = 0.5
+    e1 = np.arange(10, dtype=np.uint16).reshape(1, 10) * 7 % 80
+    g2 = g1.copy()
+    g2[0, 10] = 0.0
+    e4 = np.stack([rng.choice(80, 10, replace=False) for _ in range(4)]).astype(np.uint16)
+    g4 = np.zeros((4, 11), np.float32)
+    g4[:, :10] = softmax_gates(rng, 4)
+    g4[1, 10] = 0.25
+    x4 = rng.standard_normal((4, H)).astype(np.float32)
+    return [("shared", e1, g1, x1), ("routed", e1.astype(np.uint16), g2, x1), ("burst4", e4, g4, x4)]
+
+
+def test_q8_256_matches_the_reference_avx2_backend(eng):
+    ref = ref_library()
+    avx2 = vt.Backend.in_dll(ref, "fr_avx2")
+    lay = oracle.layout(H, fa.FMT_NATIVE)
+    blocks, layer = (0, 5, 13), 3
+    units = native_units(ref, lay, blocks, layer)
+    for b in blocks:
+        assert eng.reserve(b, H, fa.FMT_NATIVE) == fa.OK
+        for e in list(range(80)) + [512]:
+            assert eng.refresh(b, units[b], layer, e) == fa.OK
+    ref.fr_avx2_set_tuning(len(blocks), 1, 4, 0)
+    assert ref.fr_avx2_configure(len(blocks), 1) == 0
+    for b in blocks:
+        assert avx2.load(b, units[b].ctypes.data, lay.block) == 0
+    try:
+        for name, experts, gates, x in requests(np.random.default_rng(7)):
+            print(f"q8_256 {name}: burst {x.shape[0]}, blocks {blocks}, layer {layer}", flush=True)
+            rc, y = eng.run(layer, experts, gates, x, fa.MODE_Q8_256)
+            assert rc == fa.OK, rc
+            assert eng.sample().blocks == len(blocks)
+            rc, ya = avx2_run(avx2, layer, experts, gates, x)
+            assert rc == 0
+            rc, yr = oracle.ref_run(units, fa.FMT_NATIVE, False, oracle_request(layer, experts, gates, x))
+            assert rc == 0
+            gpu_avx2 = close(ya, y, AVX2_TOL)
+            avx2_ref = close(yr, ya, BACKEND_TOL)
+            close(yr, y, BACKEND_TOL)
+            print(f"  gpu vs avx2 {gpu_avx2}, avx2 vs ref {avx2_ref}", flush=True)
+            # The device follows the AVX2 arithmetic, not ref's: far closer to it.
+            assert gpu_avx2[0] < 0.05 * avx2_ref[0], (gpu_avx2, avx2_ref)
+            rc, again = eng.run(layer, experts, gates, x, fa.MODE_Q8_256)
+            assert rc == fa.OK and np.array_equal(again.view(np.uint32), y.view(np.uint32))
+        # A burst row equals its token run alone, bit for bit.
+        _, e4, g4, x4 = requests(np.random.default_rng(7))[2]
+        rc, yb = eng.run(layer, e4, g4, x4, fa.MODE_Q8_256)
+        assert rc == fa.OK
+        for t in range(4):
+            rc, y1 = eng.run(layer, e4[t:t + 1], g4[t:t + 1], x4[t:t + 1], fa.MODE_Q8_256)
+            assert rc == fa.OK and np.array_equal(y1[0].view(np.uint32), yb[t].view(np.uint32)), t
+    finally:
+        for b in blocks:
+            avx2.unload(b)
+            eng.release(b)
+        ref.fr_avx2_close()
+
+
+def test_q8_256_routes_and_errors(eng):
+    """Q8_0 units take the same kernel; legacy Q4_0 blocks run as Q8 (the
+    AVX2 legacy codes are fr_q8_activation's), bit-identical to MODE_Q8;
+    formats outside the AVX2 backend's, the layer-kernel route and prefill
+    chunks are FR_HIP_UNSUPPORTED; a non-finite x is FR_NUMERIC."""
+    hidden = 4096
+    rng = np.random.default_rng(11)
+    experts = rng.choice(512, 10, replace=False).astype(np.uint16).reshape(1, 10)
+    gates = np.zeros((1, 11), np.float32)
+    gates[:, :10] = softmax_gates(rng, 1)
+    x = rng.standard_normal((1, hidden)).astype(np.float32)
+    # All-Q8_0 units, against the F32 path (the code rounding bounds the gap).
+    for b in (0, 1):
+        assert eng.synthetic(b, hidden, fa.FMT_Q8, 1, 900 + b) == fa.OK
+    try:
+        rc, y = eng.run(0, experts, gates, x, fa.MODE_Q8_256)
+        assert rc == fa.OK
+        rc, yf = eng.run(0, experts, gates, x, fa.MODE_F32)
+        assert rc == fa.OK
+        rc, err = oracle.compare(yf[0], y[0])
+        assert rc == 0 and err[0] < 0.02, err
+        bad = x.copy()
+        bad[0, 17] = np.inf
+        rc, yb = eng.run(0, experts, gates, bad, fa.MODE_Q8_256)
+        assert rc == fa.NUMERIC and not yb.any()
+        eng.route(fa.ROUTE_NO_DECODE)
+        try:
+            assert eng.run(0, experts, gates, x, fa.MODE_Q8_256)[0] == fa.UNSUPPORTED
+        finally:
+            eng.route(0)
+        assert eng.run_batch(0, experts, gates, x, fa.MODE_Q8_256)[0] == fa.UNSUPPORTED
+    finally:
+        for b in (0, 1):
+            eng.release(b)
+    for fmt in (fa.FMT_Q4KT, fa.FMT_MXFP4):
+        assert eng.synthetic(0, hidden, fmt, 1, 77) == fa.OK
+        try:
+            assert eng.run(0, experts, gates, x, fa.MODE_Q8_256)[0] == fa.UNSUPPORTED, fmt
+        finally:
+            eng.release(0)
+    # Legacy units exist at the reference's H = 2560 only.
+    x2 = rng.standard_normal((1, 2560)).astype(np.float32)
+    assert eng.synthetic(0, 2560, fa.FMT_LEGACY, 1, 78) == fa.OK
+    try:
+        rc, y8 = eng.run(0, experts, gates, x2, fa.MODE_Q8)
+        assert rc == fa.OK
+        rc, y256 = eng.run(0, experts, gates, x2, fa.MODE_Q8_256)
+        assert rc == fa.OK and np.array_equal(y8.view(np.uint32), y256.view(np.uint32))
+    finally:
+        eng.release(0)

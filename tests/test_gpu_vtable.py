@@ -24,6 +24,17 @@ def test_reference_self_test():
     assert vt.backend().self_test(vt.GOLDEN.encode()) == vt.OK
 
 
+def test_reference_self_test_q8_256():
+    """The "hip-q8-256" table (the AVX2 backend's arithmetic) through the same
+    harness: the legacy corpus (run as ref-q8, whose codes that backend's
+    legacy path shares) and the native self-test, within the backend
+    tolerance."""
+    t = vt.backend("fr_hip_q8_256")
+    assert t.name == b"hip-q8-256"
+    print("hip-q8-256 self_test: golden corpus, then native self-test", flush=True)
+    assert t.self_test(vt.GOLDEN.encode()) == vt.OK
+
+
 def test_reference_self_test_q8():
     """The "hip-q8" table (ref-q8 arithmetic) through the same harness: the
     corpus within the backend tolerance, the native self-test against ref."""

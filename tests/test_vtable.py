@@ -28,11 +28,13 @@ def test_name_and_table():
         assert C.cast(getattr(m, f), C.c_void_p).value == C.cast(getattr(b, f), C.c_void_p).value
 
 
-def test_q8_table_shares_the_backend():
-    """"hip-q8" differs from "hip" only in run, bench and self_test (the
-    ref-q8 arithmetic); probe, load and unload are the same functions."""
-    b, q = vt.backend(), vt.backend("fr_hip_q8")
-    assert q.name == b"hip-q8"
+@pytest.mark.parametrize("symbol,name", [("fr_hip_q8", b"hip-q8"), ("fr_hip_q8_256", b"hip-q8-256")])
+def test_q8_table_shares_the_backend(symbol, name):
+    """"hip-q8" (ref-q8 arithmetic) and "hip-q8-256" (the AVX2 backend's)
+    differ from "hip" only in run, bench and self_test; probe, load and
+    unload are the same functions."""
+    b, q = vt.backend(), vt.backend(symbol)
+    assert q.name == name
     for f in ("probe", "load", "unload"):
         assert C.cast(getattr(q, f), C.c_void_p).value == C.cast(getattr(b, f), C.c_void_p).value
     for f in ("run", "bench", "self_test"):
