@@ -176,6 +176,63 @@ def quantize8(x, group):
     return q, d, s
 
 
+def q8_256_run(blocks, fmt, req):
+    """The AVX2 backend's native arithmetic (backends/avx2.c:170-174, its run
+    at :615-716), restated with numpy up to the order of its float additions,
+    for native (Q4_K gate/up, MXFP4 down, Q8_0 shared) and all-Q8_0 units:
+    - x per token into int8 codes and one d per 256 by quantize8 (:633);
+    - each gate/up row's dot as the exact sum of weight x code x d, which is
+      what its integer dots times one float scale per block add up to
+      (Q4_K :262-319, the 6-bit scales applied in integers and the min term
+      through the int16 code sums; Q8_0 rows :237-248);
+    - a and u narrowed to float, h = a/(1 + e^-a)*u in float (:428), a
+      non-finite h FR_NUMERIC (:433);
+    - h into int8 codes and one d per 32 by quantize8 (:434);
+    - the down as the exact sum of weight x h code, times h's d and the gate
+      (MXFP4 :331-362 with its codes doubled into integers, Q8_0 :364-390);
+    - sums over experts and blocks in fp64, narrowed once (:705-709).
+    Weights come from the oracle's float decode, exact for the checker's
+    data (Q4_K d and dmin of close exponents). Returns (rc, y[burst, hidden]).
+    """
+    H, T = req.hidden, req.burst
+    lay = layout(H, fmt)
+    xs = np.ctypeslib.as_array(req.x)[:T, :H]
+    experts, gates = req.experts()[:T], req.gates()[:T]
+    y = np.zeros((T, H), np.float64)
+    for t in range(T):
+        x = np.ascontiguousarray(xs[t], np.float32)
+        if not np.isfinite(x).all():
+            return NUMERIC, None
+        q, d, _ = quantize8(x, 256)
+        xq = q.astype(np.float64) * np.repeat(d.astype(np.float64), 256)
+        for j in range(11):
+            g = float(gates[t, j])
+            if j == 10 and g == 0.0:
+                continue
+            eid = SHARED if j == 10 else int(experts[t, j])
+            shared = eid == SHARED
+            gu = lay.shared_gu_type if shared else lay.gu_type
+            dn = lay.shared_down_type if shared else lay.down_type
+            proj = lay.shared_proj if shared else lay.proj
+            for unit in blocks:
+                if unit is None:
+                    continue
+                off = slice_offset(lay, req.layer, eid)
+                sl = unit[off:off + (lay.shared_slice if shared else lay.slice)]
+                W = dequant(sl[:2 * proj], gu, 64 * H).astype(np.float64).reshape(64, H)
+                a, u = np.float32(W[:32] @ xq), np.float32(W[32:] @ xq)
+                with np.errstate(over="ignore", invalid="ignore"):
+                    h = (a / (np.float32(1) + np.exp(-a))) * u
+                if not np.isfinite(h).all():
+                    return NUMERIC, None
+                hq, hd, _ = quantize8(h.astype(np.float32), 32)
+                Wd = dequant(sl[2 * proj:], dn, 32 * H).astype(np.float64).reshape(H, 32)
+                y[t] += g * (Wd @ hq.astype(np.float64)) * float(hd[0])
+    if not np.isfinite(y).all() or (np.abs(y) > np.finfo(np.float32).max).any():
+        return NUMERIC, None
+    return OK, y.astype(np.float32)
+
+
 def native_dot(row, typ, x, n=None):
     x = np.ascontiguousarray(x, np.float32)
     out = C.c_double(123.0)

@@ -180,6 +180,45 @@ def test_q8_256_matches_the_reference_avx2_backend(eng):
         ref.fr_avx2_close()
 
 
+def test_q8_256_at_hidden_4096_matches_the_restatement(eng):
+    """At the headline H = 4096, which the compiled AVX2 backend does not
+    take, against the oracle's restatement of its arithmetic
+    (oracle.q8_256_run, pinned against that backend at H = 2560 by
+    tests/test_oracle_q8_256.py): synthetic native units, a token with the
+    shared expert and a 3-token burst."""
+    hidden, seed, blocks = 4096, 4242, (1, 8, 17)
+    lay = oracle.layout(hidden, fa.FMT_NATIVE)
+    rng = np.random.default_rng(4096)
+    experts = np.stack([rng.choice(512, 10, replace=False) for _ in range(3)]).astype(np.uint16)
+    gates = np.zeros((3, 11), np.float32)
+    gates[:, :10] = softmax_gates(rng, 3)
+    gates[0, 10] = 0.5
+    x = rng.standard_normal((3, hidden)).astype(np.float32)
+    units = [None] * 20
+    for b in blocks:
+        assert eng.synthetic(b, hidden, fa.FMT_NATIVE, 1, seed) == fa.OK
+        u = sparse_unit(lay)
+        for e in set(int(v) for v in experts.ravel()) | {512}:
+            off = oracle.slice_offset(lay, 0, e)
+            data = oracle.synth_slice(lay, seed, b, 0, e)
+            u[off:off + data.size] = data
+        units[b] = u
+    try:
+        for sel in (slice(0, 1), slice(0, 3)):
+            print(f"q8_256 at 4096: burst {sel.stop}", flush=True)
+            rc, y = eng.run(0, experts[sel], gates[sel], x[sel], fa.MODE_Q8_256)
+            assert rc == fa.OK, rc
+            rc, yo = oracle.q8_256_run(units, fa.FMT_NATIVE, oracle_request(0, experts[sel], gates[sel], x[sel]))
+            assert rc == oracle.OK
+            assert np.isfinite(y).all() and np.abs(yo).min(axis=1).max() >= 0 and (np.abs(yo).max(axis=1) > 0).all()
+            # Both sum exact products in fp64 and narrow once: equal but for rare
+            # last-bit ties (and an h code that a device expf ulp could move).
+            print(f"  gpu vs restatement {close(yo, y, AVX2_TOL)}, max|y| {np.abs(yo).max():.3e}", flush=True)
+    finally:
+        for b in blocks:
+            eng.release(b)
+
+
 def test_q8_256_routes_and_errors(eng):
     """Q8_0 units take the same kernel; legacy Q4_0 blocks run as Q8 (the
     AVX2 legacy codes are fr_q8_activation's), bit-identical to MODE_Q8;
