@@ -512,10 +512,10 @@ def time_run_calls(call, count, warmup=512, samples=1024):
     return out
 
 
-def run_leg(fa, lib, reqs, weight_bytes, warmup=512, samples=1024):
+def run_leg(fa, lib, reqs, weight_bytes, warmup=512, samples=1024, mode=None):
     """fr_hip_run timed the reference's way over prepared requests (layers
     rotating as the requests do); ctypes call overhead is inside the timer."""
-    prepared = [fa.make_request(*r, fa.MODE_F32) for r in reqs]
+    prepared = [fa.make_request(*r, fa.MODE_F32 if mode is None else mode) for r in reqs]
     y = np.zeros((8, HIDDEN), np.float32)
     yp = fa.fptr(y)
     run = lib.fr_hip_run
@@ -804,7 +804,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' legs")
     ap.add_argument("--copy-kernel", type=int, default=0)
+    ap.add_argument("--blocks", type=int, default=SLICES,
+                    help="owned slices of the measured leg (1..20; config 1 is 1); other values skip the other legs")
+    ap.add_argument("--mode", default="f32", choices=["f32", "q8", "q8_256"],
+                    help="arithmetic of the measured leg; other than f32 skips the other legs")
     args = ap.parse_args()
+    if not 1 <= args.blocks <= SLICES:
+        ap.error("--blocks is 1..20")
+    if args.blocks != SLICES or args.mode != "f32":
+        args.no_extra = args.no_cpu = True
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the layer share is built and timed on a "
               "single MI355X, and its multi-GPU sharding is a design, not a measured path.", file=sys.stderr)
@@ -833,16 +841,17 @@ def main():
     burst = wl["burst"]
     lib = fa.lib()
     eng = fa.Engine(0)
+    mode = {"f32": fa.MODE_F32, "q8": fa.MODE_Q8, "q8_256": fa.MODE_Q8_256}[args.mode]
     t0 = time.perf_counter()
-    for b in range(SLICES):
+    for b in range(args.blocks):
         fa.check(eng.synthetic(b, HIDDEN, fmt, LAYERS, SEED), "fr_hip_synthetic")
-    log(f"resident: {SLICES} blocks x {LAYERS} layers generated in {time.perf_counter() - t0:.1f} s")
+    log(f"resident: {args.blocks} blocks x {LAYERS} layers generated in {time.perf_counter() - t0:.1f} s")
 
     if args.workload == "run":
         # run() alone, the reference's way: for kernel traces of run() calls.
         reqs = make_requests(1024, burst, wl["routing"], SEED + 1)
-        wts = float(np.mean([algorithmic_bytes(fa, fmt, r[1], r[2])[0] for r in reqs]))
-        rec = run_leg(fa, lib, reqs, wts)
+        wts = float(np.mean([algorithmic_bytes(fa, fmt, r[1], r[2], args.blocks)[0] for r in reqs]))
+        rec = run_leg(fa, lib, reqs, wts, mode=mode)
         for b in range(SLICES):
             eng.release(b)
         print(json.dumps({"workload": wl["text"], "run": rec}), flush=True)
@@ -850,7 +859,7 @@ def main():
 
     n = args.warmup + args.steps
     reqs = make_requests(n, burst, wl["routing"], SEED + 1)
-    L = Launches(fa, lib, eng, fmt, reqs)
+    L = Launches(fa, lib, eng, fmt, reqs, args.blocks, mode)
     for i in range(args.warmup):
         L.enqueue(i)
     L.stream.synchronize()
@@ -870,12 +879,12 @@ def main():
     log(f"headline: {kernel_ms * 1e3:.3f} us per launch, {achieved:.1f} GB/s")
 
     ceiling, ceiling_bytes = achievable_leg(eng, lib, [L.host[i, :] for i in range(args.warmup, args.warmup + 8)])
-    run_rec = run_leg(fa, lib, reqs[:1024], float(L.wts[:1024].mean()))
+    run_rec = run_leg(fa, lib, reqs[:1024], float(L.wts[:1024].mean()), mode=mode)
     log(f"run(): p50 {run_rec['p50_us']} us p99 {run_rec['p99_us']} us")
 
     traffic = None
     tfile = os.path.join(ROOT, "profiles", f"decode_{key}_traffic.json")
-    if os.path.exists(tfile):
+    if os.path.exists(tfile) and args.blocks == SLICES and args.mode == "f32":   # counted on that workload
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
 
     scalar = None
@@ -946,10 +955,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32" if args.mode == "f32" else "i8+f64",
         "data": "synthetic (seeded device generator; Q4_K d/dmin fp16 U[1e-3,1e-2], x ~ N(0,1))",
-        "config": {"workload": wl["text"], "hidden": HIDDEN, "experts": 512, "active_experts": 10,
-                   "slices": SLICES, "burst": burst, "format": wl["fmt"][4:], "mode": "f32",
+        "config": {"workload": wl["text"] if args.blocks == SLICES else
+                   wl["text"].replace(f"{SLICES} owned slices", f"{args.blocks} owned slices")
+                             .replace(f"{SLICES} slices", f"{args.blocks} slices"),
+                   "hidden": HIDDEN, "experts": 512, "active_experts": 10,
+                   "slices": args.blocks, "burst": burst, "format": wl["fmt"][4:], "mode": args.mode,
                    "layers_rotated": LAYERS},
         "hbm_frac": round(weight_gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(burst * args.steps / wall, 1),
