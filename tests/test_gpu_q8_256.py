@@ -185,15 +185,17 @@ def test_q8_256_at_hidden_4096_matches_the_restatement(eng):
     take, against the oracle's restatement of its arithmetic
     (oracle.q8_256_run, pinned against that backend at H = 2560 by
     tests/test_oracle_q8_256.py): synthetic native units, a token with the
-    shared expert and a 3-token burst."""
+    shared expert, a 3-token burst and the largest, 8 tokens (four with the
+    shared expert)."""
     hidden, seed, blocks = 4096, 4242, (1, 8, 17)
     lay = oracle.layout(hidden, fa.FMT_NATIVE)
     rng = np.random.default_rng(4096)
-    experts = np.stack([rng.choice(512, 10, replace=False) for _ in range(3)]).astype(np.uint16)
-    gates = np.zeros((3, 11), np.float32)
-    gates[:, :10] = softmax_gates(rng, 3)
+    experts = np.stack([rng.choice(512, 10, replace=False) for _ in range(8)]).astype(np.uint16)
+    gates = np.zeros((8, 11), np.float32)
+    gates[:, :10] = softmax_gates(rng, 8)
     gates[0, 10] = 0.5
-    x = rng.standard_normal((3, hidden)).astype(np.float32)
+    gates[5:, 10] = 0.125
+    x = rng.standard_normal((8, hidden)).astype(np.float32)
     units = [None] * 20
     for b in blocks:
         assert eng.synthetic(b, hidden, fa.FMT_NATIVE, 1, seed) == fa.OK
@@ -204,7 +206,7 @@ def test_q8_256_at_hidden_4096_matches_the_restatement(eng):
             u[off:off + data.size] = data
         units[b] = u
     try:
-        for sel in (slice(0, 1), slice(0, 3)):
+        for sel in (slice(0, 1), slice(0, 3), slice(0, 8)):
             print(f"q8_256 at 4096: burst {sel.stop}", flush=True)
             rc, y = eng.run(0, experts[sel], gates[sel], x[sel], fa.MODE_Q8_256)
             assert rc == fa.OK, rc
