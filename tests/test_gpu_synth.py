@@ -375,14 +375,16 @@ def test_ref_q8_decode_error_paths(eng):
             eng.release(b)
 
 
-@pytest.mark.parametrize("nblocks,split", [(1, 4), (3, 4), (5, 4), (6, 2), (11, 2), (12, 1)])
-def test_split_units_for_few_blocks(eng, nblocks, split):
+@pytest.mark.parametrize("nblocks,split,hidden", [(1, 4, 4096), (3, 4, 4096), (5, 4, 4096), (6, 2, 4096),
+                                                 (11, 2, 4096), (12, 1, 4096), (1, 4, 2560), (7, 2, 2560)])
+def test_split_units_for_few_blocks(eng, nblocks, split, hidden):
     """A node that owns at most 5 (11) blocks splits each all-Q4_K unit into
     4 (2) items of fewer row-blocks (decode_split_kernel): a single token
     against the oracle and the layer kernel, bit for bit run to run, and a
     4-token burst whose rows are bit-identical to the tokens run alone (the
-    split depends on the owned blocks only)."""
-    hidden, seed = 4096, 5150 + nblocks
+    split depends on the owned blocks only). At hidden 2560 three of the
+    eight wavefronts own no super-block."""
+    seed = 5150 + nblocks
     lay = oracle.layout(hidden, fa.FMT_Q4KT)
     rng = np.random.default_rng(nblocks)
     blocks = sorted(rng.choice(20, nblocks, replace=False).tolist())
