@@ -16,10 +16,12 @@ plan (routing, gates, x) is also resident in HBM when timing starts.
 stdout: exactly one JSON line. Everything else goes to stderr.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload q4k]
-                  [--cpu-seconds S] [--no-cpu]
+                  [--cpu-seconds S] [--no-cpu] [--blocks N] [--mode f32]
                   workloads: q4k (the default), mtp4 (4-token Zipf burst),
                   q8, mxfp4 (all-Q8_0 / all-MXFP4 shares), native (Q4_K
-                  gate/up with an MXFP4 down)
+                  gate/up with an MXFP4 down); --blocks N owns N of the 20
+                  slices (1: config 1), --mode q8 / q8_256 runs the ref-q8 /
+                  AVX2 arithmetic (either skips the other legs)
   python bench.py --workload prefill   a step is one 48-layer chunk of 512
                                         tokens through fr_hip_run_batch
   python bench.py --copy-kernel BYTES   plain device copy, for scaling the
