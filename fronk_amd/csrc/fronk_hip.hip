@@ -2103,7 +2103,7 @@ __device__ __forceinline__ int cvtps_i32(float r) {
 __device__ __forceinline__ int sat_i8(int v) { return min(max(v, -128), 127); }
 
 // quantize8 of x per 256 in the row-format kernel's lane-major layout
-// (digit 0 the code, digit 1 zero): thread t holds values 8(t%4)..+7 of
+// (digit 0 the code; the q8_256 dots read no other): thread t holds values 8(t%4)..+7 of
 // sub-block t/4; the 32 threads of a 256-group agree on its largest
 // magnitude. Each sub-block's weight is the group's d, its sum the int16 sum
 // of its codes times d (exact in double).
@@ -2136,7 +2136,6 @@ __device__ __forceinline__ void stage_x_q256(const float4 (&v4)[2], unsigned nsu
   sum += (uint32_t)__shfl_xor((int)sum, 2);
   if (s < nsub) {
     *reinterpret_cast<uint2*>(&L.xl[0][s & 1][q >> 1][s >> 1][2 * (q & 1)]) = make_uint2(w[0], w[1]);
-    *reinterpret_cast<uint2*>(&L.xl[1][s & 1][q >> 1][s >> 1][2 * (q & 1)]) = make_uint2(0u, 0u);
     if (q == 0) {
       *reinterpret_cast<float2*>(&L.xw[s][0]) = make_float2(d, 0.f);
       L.xsd[s] = (double)(int16_t)(uint16_t)sum * (double)d;
@@ -2932,10 +2931,10 @@ struct LaneDigitsQ8 {
   double sum;    // exact sum of the sub-block's quantized values
 };
 
-template <int J>
+template <int J, int kDigits = 2>
 __device__ __forceinline__ void load_digits_q8(const RowsLds& L, int c, LaneDigitsQ8& X) {
 #pragma unroll
-  for (int d = 0; d < 2; ++d)
+  for (int d = 0; d < kDigits; ++d)
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int4 v = *reinterpret_cast<const int4*>(&L.xl[d][J][k][c][0]);
@@ -3103,7 +3102,7 @@ __device__ __forceinline__ uint32_t rows_unit_q8(double* wgpart, unsigned ustrid
   __syncthreads();   // x's digits are in LDS
   double part[2 * kRowsWaveNeurons];
   LaneDigitsQ8 X;
-  load_digits_q8<0>(L, c, X);
+  load_digits_q8<0, kDigits>(L, c, X);
 #pragma unroll
   for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
     float sc[2], mn[2];
@@ -3113,7 +3112,7 @@ __device__ __forceinline__ uint32_t rows_unit_q8(double* wgpart, unsigned ustrid
     part[r] = lane_dot_digits_q8<GU, 0, kDigits>(raw[r], sc, mn, X);
   }
   rows_load_down<DN>(down, hidden, c0, R);
-  load_digits_q8<1>(L, c, X);
+  load_digits_q8<1, kDigits>(L, c, X);
   double dot[2 * kRowsWaveNeurons];
 #pragma unroll
   for (int r = 0; r < 2 * kRowsWaveNeurons; ++r) {
