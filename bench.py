@@ -61,6 +61,10 @@ WORKLOADS = {
     "mtp4": dict(fmt="FMT_Q4KT", burst=4, routing="zipf",
                  text="MoE layer-share burst: 4 tokens, per-token top-10 of 512 under Zipf(1.1), 20 slices, "
                       "hidden 4096, Q4_K (down transposed); bytes counted once per unique expert"),
+    "shared4": dict(fmt="FMT_Q4KT", burst=4, routing="shared",
+                    text="MoE layer-share burst: 4 tokens routed to the same 10 of 512 experts (each in its own "
+                         "order), 20 slices, hidden 4096, Q4_K (down transposed); bytes counted once per unique "
+                         "expert"),
 }
 
 
@@ -79,6 +83,9 @@ def softmax_gates(rng, burst):
 def draw_routes(rng, burst, routing, zipf_perm, zipf_p):
     if routing == "uniform":
         return np.stack([rng.choice(512, 10, replace=False) for _ in range(burst)]).astype(np.uint16)
+    if routing == "shared":
+        base = rng.choice(512, 10, replace=False)
+        return np.stack([rng.permutation(base) for _ in range(burst)]).astype(np.uint16)
     return np.stack([zipf_perm[rng.choice(512, 10, replace=False, p=zipf_p)] for _ in range(burst)]).astype(np.uint16)
 
 
@@ -125,7 +132,7 @@ def grid_kernels(lib, plan):
     if mode == 3 and kind == 2:
         return "decode_rows_q8_kernel (q8_256) + decode_reduce"
     return {1: "decode_kernel + decode_reduce", 2: "decode_rows_kernel + decode_reduce",
-            3: "decode_split_kernel + decode_reduce"}.get(kind, "layer_kernel")
+            3: "decode_split_kernel + decode_reduce", 4: "decode_burst_kernel + decode_reduce"}.get(kind, "layer_kernel")
 
 
 def plan_slices(plan):
@@ -896,6 +903,7 @@ def main():
     extra = {}
     if not args.no_extra and key == "q4k":
         extra["config4_mtp4"] = decode_leg(fa, lib, eng, "mtp4", 300, 50, SEED + 4)
+        extra["burst4_shared_experts"] = decode_leg(fa, lib, eng, "shared4", 300, 50, SEED + 11)
         q8 = decode_leg(fa, lib, eng, "q4k", 100, 20, SEED + 5, mode=fa.MODE_Q8)
         q8["workload"] = ("config 2 in the ref-q8 arithmetic (the hip-q8 table: x and h through "
                           "fr_q8_activation, fp64 sums)")

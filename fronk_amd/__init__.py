@@ -16,9 +16,9 @@ FMT_LEGACY, FMT_NATIVE, FMT_Q4KT, FMT_Q8, FMT_MXFP4 = 0, 1, 2, 3, 4
 MODE_F32, MODE_F64, MODE_Q8, MODE_Q8_256 = 0, 1, 2, 3
 Q4_0, Q8_0, Q4_K, MXFP4 = 2, 8, 12, 39
 MAX_BURST, MAX_HIDDEN, BLOCKS = 8, 4096, 20
-ROUTE_NO_DECODE = 2
+ROUTE_NO_DECODE, ROUTE_NO_BURST, ROUTE_BURST = 2, 4, 8
 # Plan kinds (the kernel a plan runs), plan header word 16.
-KIND_LAYER, KIND_DECODE, KIND_DECODE_ROWS, KIND_DECODE_SPLIT = 0, 1, 2, 3
+KIND_LAYER, KIND_DECODE, KIND_DECODE_ROWS, KIND_DECODE_SPLIT, KIND_DECODE_BURST = 0, 1, 2, 3, 4
 
 LIB_PATH = _build.HIP_LIB
 

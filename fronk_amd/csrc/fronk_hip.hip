@@ -93,7 +93,7 @@ static_assert(sizeof(PlanHeader) == 80, "header layout");
 // kernel for all-Q4_K units with the transposed down (F32, routed experts
 // only), whose work list is (token, pair) units, token-major, each with its
 // own partial.
-enum : uint32_t { KIND_LAYER = 0, KIND_DECODE = 1, KIND_DECODE_ROWS = 2, KIND_DECODE_SPLIT = 3 };
+enum : uint32_t { KIND_LAYER = 0, KIND_DECODE = 1, KIND_DECODE_ROWS = 2, KIND_DECODE_SPLIT = 3, KIND_DECODE_BURST = 4 };
 // A decode plan's items (work-list entries with a partial each): one per
 // unit, or `split` (2 or 4) per unit for KIND_DECODE_SPLIT.
 constexpr int kMaxDecodeItems = 2048;
@@ -102,6 +102,11 @@ struct DecodeToken {
   uint32_t first, count;
 };
 constexpr int kDecodeUnitsPerToken = 11 * kBlocks;   // 10 routed experts and the shared one
+// Decode plans' work lists: every (token, pair) unit of a full burst fits,
+// shared expert included.
+constexpr int kMaxDecodeUnits = kMaxBurst * kDecodeUnitsPerToken;
+constexpr int kMaxPlanPairs = kMaxDecodeUnits > kMaxPairs ? kMaxDecodeUnits : kMaxPairs;
+static_assert(kMaxDecodeUnits <= kMaxDecodeItems, "a full burst's unit partials fit");
 
 struct Scratch {
   uint32_t* done;            // [2][kMaxPairs] phase-A wave completions per pair
@@ -1426,6 +1431,9 @@ __device__ __forceinline__ uint4 bld(const PairBuf& B, uint32_t voff, uint32_t s
 
 constexpr int kSubBlocks = kMaxHidden / 32;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 struct DecodeDnBytes {                 // one lane's down bytes of one round
   uint4 dq[2];                         // nibbles: super-block 2w + l/32, neurons 8r..8r+7,
@@ -1953,6 +1961,506 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const uint
       down_round(D[r], L.h[wave], wave, lane, nsb, L, y, bad);
     }
     store_partial(S.wgpart, S.ustride, plan_read(upart + p) * split + part, wave, lane, y);
+  }
+  if (bad) flag(status, bad);
+}
+
+// ------------------------------------------------- decode kernel, bursts
+//
+// F32, a burst of two or more tokens, every pair Q4_K gate/up (TQ4_KM tiles)
+// with the transposed Q4_K down, routed experts only, on a node that owns 12
+// or more blocks: one workgroup turn per unique (expert, block) pair, which
+// computes every token that routes to it at once. The pair's bytes are read
+// once, and the tokens sit in the columns of f16 matrix-core products, so a
+// token costs a column of each product instead of a pass of its own.
+//
+// Columns: token t in column 2t (hi part of its operand) and 2t+1 (lo part).
+// Gate/up, per super-block and row-block: A = sc*q, the 6-bit sub-block scale
+// times the nibble (< 1024), written straight into the bits of an f16
+// subnormal by one packed 16-bit multiply, so that A = sc*q*2^-24 exactly;
+// lane 16kg + i holds row i, sub-block 4p + kg, as the TQ4_KM tiles lie, so
+// one v_mfma_f32_16x16x32_f16 spans 8 positions of 4 sub-blocks and 8 of them
+// the super-block. B = x' of the column's token, x' = x*2^-e with |x'| < 2^15
+// over the token's values in the super-block, as hi = f16(x'), lo = f16(x' -
+// hi) (22 significant bits). The super-block's sums are scaled once by
+// d*2^(24+e); the min terms -dmin*m*sum(x) take v_mfma_f32_16x16x4f32 per
+// four sub-blocks on the fp32 sub-block sums of x. x is staged once per
+// workgroup: each wavefront turns its own two super-blocks of every token
+// into B operands that stay in registers for all of its pairs.
+//
+// Down, after the fourth round, per tile of 16 outputs (inside one 32-output
+// sub-block): A = sc*q of the 16 outputs x 32 neurons (each neuron's scale of
+// that sub-block), B = d*gate*h of each neuron and column in two f16 parts
+// over a power of two per (super-block, token). The min terms
+// -dmin*m*gate*h are one more product per sub-block (A = m, the same for
+// every output of the sub-block) that starts its two tiles' accumulators.
+// The 16-byte down units hold 4 outputs x 8 neurons; lane 16kg + 4a + q loads
+// the unit its quad needs for tile 4G + q, the quad shares it by DPP
+// broadcast, and each lane takes its own output q.
+//
+// Partials: one per (token, pair), in decode_kernel's position layout and
+// token-major numbering, which decode_reduce sums in the reference's order.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+struct BurstLds {
+  // Rows are padded so that the 8 tokens' 16-byte pieces fall on distinct banks.
+  float rowp[4][kDecodeWaves][kMaxBurst][20];   // [round][wave][token][row]: each wavefront's row sums
+  float h[kMaxBurst][kNeurons + 4];             // [token][neuron] gate*h of the pair
+  uint4 hdr[kDecodeWaves][2][64];               // [wave][super-block][row-block*16 + row]: gate/up headers
+  float dg[kDecodeWaves][2][64];                // d of each gate/up header
+  uint4 dsc[kDecodeWaves][2][8][4];             // [wave][super-block][sub-block][kg]: down sc of neurons 8kg.. as u16
+  uint4 dmn[kDecodeWaves][2][8][4];             // the down mins, same layout
+  float dd[kDecodeWaves][2][kNeurons];          // [wave][super-block][neuron] down d
+  float dm[kDecodeWaves][2][kNeurons];          // down dmin
+  float out[kDecodeWaves][kMaxBurst][260];      // [wave][token][output]: one super-block's down outputs (unscaled)
+};
+// x of up to 4 tokens at a time, staged by the whole workgroup: per token
+// and part a row of 4096 f16 values (16 bytes of padding between rows, so
+// that the 16 lanes of a 16-byte read hit distinct banks), 2^e per
+// (token, super-block) and the fp32 sum of each 32-value sub-block.
+constexpr int kStageTokens = 4;
+constexpr int kStageRow = kMaxHidden + 8;   // f16 values per (token, part) row
+struct BurstStage {
+  _Float16 x[kStageTokens * 2][kStageRow];
+  int e[kStageTokens][kMaxHidden / 256];
+  float sum[kStageTokens][kSubBlocks];
+};
+union BurstShared {
+  BurstStage stage;   // before the first pair
+  BurstLds pair;      // from the first pair on
+};
+static_assert(sizeof(BurstShared) <= 160 * 1024, "burst LDS");
+
+// A round's gate/up nibbles of the wavefront's two super-blocks,
+// [super-block][part] (lane 16kg + i: row i, sub-block 4 part + kg).
+struct BurstRound {
+  uint4 q[2][2];
+};
+__device__ __forceinline__ void load_burst_round(const PairBuf& B, unsigned rb, unsigned lb0, unsigned lb1, int lane,
+                                                 BurstRound& R) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+      R.q[s][p] = bld(B, 16 * (uint32_t)lane, 9216 * (s ? lb1 : lb0) + 1024 + 2048 * rb + 1024 * p);
+}
+// The pair's gate/up headers of the two super-blocks: lane l holds the
+// 16-byte header of row l%16 of row-block l/16.
+struct BurstHdr {
+  uint4 h[2];
+};
+__device__ __forceinline__ void load_burst_hdr(const PairBuf& B, unsigned lb0, unsigned lb1, int lane, BurstHdr& H) {
+  H.h[0] = bld(B, 16 * (uint32_t)lane, 9216 * lb0);
+  H.h[1] = bld(B, 16 * (uint32_t)lane, 9216 * lb1);
+}
+// The down bytes: unit (kg, 4(4G + q) + a) of each super-block for lane
+// 16kg + 4a + q (the unit its quad needs for tile 4G + q), and the header of
+// neuron l%32 of super-block 2w + l/32 (voff_h carries the super-block).
+struct BurstDown {
+  uint4 u[2][4];
+  uint4 h;
+};
+__device__ __forceinline__ void load_burst_down(const PairBuf& B, unsigned lb0, unsigned lb1, uint32_t voff_u,
+                                                uint32_t voff_h, BurstDown& D) {
+  const uint32_t base = 2 * B.proj;
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int G = 0; G < 4; ++G) D.u[s][G] = bld(B, voff_u, base + 4608 * (s ? lb1 : lb0) + 256 * G);
+  D.h = bld(B, voff_h, base + 4096);
+}
+
+__device__ __forceinline__ uint32_t mul_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
+}
+// Word w of a gate/up lane chunk (positions 8v..8v+3 in the low nibbles,
+// 8v+4..8v+7 in the high ones) times the scale pair s2 = sc | sc << 16, as 8
+// f16 subnormals sc*q*2^-24 in position order.
+__device__ __forceinline__ f16x8 burst_a(uint32_t w, uint32_t s2) {
+  const uint32_t lo = nib_lo(w), hi = nib_hi(w);
+  const u32x4 a = {mul_u16x2(__builtin_amdgcn_perm(0u, lo, 0x0c010c00u), s2),
+                   mul_u16x2(__builtin_amdgcn_perm(0u, lo, 0x0c030c02u), s2),
+                   mul_u16x2(__builtin_amdgcn_perm(0u, hi, 0x0c010c00u), s2),
+                   mul_u16x2(__builtin_amdgcn_perm(0u, hi, 0x0c030c02u), s2)};
+  return __builtin_bit_cast(f16x8, a);
+}
+// v split into the f16 part of the lane's column: hi = f16(v), lo = f16(v - hi).
+__device__ __forceinline__ _Float16 f16_part(float v, bool lo) {
+  const _Float16 h = (_Float16)v;
+  return lo ? (_Float16)(v - (float)h) : h;
+}
+// Lane mq's dword v of its quad, masked to the two nibbles at bit `shift`
+// and 16 + shift (the mask goes with the DPP read, so the move folds into
+// the AND), then shifted down: one output's two neurons as a u16 pair.
+template <int MQ>
+__device__ __forceinline__ uint32_t quad_nibbles(uint32_t v, uint32_t mask, uint32_t shift) {
+  constexpr int ctrl = MQ | MQ << 2 | MQ << 4 | MQ << 6;
+  return ((uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xf, 0xf, false) & mask) >> shift;
+}
+// One down tile (outputs 16m..16m+15 of a super-block) for every column: A
+// = sc*q of the lane's output (position q of the quad's unit) and neurons
+// 8kg..8kg+7, the product started at the sub-block's min terms.
+template <int MQ>
+__device__ __forceinline__ f32x4 burst_tile(const uint4& U, uint32_t mask, uint32_t shift, const uint4& scp,
+                                            const f16x8& bd, const f32x4& cmin) {
+  const u32x4 a = {mul_u16x2(quad_nibbles<MQ>(U.x, mask, shift), scp.x),
+                   mul_u16x2(quad_nibbles<MQ>(U.y, mask, shift), scp.y),
+                   mul_u16x2(quad_nibbles<MQ>(U.z, mask, shift), scp.z),
+                   mul_u16x2(quad_nibbles<MQ>(U.w, mask, shift), scp.w)};
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), bd, cmin, 0, 0, 0);
+}
+// Max over the 32 lanes of each half wavefront (quad butterflies, two row
+// rotations, then the other row of the half through a swizzle).
+__device__ __forceinline__ float half_wave_max(float m) {
+  m = fmaxf(m, dpp_f<kQuadXor1>(m));
+  m = fmaxf(m, dpp_f<kQuadXor2>(m));
+  m = fmaxf(m, dpp_f<kRowRor4>(m));
+  m = fmaxf(m, dpp_f<kRowRor8>(m));
+  return fmaxf(m, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(m), 0x401F)));   // lane ^ 16
+}
+
+__global__ __launch_bounds__(kDecodeThreads) void decode_burst_kernel(const uint8_t* __restrict__ plan, Scratch S) {
+  const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
+  uint32_t* status = decode_status(S);
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
+  const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden)), nsb = hidden / 256;
+  const unsigned np = plan_field(PH, offsetof(PlanHeader, npairs)), tpw = plan_field(PH, offsetof(PlanHeader, tpw));
+  const unsigned burst = plan_field(PH, offsetof(PlanHeader, burst));
+  // Each pair's partial index for tokens 0..7 (after the token table).
+  const uint32_t* bpart = reinterpret_cast<const uint32_t*>(plan + plan_field(PH, offsetof(PlanHeader, groups_off)) +
+                                                          burst * sizeof(DecodeToken));
+  const float* xg = reinterpret_cast<const float*>(plan + plan_field(PH, offsetof(PlanHeader, x_off)));
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __shared__ __align__(16) BurstShared SH;
+  BurstLds& L = SH.pair;
+  const unsigned kg = (unsigned)lane >> 4, col = (unsigned)lane & 15, tok = col >> 1;
+  const bool lo_part = (col & 1) != 0, tin = tok < burst;
+  const unsigned sb0 = 2 * (unsigned)wave, sb1 = sb0 + 1;
+  const bool has0 = sb0 < nsb, has1 = sb1 < nsb;
+  const unsigned lb0 = min(sb0, nsb - 1), lb1 = min(sb1, nsb - 1);
+  // Down offsets: lane 16kg + 4a + q loads unit (kg, 4(4G + q) + a); the
+  // header of neuron l%32 of super-block 2w + l/32.
+  const unsigned qa = ((unsigned)lane >> 2) & 3, qq = (unsigned)lane & 3;
+  const uint32_t voff_u = 1024 * kg + 64 * qq + 16 * qa;
+  const uint32_t voff_h = 4608 * ((unsigned)lane >> 5 ? lb1 : lb0) + 16 * ((unsigned)lane & 31);
+  const bool dh_valid = 2 * (unsigned)wave + ((unsigned)lane >> 5) < nsb;
+  uint32_t bad = 0;
+
+  unsigned p = blockIdx.x * tpw;   // this workgroup's chunk: pairs [p, min(p + tpw, np))
+  const unsigned pend = min(p + tpw, np);
+  PairBuf B = pair_buf(pairs + p);
+
+  // x of the burst into B operands: lane (kg, column) of wavefront w holds,
+  // for super-block 2w + s, sub-blocks kg and 4 + kg of the column's token
+  // (its hi or lo part), for all of the workgroup's pairs. The workgroup
+  // stages up to 4 tokens at a time in LDS: thread i takes values
+  // 8i..8i+7 of each token (the 32 threads of a super-block agree on its
+  // power of two), then every lane reads its operands. The first chunk's x
+  // is requested before the first pair's bytes, so that waiting for it does
+  // not wait for the weights.
+  const unsigned v0 = 8 * (unsigned)tid, sbx = (unsigned)tid >> 5;
+  const bool xlive = v0 < hidden;
+  float4 xv[kStageTokens][2];
+  auto load_x = [&](unsigned c0) {
+    const unsigned nt = min(burst - c0, (unsigned)kStageTokens);
+#pragma unroll
+    for (unsigned tl = 0; tl < (unsigned)kStageTokens; ++tl) {
+      const float* xt = xg + (size_t)(c0 + min(tl, nt - 1)) * hidden + (xlive ? v0 : 0);
+      xv[tl][0] = *reinterpret_cast<const float4*>(xt);
+      xv[tl][1] = *reinterpret_cast<const float4*>(xt + 4);
+    }
+  };
+  load_x(0);
+  BurstRound R[4];
+  BurstHdr HD;
+  load_burst_hdr(B, lb0, lb1, lane, HD);
+  load_burst_round(B, 0, lb0, lb1, lane, R[0]);
+  load_burst_round(B, 1, lb0, lb1, lane, R[1]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  f16x8 bx[2][2][4];   // [super-block][part p][word v]: positions 8v..8v+7 of sub-block 4p + kg
+  float xsm[2][2];     // sum of x over sub-block 4p + kg (hi columns of the burst's tokens; 0 otherwise)
+  int xe[2];           // 24 + e of the column's token in the super-block
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    xe[s] = 0;
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      xsm[s][pp] = 0.f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) bx[s][pp][v] = f16x8{};
+    }
+  }
+  {
+    BurstStage& X = SH.stage;
+    for (unsigned c0 = 0; c0 < burst; c0 += kStageTokens) {
+      const unsigned nt = min(burst - c0, (unsigned)kStageTokens);
+      if (c0) {
+        load_x(c0);
+        __syncthreads();   // the previous chunk's operands are read
+      }
+#pragma unroll
+      for (unsigned tl = 0; tl < (unsigned)kStageTokens; ++tl) {
+        const float v8[8] = {xv[tl][0].x, xv[tl][0].y, xv[tl][0].z, xv[tl][0].w,
+                             xv[tl][1].x, xv[tl][1].y, xv[tl][1].z, xv[tl][1].w};
+        float m = 0.f, sum = 0.f;
+        bool fin = true;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          m = fmaxf(m, fabsf(v8[k]));
+          fin = fin && isfinite(v8[k]);
+          sum += v8[k];
+        }
+        if (!fin && xlive && tl < nt) bad |= kErrRange;   // a non-finite x makes the token's a non-finite
+        m = half_wave_max(m);
+        sum += dpp_f<kQuadXor1>(sum);
+        sum += dpp_f<kQuadXor2>(sum);   // the 4 threads of a 32-value sub-block
+        int E = 0;
+        if (m > 0.f) (void)frexpf(m, &E);   // m < 2^E over the super-block
+        const int e = E - 15;
+        f16x8 hi, lo;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float xp = fin ? ldexpf(v8[k], -e) : 0.f;
+          hi[k] = (_Float16)xp;
+          lo[k] = (_Float16)(xp - (float)hi[k]);
+        }
+        if (xlive) {
+          *reinterpret_cast<f16x8*>(&X.x[2 * tl][v0]) = hi;
+          *reinterpret_cast<f16x8*>(&X.x[2 * tl + 1][v0]) = lo;
+          if ((tid & 3) == 0) X.sum[tl][v0 / 32] = fin ? sum : 0.f;
+          if ((tid & 31) == 0) X.e[tl][sbx] = e;
+        }
+      }
+      __syncthreads();   // the chunk is in LDS
+      // Lanes whose token is in this chunk take their operands.
+      const bool mine = tin && tok >= c0 && tok < c0 + nt;
+      const unsigned row = 2 * min(tok - min(tok, c0), (unsigned)kStageTokens - 1) + (lo_part ? 1u : 0u);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const unsigned sb = s ? lb1 : lb0;
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            // Columns of tokens past the burst take a staged token's values:
+            // their products are never used.
+            const f16x8 r = *reinterpret_cast<const f16x8*>(&X.x[row][256 * sb + 32 * (4 * pp + kg) + 8 * v]);
+            bx[s][pp][v] = mine || c0 == 0 ? r : bx[s][pp][v];
+          }
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          const float sm = X.sum[row >> 1][8 * sb + 4 * pp + kg];
+          xsm[s][pp] = mine && !lo_part ? sm : xsm[s][pp];
+        }
+        const int e = X.e[row >> 1][sb];
+        xe[s] = mine ? 24 + e : xe[s];
+      }
+    }
+    __syncthreads();   // the staging area becomes the pair loop's
+  }
+
+  float* rowp_w = &L.rowp[0][wave][tok][4 * kg];
+  for (;;) {
+    const unsigned q = p + 1;
+    const bool more = q < pend;
+    const PairBuf Bn = pair_buf(pairs + (more ? q : p), more);
+    const uint32_t tmask = uniform(plan_read(reinterpret_cast<const uint32_t*>(pairs + p) + 3)) >> 16 & 0xffu;
+    float gate = 0.f;   // the column's token's gate (scalar reads, then a per-lane pick)
+    uint32_t units[kMaxBurst];   // each token's partial index
+    {
+      const uint32_t* gw = reinterpret_cast<const uint32_t*>(pairs[p].gate);
+#pragma unroll
+      for (unsigned t = 0; t < (unsigned)kMaxBurst; ++t) {
+        const float g = __uint_as_float(uniform(plan_read(gw + t)));
+        units[t] = uniform(plan_read(bpart + (size_t)p * kMaxBurst + t));
+        gate = tok == t ? g : gate;
+      }
+    }
+    // The pair's gate/up headers into this wavefront's LDS, with each d.
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      L.hdr[wave][s][lane] = HD.h[s];
+      L.dg[wave][s][lane] = half_to_float(HD.h[s].x & 0xffff);
+    }
+    __builtin_amdgcn_wave_barrier();
+    BurstDown D;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      __builtin_amdgcn_sched_barrier(0);
+      // Two rounds ahead: rounds 2 and 3, the down, then the next pair's
+      // headers and rounds 0 and 1 (zeros after the last pair).
+      if (rb < 2) load_burst_round(B, rb + 2, lb0, lb1, lane, R[rb + 2]);
+      if (rb == 1) load_burst_down(B, lb0, lb1, voff_u, voff_h, D);
+      if (rb == 2) {
+        load_burst_hdr(Bn, lb0, lb1, lane, HD);
+        load_burst_round(Bn, 0, lb0, lb1, lane, R[0]);
+      }
+      if (rb == 3) load_burst_round(Bn, 1, lb0, lb1, lane, R[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const BurstRound& C = R[rb];
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      f32x4 cmin = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (!(s ? has1 : has0)) continue;
+        const uint4 hc = L.hdr[wave][s][16 * rb + col];   // row i = col of this row-block
+        const float4 drow = *reinterpret_cast<const float4*>(&L.dg[wave][s][16 * rb + 4 * kg]);
+        if (half_bad(hc.x) || half_bad(hc.x >> 16)) bad |= kErrScale;
+        const float dmn = half_to_float(hc.x >> 16);
+        uint32_t sc0, mi0, sc1, mi1;
+        q4k_scale_min(hc.y, hc.z, hc.w, kg, sc0, mi0);
+        q4k_scale_min(hc.y, hc.z, hc.w, 4 + kg, sc1, mi1);
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(burst_a(word(C.q[s][0], v), sc0 * 0x10001u), bx[s][0][v], c, 0,
+                                                     0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(burst_a(word(C.q[s][1], v), sc1 * 0x10001u), bx[s][1][v], c, 0,
+                                                     0, 0);
+        cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-dmn * (float)mi0, xsm[s][0], cmin, 0, 0, 0);
+        cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-dmn * (float)mi1, xsm[s][1], cmin, 0, 0, 0);
+        acc[0] = fmaf(c[0], ldexpf(drow.x, xe[s]), acc[0]);
+        acc[1] = fmaf(c[1], ldexpf(drow.y, xe[s]), acc[1]);
+        acc[2] = fmaf(c[2], ldexpf(drow.z, xe[s]), acc[2]);
+        acc[3] = fmaf(c[3], ldexpf(drow.w, xe[s]), acc[3]);
+      }
+      float v4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        v4[r] = acc[r] + cmin[r];
+        v4[r] += dpp_f<kQuadXor1>(v4[r]);   // hi + lo of the column pair
+      }
+      if (!lo_part) *reinterpret_cast<float4*>(rowp_w + rb * (kDecodeWaves * kMaxBurst * 20)) =
+          make_float4(v4[0], v4[1], v4[2], v4[3]);
+      __syncthreads();   // every wavefront's row sums of row-block rb are in LDS
+      if (wave == rb) {
+        // Lane (neuron i, token t): a = gate row i, u = up row 8 + i.
+        const unsigned i = (unsigned)lane >> 3, t = (unsigned)lane & 7;
+        float a = 0.f, u = 0.f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+          a += L.rowp[rb][w][t][i];
+          u += L.rowp[rb][w][t][8 + i];
+        }
+        const float g = __shfl(gate, (int)(2 * t));
+        float hv = 0.f;
+        if (t < burst && (tmask >> t & 1u)) {
+          uint32_t hb = 0;
+          hv = g * silu_mul_f32(a, u, hb);
+          bad |= hb;
+        }
+        L.h[t][8 * rb + i] = hv;
+      }
+    }
+    __syncthreads();   // the pair's h is in LDS
+
+    // Down tables from the neuron headers (this wavefront's own LDS).
+    {
+      const uint4 dh = D.h;
+      const unsigned n = (unsigned)lane & 31, s = (unsigned)lane >> 5;
+      if (dh_valid && (half_bad(dh.x) || half_bad(dh.x >> 16))) bad |= kErrScale;
+      L.dd[wave][s][n] = half_to_float(dh.x & 0xffff);
+      L.dm[wave][s][n] = half_to_float(dh.x >> 16);
+      const uint32_t sc_lo = dh.y & 0x3F3F3F3Fu, mi_lo = dh.z & 0x3F3F3F3Fu;
+      const uint32_t sc_hi = (dh.w & 0x0F0F0F0Fu) | ((dh.y >> 2) & 0x30303030u);
+      const uint32_t mi_hi = ((dh.w >> 4) & 0x0F0F0F0Fu) | ((dh.z >> 2) & 0x30303030u);
+      uint16_t* ts = reinterpret_cast<uint16_t*>(&L.dsc[wave][s][0][0]);
+      uint16_t* tm = reinterpret_cast<uint16_t*>(&L.dmn[wave][s][0][0]);
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        ts[32 * g + n] = (uint16_t)((g < 4 ? sc_lo : sc_hi) >> (8 * (g & 3)) & 0xffu);
+        tm[32 * g + n] = (uint16_t)((g < 4 ? mi_lo : mi_hi) >> (8 * (g & 3)) & 0xffu);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    {
+      // B of the down: d*gate*h and -dmin*gate*h of neurons 8kg..8kg+7 for
+      // the column's token, over a power of two per (super-block, token).
+      const float4 ha = *reinterpret_cast<const float4*>(&L.h[tok][8 * kg]);
+      const float4 hb4 = *reinterpret_cast<const float4*>(&L.h[tok][8 * kg + 4]);
+      const float hv[8] = {ha.x, ha.y, ha.z, ha.w, hb4.x, hb4.y, hb4.z, hb4.w};
+      const uint32_t shift = 4 * qq, mask = 0x000F000Fu << shift;
+      float* outw = &L.out[wave][tok][4 * kg];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (!(s ? has1 : has0)) continue;
+        float cd[8], cm[8], m = 0.f;
+        {
+          const float4 d0 = *reinterpret_cast<const float4*>(&L.dd[wave][s][8 * kg]);
+          const float4 d1 = *reinterpret_cast<const float4*>(&L.dd[wave][s][8 * kg + 4]);
+          const float4 m0 = *reinterpret_cast<const float4*>(&L.dm[wave][s][8 * kg]);
+          const float4 m1 = *reinterpret_cast<const float4*>(&L.dm[wave][s][8 * kg + 4]);
+          const float dv[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+          const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            cd[j] = dv[j] * hv[j];
+            cm[j] = -mv[j] * hv[j];
+            m = fmaxf(m, fmaxf(fabsf(cd[j]), fabsf(cm[j])));
+          }
+        }
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        int E = 0;
+        if (m > 0.f) (void)frexpf(m, &E);
+        const int e = E - 15;
+        f16x8 bd, bm;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          bd[j] = f16_part(ldexpf(cd[j], -e), lo_part);
+          bm[j] = f16_part(ldexpf(cm[j], -e), lo_part);
+        }
+        const int ye = 24 + e;
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int G = 0; G < 4; ++G) {
+          // Tiles 4G..4G+3: sub-blocks 2G (tiles 4G, 4G+1) and 2G+1.
+          const uint4 sc0 = L.dsc[wave][s][2 * G][kg], sc1 = L.dsc[wave][s][2 * G + 1][kg];
+          const f32x4 cm0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(f16x8, L.dmn[wave][s][2 * G][kg]), bm, z, 0, 0, 0);
+          const f32x4 cm1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(f16x8, L.dmn[wave][s][2 * G + 1][kg]), bm, z, 0, 0, 0);
+          const uint4 U = D.u[s][G];
+          f32x4 c[4];
+          c[0] = burst_tile<0>(U, mask, shift, sc0, bd, cm0);
+          c[1] = burst_tile<1>(U, mask, shift, sc0, bd, cm0);
+          c[2] = burst_tile<2>(U, mask, shift, sc1, bd, cm1);
+          c[3] = burst_tile<3>(U, mask, shift, sc1, bd, cm1);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            // Outputs 16(4G + k) + 4kg..+3 of the column: hi + lo (the
+            // store below applies 2^ye).
+            float4 y4;
+            y4.x = c[k][0] + dpp_f<kQuadXor1>(c[k][0]);
+            y4.y = c[k][1] + dpp_f<kQuadXor1>(c[k][1]);
+            y4.z = c[k][2] + dpp_f<kQuadXor1>(c[k][2]);
+            y4.w = c[k][3] + dpp_f<kQuadXor1>(c[k][3]);
+            if (!lo_part) *reinterpret_cast<float4*>(outw + 16 * (4 * G + k)) = y4;
+          }
+        }
+        __builtin_amdgcn_wave_barrier();
+        // The super-block's outputs of each routed token, times 2^ye,
+        // stored whole: lane l takes outputs 4l..4l+3, positions 512w +
+        // 256(l%2) + 4(32s + l/2) of decode_kernel's layout.
+        const unsigned pos = 512 * (unsigned)wave + 256 * ((unsigned)lane & 1) + 4 * (32 * (unsigned)s + ((unsigned)lane >> 1));
+        for (uint32_t tm = tmask; tm; tm &= tm - 1) {
+          const unsigned t = (unsigned)__builtin_ctz(tm);
+          uint32_t unit = units[0];
+#pragma unroll
+          for (unsigned k = 1; k < (unsigned)kMaxBurst; ++k) unit = t == k ? units[k] : unit;
+          const int yt = __builtin_amdgcn_readlane(ye, (int)(2 * t));   // the token's hi column
+          const float4 y4 = *reinterpret_cast<const float4*>(&L.out[wave][t][4 * lane]);
+          *reinterpret_cast<float4*>(S.wgpart + partial_index(unit, pos, S.ustride)) =
+              make_float4(ldexpf(y4.x, yt), ldexpf(y4.y, yt), ldexpf(y4.z, yt), ldexpf(y4.w, yt));
+        }
+        __builtin_amdgcn_wave_barrier();   // the outputs are read before the next super-block writes them
+      }
+    }
+    if (!more) break;
+    p = q;
+    B = Bn;
   }
   if (bad) flag(status, bad);
 }
@@ -3442,7 +3950,6 @@ constexpr int kTileTokens = 16;          // tokens of one expert tile (the MFMA 
 constexpr int kBatchThreads = 512;
 constexpr int kMaxBatchTokens = 4096;
 constexpr int kDownCols = 1024;          // outputs of one prefill_down workgroup
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct BatchTile {                       // one routed expert and up to 16 of its tokens
   uint32_t expert, ntok, slot0, pad;
@@ -3536,9 +4043,6 @@ struct GateUpLds {
   float main[kDecodeWaves][16][kTileTokens]; // [wave][row][token] scale-weighted dot part
   float mins[kDecodeWaves][16][kTileTokens]; // [wave][row][token] min part
 };
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // Two nibble values (bytes b and b+1 of v, each below 16) times the 6-bit
 // scale sc as two f16 in one dword: the packed 16-bit multiply-add forms the
@@ -4107,6 +4611,8 @@ struct Engine {
   // decode kernels (fr_hip_route changes it later).
   uint32_t group_bytes = 49152;
   bool no_decode = false;
+  bool no_burst = false;          // bursts of all-Q4_K units one unit per (token, pair) on decode_kernel
+  bool force_burst = false;       // every such burst on decode_burst_kernel, whatever its expert sharing
   uint8_t* plan_dev = nullptr;
   uint8_t* plan_host = nullptr;   // pinned, mapped
   const uint4* plan_mapped = nullptr;   // the device's view of plan_host
@@ -4141,7 +4647,10 @@ bool g_open = false;
 void release_engine();
 
 size_t plan_capacity(uint32_t burst, uint32_t hidden) {
-  return sizeof(PlanHeader) + (size_t)kMaxPairs * sizeof(PairDesc) + (size_t)kMaxPairs * sizeof(GroupDesc) + 256 +
+  // Pair or unit descriptors, then the group table, the decode token table
+  // and unit indices, or the burst kernel's per-pair partial indices.
+  return sizeof(PlanHeader) + (size_t)kMaxPlanPairs * sizeof(PairDesc) +
+         (size_t)kMaxPlanPairs * kMaxBurst * sizeof(uint32_t) + kMaxBurst * sizeof(DecodeToken) + 256 +
          (size_t)burst * hidden * sizeof(float);
 }
 
@@ -4260,9 +4769,79 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   for (int s2 = 0; q4kt && s2 < nu; ++s2) q4kt = ids[s2] != kShared;
   uint32_t nunits = 0;
   for (uint32_t t = 0; t < T; ++t) nunits += (10u + (r->gate[t * 11 + 10] != 0.f ? 1u : 0u)) * (uint32_t)nloaded;
-  const bool decode = (q4kt || rows) && nunits <= (uint32_t)kMaxPairs;
+  const bool decode = (q4kt || rows) && nunits <= (uint32_t)kMaxDecodeUnits;
+  // F32 all-Q4_K units of a node with few owned blocks are split into
+  // items of fewer row-blocks (decode_split_kernel); the split depends on
+  // the owned blocks only, never on the burst. Bursts of two or more tokens
+  // on the unsplit route whose tokens share experts run one workgroup turn
+  // per unique pair (decode_burst_kernel): it pays from about two routed
+  // tokens per unique expert on average (10 T >= 2 unique); below that the
+  // per-(token, pair) units are faster (measured: 4 tokens on one expert
+  // set 28.9 against 47.9 us, a 4-token Zipf(1.1) burst with 1.3 tokens
+  // per expert 58 against 52 us).
+  const uint32_t split = q4kt && mode == MODE_F32 ? (nloaded <= 5 ? 4u : nloaded <= 11 ? 2u : 1u) : 1u;
+  const bool burst_k = q4kt && mode == MODE_F32 && T >= 2 && split == 1 && !E.no_burst &&
+                       (E.force_burst || 10u * T >= 2u * (uint32_t)nu);
   uint32_t np = 0;
-  if (decode && !E.no_decode) {
+  if (decode && !E.no_decode && burst_k) {
+    DecodeToken tok[kMaxBurst];
+    for (uint32_t t = 0, first = 0; t < T; ++t) {
+      tok[t].first = first;
+      tok[t].count = 10u * (uint32_t)nloaded;
+      first += tok[t].count;
+    }
+    // Unique pairs, experts in first-appearance order and blocks ascending;
+    // each with its tokens' gates and, per token, the partial index of the
+    // (token, pair) unit in the token-major numbering of decode_kernel.
+    np = (uint32_t)nu * (uint32_t)nloaded;
+    H->groups_off = H->pairs_off + np * sizeof(PairDesc);
+    memcpy(out + H->groups_off, tok, T * sizeof(DecodeToken));
+    uint32_t* bpart = reinterpret_cast<uint32_t*>(out + H->groups_off + T * sizeof(DecodeToken));
+    uint32_t w = 0;
+    for (int s2 = 0; s2 < nu; ++s2) {
+      uint8_t place[kMaxBurst] = {};
+      for (uint32_t t = 0; t < T; ++t) {
+        if (!(masks[s2] >> t & 1u)) continue;
+        int e = 0;
+        while (r->expert[t * 10 + e] != ids[s2]) ++e;
+        place[t] = (uint8_t)e;
+      }
+      int brank = 0;
+      for (int b = 0; b < kBlocks; ++b) {
+        if (!E.block[b]) continue;
+        const Layout& l = E.lay[b];
+        PairDesc& P = pairs[w];
+        memset(&P, 0, sizeof(P));
+        P.slice = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer + (uint64_t)ids[s2] * l.slice);
+        P.proj = (uint32_t)l.proj;
+        P.gu = (uint8_t)l.gu;
+        P.dn = (uint8_t)l.dn;
+        P.tmask = masks[s2];
+        for (uint32_t t = 0; t < T; ++t) {
+          P.gate[t] = gates[s2][t];
+          bpart[w * kMaxBurst + t] =
+              masks[s2] >> t & 1u ? tok[t].first + (uint32_t)place[t] * (uint32_t)nloaded + (uint32_t)brank : 0u;
+        }
+        for (uint32_t t = T; t < (uint32_t)kMaxBurst; ++t) bpart[w * kMaxBurst + t] = 0u;
+        ++w;
+        ++brank;
+      }
+    }
+    if (w != np) return FR_HIP_INVALID;
+    H->hidden = hidden;
+    H->burst = T;
+    H->mode = mode;
+    H->npairs = np;
+    H->ngroups = T;
+    H->x_off = (uint32_t)((H->groups_off + T * sizeof(DecodeToken) + np * kMaxBurst * sizeof(uint32_t) + 255) & ~255u);
+    memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
+    H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
+    const uint32_t cap = E.cus < (unsigned)kDecodeGridMax ? E.cus : (unsigned)kDecodeGridMax;
+    H->kind = KIND_DECODE_BURST;
+    H->pad = 0;
+    H->tpw = (np + cap - 1) / cap;
+    H->grid = (np + H->tpw - 1) / H->tpw;
+  } else if (decode && !E.no_decode) {
     // Units are (token, pair). Their partials are numbered token-major in the
     // reference's order (token, routed expert in request order, ascending
     // block), which the reduction follows; the work list is pair-major, so
@@ -4315,7 +4894,7 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
       }
     }
     if (w != nunits) return FR_HIP_INVALID;   // every token routes 10 distinct experts
-    if (w > (uint32_t)kMaxPairs) return FR_HIP_INVALID;
+    if (w > (uint32_t)kMaxDecodeUnits) return FR_HIP_INVALID;
     H->hidden = hidden;
     H->burst = T;
     H->mode = mode;
@@ -4333,10 +4912,6 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
     bool with_shared = false;
     for (uint32_t t = 0; t < T; ++t) with_shared = with_shared || r->gate[t * 11 + 10] != 0.f;
     H->pad = q4kt ? 0u : combo | (with_shared ? kComboShared : 0u);
-    // F32 all-Q4_K units of a node with few owned blocks are split into
-    // items of fewer row-blocks (decode_split_kernel); the split depends on
-    // the owned blocks only, never on the burst.
-    const uint32_t split = q4kt && mode == MODE_F32 ? (nloaded <= 5 ? 4u : nloaded <= 11 ? 2u : 1u) : 1u;
     if (split > 1) {
       H->kind = KIND_DECODE_SPLIT;
       H->pad = split;
@@ -4433,7 +5008,8 @@ bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, 
   const dim3 g(grid), b(kDecodeThreads);
   // decode_q8_kernel or decode_rows_q8_kernel: double partials.
   const bool q8 = H.mode == MODE_Q8 || H.mode == MODE_Q8_256;
-  if (H.kind == KIND_DECODE_SPLIT && H.pad == 4) hipLaunchKernelGGL(decode_split_kernel<1>, g, b, 0, stream, dev_plan, S);
+  if (H.kind == KIND_DECODE_BURST) hipLaunchKernelGGL(decode_burst_kernel, g, b, 0, stream, dev_plan, S);
+  else if (H.kind == KIND_DECODE_SPLIT && H.pad == 4) hipLaunchKernelGGL(decode_split_kernel<1>, g, b, 0, stream, dev_plan, S);
   else if (H.kind == KIND_DECODE_SPLIT) hipLaunchKernelGGL(decode_split_kernel<2>, g, b, 0, stream, dev_plan, S);
   else if (H.kind == KIND_DECODE && q8) hipLaunchKernelGGL(decode_q8_kernel, g, b, 0, stream, dev_plan, S);
   else if (H.kind == KIND_DECODE) hipLaunchKernelGGL(decode_kernel, g, b, 0, stream, dev_plan, S);
@@ -4508,9 +5084,14 @@ __global__ __launch_bounds__(64) void stage_plan(const uint4* __restrict__ src, 
 // buffers (fr_hip_run), and the engine's output parity is left as it is.
 int launch(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, hipStream_t stream, bool host = false) {
   if ((size_t)H.ngroups * H.burst * H.hidden * sizeof(double) > E.partial_bytes) return FR_HIP_UNSUPPORTED;
-  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS || H.kind == KIND_DECODE_SPLIT;
+  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS || H.kind == KIND_DECODE_SPLIT ||
+                      H.kind == KIND_DECODE_BURST;
   const unsigned items = H.kind == KIND_DECODE_SPLIT ? H.npairs * H.pad : H.npairs;
   if (H.kind == KIND_DECODE_SPLIT && H.pad != 2 && H.pad != 4) return FR_HIP_INVALID;
+  // A burst plan's partials: 10 routed experts x the owned blocks per token.
+  if (H.kind == KIND_DECODE_BURST && (H.mode != MODE_F32 || H.burst < 2 || H.npairs > (unsigned)kMaxPairs ||
+                                      H.burst * 10u * (unsigned)kBlocks > (unsigned)kMaxDecodeItems))
+    return FR_HIP_INVALID;
   if (decode && (grid > (unsigned)kDecodeGridMax || grid > items || items > (unsigned)kMaxDecodeItems ||
                  H.ngroups != H.burst))
     return FR_HIP_INVALID;
@@ -4854,6 +5435,8 @@ static int open_engine(int device) {
   CK(hipMemset(E.hdstat, 0, sizeof(uint32_t)));
   E.group_bytes = (uint32_t)env_int("FRONK_HIP_GROUP_BYTES", 49152);
   E.no_decode = env_int("FRONK_HIP_NO_DECODE", 0) != 0;
+  E.no_burst = false;
+  E.force_burst = false;
   CK(hipMemset(E.done, 0, 2 * kMaxPairs * sizeof(uint32_t)));
   CK(hipMemset(E.fin, 0, 2 * kMaxRanges * sizeof(uint32_t)));
   CK(hipMemset(E.out, 0, 2 * (size_t)E.out_words * sizeof(uint32_t)));
@@ -5073,7 +5656,8 @@ int fr_hip_launch(const void* host_plan, const void* device_plan, void* stream) 
   const PlanHeader& H = *static_cast<const PlanHeader*>(host_plan);
   if (!H.burst || H.burst > (unsigned)kMaxBurst) return FR_HIP_INVALID;
   if (H.kind == KIND_LAYER ? !H.ntA || !H.ntB || H.grid != H.ntA + H.ntB
-                           : (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS && H.kind != KIND_DECODE_SPLIT) ||
+                           : (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS && H.kind != KIND_DECODE_SPLIT &&
+                              H.kind != KIND_DECODE_BURST) ||
                                  !H.grid)
     return FR_HIP_INVALID;
   return launch(static_cast<const uint8_t*>(device_plan), H, H.grid,
@@ -5136,7 +5720,8 @@ int run_once(const fr_hip_request* req, float* y, bool layer, unsigned* status_o
     hipLaunchKernelGGL(stage_plan, dim3((words + 63) / 64), dim3(64), 0, E.stream, E.plan_mapped,
                        reinterpret_cast<uint4*>(E.plan_dev), words);
   }
-  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS || H.kind == KIND_DECODE_SPLIT;
+  const bool decode = H.kind == KIND_DECODE || H.kind == KIND_DECODE_ROWS || H.kind == KIND_DECODE_SPLIT ||
+                      H.kind == KIND_DECODE_BURST;
   rc = launch(E.plan_dev, H, grid, E.stream, decode);
   if (rc) return rc;
   const size_t count = (size_t)H.burst * H.hidden;
@@ -5270,8 +5855,11 @@ int fr_hip_sample_get(fr_hip_sample* out) {
 
 int fr_hip_route(unsigned flags) {
   if (!g_open) return FR_HIP_STATE;
-  if (flags & ~(unsigned)FR_HIP_ROUTE_NO_DECODE) return FR_HIP_INVALID;
+  if (flags & ~(unsigned)(FR_HIP_ROUTE_NO_DECODE | FR_HIP_ROUTE_NO_BURST | FR_HIP_ROUTE_BURST)) return FR_HIP_INVALID;
+  if ((flags & FR_HIP_ROUTE_NO_BURST) && (flags & FR_HIP_ROUTE_BURST)) return FR_HIP_INVALID;
   E.no_decode = (flags & FR_HIP_ROUTE_NO_DECODE) != 0;
+  E.no_burst = (flags & FR_HIP_ROUTE_NO_BURST) != 0;
+  E.force_burst = (flags & FR_HIP_ROUTE_BURST) != 0;
   return FR_HIP_OK;
 }
 

@@ -157,9 +157,13 @@ int fr_hip_sample_get(fr_hip_sample *out);
  * counterpart). By default a request runs on the first kernel that covers
  * it: the decode kernels (decode_kernel / decode_rows_kernel and their
  * fixed-order reduction), then layer_kernel. FR_HIP_ROUTE_NO_DECODE sends
- * every request to layer_kernel. Applies to plans built after the call;
+ * every request to layer_kernel. Bursts of all-Q4_K units whose tokens share
+ * experts (10 T >= 2 unique experts) run one unique pair at a time on
+ * decode_burst_kernel, other bursts one (token, pair) unit at a time on
+ * decode_kernel; FR_HIP_ROUTE_NO_BURST sends every such burst to
+ * decode_kernel, FR_HIP_ROUTE_BURST every such burst to decode_burst_kernel. Applies to plans built after the call;
  * FRONK_HIP_NO_DECODE in the environment gives the value at open. */
-enum { FR_HIP_ROUTE_NO_DECODE = 2 };
+enum { FR_HIP_ROUTE_NO_DECODE = 2, FR_HIP_ROUTE_NO_BURST = 4, FR_HIP_ROUTE_BURST = 8 };
 int fr_hip_route(unsigned flags);
 
 /* Streaming-read probe for the achievable-bandwidth figure (no reference

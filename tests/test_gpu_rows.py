@@ -89,8 +89,8 @@ def test_rows_kernel_agrees_with_oracle_and_layer_kernel(eng, fmt, hidden, share
 @pytest.mark.parametrize("fmt,burst,shared_tokens", [(fa.FMT_NATIVE, 3, (1,)), (fa.FMT_Q8, 4, ()),
                                                      (fa.FMT_NATIVE, 8, (0,))])
 def test_rows_burst_rows_equal_single_token_runs(eng, fmt, burst, shared_tokens):
-    """The last case fills the unit list exactly: 8 tokens x 10 experts x 20
-    blocks plus one token's shared expert on 20 blocks = 1,620 units."""
+    """The last case: 8 tokens x 10 experts x 20 blocks plus one token's
+    shared expert on 20 blocks = 1,620 units."""
     hidden, seed = 4096, 4321 + fmt
     lay = oracle.layout(hidden, fmt)
     rng = np.random.default_rng(burst)
@@ -121,10 +121,16 @@ def test_rows_burst_rows_equal_single_token_runs(eng, fmt, burst, shared_tokens)
             eng.release(b)
 
 
-def test_rows_unit_list_overflow_falls_back_to_layer_kernel(eng):
-    """Eight tokens that all use the shared expert need 1,760 units, more than
-    the unit partials hold: the request runs on the layer kernel."""
-    hidden, fmt, seed = 4096, fa.FMT_Q8, 55
+@pytest.mark.parametrize("fmt,modes", [(fa.FMT_Q8, (fa.MODE_F32, fa.MODE_Q8)),
+                                       (fa.FMT_NATIVE, (fa.MODE_F32, fa.MODE_Q8_256))])
+def test_rows_full_burst_with_shared_expert_stays_on_decode(eng, fmt, modes):
+    """Eight tokens that all use the shared expert are the largest decode
+    request: 8 x (10 + 1) x 20 = 1,760 units. It runs on the row-format decode
+    kernel in every mode (F32 against the oracle, Q8 and the q8_256 arithmetic
+    of the AVX2 backend included), and every row equals its token run alone
+    bit for bit."""
+    hidden, seed = 4096, 55 + fmt
+    lay = oracle.layout(hidden, fmt)
     for b in range(20):
         assert eng.synthetic(b, hidden, fmt, 1, seed) == fa.OK
     try:
@@ -134,8 +140,22 @@ def test_rows_unit_list_overflow_falls_back_to_layer_kernel(eng):
         gates[:, :10] = softmax_gates(rng, 8)
         gates[:, 10] = 0.125
         x = rng.standard_normal((8, hidden)).astype(np.float32)
-        kind, _ = plan_kind(eng, 0, experts, gates, x)
-        assert kind == 0
+        for mode in modes:
+            plan, grid = eng.plan(0, experts, gates, x, mode)
+            head = np.frombuffer(plan[:80].tobytes(), np.uint32)
+            assert int(head[16]) == KIND_DECODE_ROWS and int(head[3]) == 1760, (mode, head[16], head[3])
+            print(f"full burst with shared expert fmt={fmt} mode={mode} grid={grid}", flush=True)
+            rc, y = eng.run(0, experts, gates, x, mode)
+            assert rc == fa.OK, (mode, rc)
+            if mode == fa.MODE_F32:
+                units = host_units(lay, seed, experts, True)
+                rc, ref = oracle.ref_run(units, fmt, False, oracle_request(0, experts, gates, x))
+                assert rc == 0
+                check_close(ref, y, fa.MODE_F32, ("full burst", fmt))
+            for t in range(8):
+                rc, y1 = eng.run(0, experts[t:t + 1], gates[t:t + 1], x[t:t + 1], mode)
+                assert rc == fa.OK
+                assert np.array_equal(y1[0].view(np.uint32), y[t].view(np.uint32)), (mode, t)
     finally:
         for b in range(20):
             eng.release(b)

@@ -200,11 +200,13 @@ def test_decode_kernel_and_layer_kernel_agree_with_oracle(eng, hidden):
 
 @pytest.mark.parametrize("burst", [2, 3, 4, 5, 8])
 def test_decode_burst_rows_equal_single_token_runs(eng, burst):
-    """Bursts of all-Q4_K routed requests also run on the decode kernel: each
-    (token, pair) is a unit with its own partial, and a token's units are
-    summed in the single-token order. Every row must match the oracle and be
-    bit-identical to the same token run alone (the batching property of
-    src/native.c:94-117, which the reference checks with memcmp)."""
+    """Bursts of all-Q4_K routed requests on the unit route
+    (FR_HIP_ROUTE_NO_BURST): decode_kernel with each (token, pair) a unit with
+    its own partial, a token's units summed in the single-token order. Every
+    row must match the oracle and be bit-identical to the same token run alone
+    (the batching property of src/native.c:94-117, which the reference checks
+    with memcmp). The default route of these bursts, decode_burst_kernel, is
+    tested in test_gpu_burst.py."""
     hidden, seed = 4096, 777
     lay = oracle.layout(hidden, fa.FMT_Q4KT)
     rng = np.random.default_rng(burst)
@@ -215,10 +217,12 @@ def test_decode_burst_rows_equal_single_token_runs(eng, burst):
         gates = np.zeros((burst, 11), np.float32)
         gates[:, :10] = softmax_gates(rng, burst)
         x = rng.standard_normal((burst, hidden)).astype(np.float32)
+        eng.route(fa.ROUTE_NO_BURST)
         kind, grid = plan_kind(eng, 0, experts, gates, x)
         assert kind == fa.KIND_DECODE and 0 < grid <= 256, (kind, grid)
         print(f"decode burst={burst} grid={grid}", flush=True)
         rc, y = eng.run(0, experts, gates, x, fa.MODE_F32)
+        eng.route(0)
         assert rc == fa.OK
         units = []
         for b in range(20):
@@ -234,6 +238,7 @@ def test_decode_burst_rows_equal_single_token_runs(eng, burst):
             assert rc == fa.OK
             assert np.array_equal(y1[0].view(np.uint32), y[t].view(np.uint32)), f"token {t} differs from its T=1 run"
     finally:
+        eng.route(0)
         for b in range(20):
             eng.release(b)
 
@@ -422,7 +427,13 @@ def test_split_units_for_few_blocks(eng, nblocks, split, hidden):
             eng.route(0)
         assert rc == fa.OK
         check_close(ref, y_lay, fa.MODE_F32, ("split vs layer", nblocks))
-        rc, yb = eng.run(0, burst, gates, x, fa.MODE_F32)
+        # Unsplit bursts default to decode_burst_kernel (test_gpu_burst.py);
+        # the unit route keeps burst rows bit-identical to single tokens.
+        eng.route(fa.ROUTE_NO_BURST if split == 1 else 0)
+        try:
+            rc, yb = eng.run(0, burst, gates, x, fa.MODE_F32)
+        finally:
+            eng.route(0)
         assert rc == fa.OK
         rc, refb = oracle.ref_run(units, fa.FMT_Q4KT, False, oracle_request(0, burst, gates, x))
         assert rc == 0
