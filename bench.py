@@ -445,6 +445,7 @@ def prefill_leg(fa, lib, eng, steps, warmup):
 
 
 def bench_prefill(args):
+    import torch  # noqa: F401  (before the library: one HIP runtime)
     import fronk_amd as fa
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     steps = args.steps if args.steps is not None else 3

@@ -77,6 +77,9 @@ SIGNATURES = {
     "fr_hip_debug_quantize64": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_quantize8": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.c_uint, C.POINTER(C.c_int8),
                                          C.POINTER(C.c_float), C.POINTER(C.c_int16)]),
+    "fr_hip_debug_quantize_staged": (C.c_int, [C.POINTER(C.c_float), C.c_uint, C.c_uint, C.POINTER(C.c_float),
+                                               C.POINTER(C.c_double)]),
+    "fr_hip_debug_partials": (C.c_int, [C.c_uint, C.c_uint, C.POINTER(C.c_float)]),
     "fr_hip_debug_read": (C.c_int, [C.c_uint, C.c_uint64, C.c_void_p, C.c_uint64]),
 }
 
@@ -88,14 +91,11 @@ def lib():
     fallback path."""
     global _lib
     if _lib is None:
-        # torch carries its own HIP runtime (torch/lib/libamdhip64.so, soname
-        # libamdhip64.so.7). Loaded first, it also satisfies this library's
-        # dependency, so the process has one runtime; loaded after this
-        # library, torch would start a second one that finds no GPU.
-        try:
-            import torch  # noqa: F401
-        except ImportError:
-            pass
+        # The library runs on the HIP runtime it finds (its runpath: the
+        # system ROCm), like any C consumer of the backend. A process that
+        # also uses torch, which carries its own runtime of the same soname,
+        # imports torch before this call, so that one runtime serves both
+        # (bench.py and the test suite do).
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() (hipcc, gfx950)")
         L = C.CDLL(LIB_PATH)
@@ -251,6 +251,24 @@ class Engine:
         fn = lib().fr_hip_debug_quantize64 if regs else lib().fr_hip_debug_quantize
         rc = fn(fptr(x), x.size, fptr(out))
         return rc, out
+
+    def partials(self, first, count):
+        """fr_hip_debug_partials: items [first, first + count) of the last F32
+        decode launch, [count][4096] in output order."""
+        out = np.zeros((count, MAX_HIDDEN), np.float32)
+        check(lib().fr_hip_debug_partials(first, count, fptr(out)), "fr_hip_debug_partials")
+        return out
+
+    def quantize_staged(self, x, form):
+        """fr_q8_activation through the ref-q8 decode kernels' own staging
+        (form 0: decode_q8_kernel, 1: decode_rows_q8_kernel, 2: their h
+        quantizer on 32 values): (rc, rebuilt values, exact sub-block sums)."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        sums = np.zeros(max(x.size // 32, 1), np.float64)
+        rc = lib().fr_hip_debug_quantize_staged(fptr(x), x.size, form, fptr(out),
+                                                sums.ctypes.data_as(C.POINTER(C.c_double)))
+        return rc, out, sums
 
     def quantize8(self, x, group):
         """The q8_256 quantizers on the device (the AVX2 backend's quantize8):

@@ -4469,6 +4469,65 @@ __global__ __launch_bounds__(kDecodeThreads) void debug_quantize8_x(const float*
   }
 }
 
+// fr_q8_activation as the ref-q8 decode kernels apply it, read back from
+// their LDS: x of one token (up to 4096 values) staged by stage_x_q8 into
+// decode_q8_kernel's layout (form 0) or decode_rows_q8_kernel's lane-major
+// layout (form 1), each value rebuilt from its two digits as s*k + u*r, with
+// the staged exact sum of each 32-value sub-block; or 32 h values through
+// quantize_h32 (form 2). status gets the staging's error bits.
+__global__ __launch_bounds__(kDecodeThreads) void debug_quantize_staged(const float* x, uint32_t n, uint32_t form,
+                                                                       float* out, double* sums, uint32_t* status) {
+  __shared__ __align__(16) DecodeQ8Lds L;
+  __shared__ __align__(16) RowsLds R;
+  const unsigned tid = threadIdx.x, lane = tid & 63;
+  uint32_t bad = 0;
+  if (form == 2) {
+    if (tid < 64) {
+      float* hs = L.h[0];
+      if (lane < 32) hs[lane] = x[lane];
+      __builtin_amdgcn_wave_barrier();
+      quantize_h32(hs, (int)lane);
+      if (lane < 32) out[lane] = hs[lane];
+    }
+    return;
+  }
+  const unsigned nsub = n / 32, sb = tid >> 2, q = tid & 3;
+  float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  if (sb < nsub) {
+    const float4* xs = reinterpret_cast<const float4*>(x + 32 * sb + 8 * q);
+    xv[0] = xs[0];
+    xv[1] = xs[1];
+  }
+  if (form == 0) stage_x_q8(xv, 0, nsub, L, bad);
+  else stage_x_q8<RowsLds, true>(xv, 0, nsub, R, bad);
+  __syncthreads();
+  if (bad) flag(status, bad);
+  if (sb >= nsub) return;
+  uint2 k, r;
+  float ws, wu;
+  double sum;
+  if (form == 0) {
+    k = *reinterpret_cast<const uint2*>(&L.xd[0][0][sb][8 * q]);
+    r = *reinterpret_cast<const uint2*>(&L.xd[0][1][sb][8 * q]);
+    ws = L.xw[0][sb][0];
+    wu = L.xw[0][sb][1];
+    sum = L.xs[0][sb];
+  } else {
+    k = *reinterpret_cast<const uint2*>(&R.xl[0][sb & 1][q >> 1][sb >> 1][2 * (q & 1)]);
+    r = *reinterpret_cast<const uint2*>(&R.xl[1][sb & 1][q >> 1][sb >> 1][2 * (q & 1)]);
+    ws = R.xw[sb][0];
+    wu = R.xw[sb][1];
+    sum = R.xsd[sb];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int kd = (int8_t)((i < 4 ? k.x : k.y) >> (8 * (i & 3)));
+    const int rd = (int8_t)((i < 4 ? r.x : r.y) >> (8 * (i & 3)));
+    out[32 * sb + 8 * q + i] = (float)((double)kd * (double)ws + (double)rd * (double)wu);
+  }
+  if (q == 0) sums[sb] = sum;
+}
+
 // quantize8 of 32 h values (group 32) through the q8_256 h quantizer.
 __global__ __launch_bounds__(64) void debug_quantize8_h(const float* h, int8_t* q, float* d) {
   __shared__ float hs[32];
@@ -6000,5 +6059,54 @@ int fr_hip_debug_quantize8(const float* x, unsigned n, unsigned group, int8_t* q
   return rc;
 }
 int fr_hip_debug_quantize64(const float* x, unsigned n, float* out) { return debug_quantize_run(x, n, out, true); }
+
+int fr_hip_debug_partials(unsigned first, unsigned count, float* out) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!out || !count || first + count > (unsigned)kMaxDecodeItems || first + count < first) return FR_HIP_INVALID;
+  if (hipSetDevice(E.device) != hipSuccess || hipStreamSynchronize(E.stream) != hipSuccess) return FR_HIP_IO;
+  // Position block pb of the items sits at pb * kMaxDecodeItems + item (16
+  // floats each, partial_index); copy each block's run of items.
+  std::vector<float> blk((size_t)count * 16);
+  for (unsigned pb = 0; pb < (unsigned)kMaxHidden / 16; ++pb) {
+    const float* src = E.wgpart + ((size_t)pb * kMaxDecodeItems + first) * 16;
+    if (hipMemcpy(blk.data(), src, blk.size() * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) return FR_HIP_IO;
+    for (unsigned i = 0; i < count; ++i)
+      for (unsigned k = 0; k < 16; ++k) {
+        const unsigned p = 16 * pb + k;
+        const unsigned w = p >> 9, hh = (p >> 8) & 1, l = (p >> 2) & 63, cc = p & 3;   // decode_column
+        out[(size_t)i * kMaxHidden + 256 * (2 * w + (l >> 5)) + 8 * (l & 31) + 4 * hh + cc] = blk[16 * i + k];
+      }
+  }
+  return FR_HIP_OK;
+}
+
+int fr_hip_debug_quantize_staged(const float* x, unsigned n, unsigned form, float* out, double* sums) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!x || !out || form > 2) return FR_HIP_INVALID;
+  if (form == 2 ? n != 32 : (!sums || !n || n % 64 || n > (unsigned)kMaxHidden)) return FR_HIP_INVALID;
+  if (hipSetDevice(E.device) != hipSuccess) return FR_HIP_IO;
+  // One buffer: x, the rebuilt values, the sums, the status word.
+  const size_t xb = (size_t)n * sizeof(float), ob = xb, sb = (size_t)(n / 32) * sizeof(double);
+  uint8_t* buf = nullptr;
+  if (hipMalloc(&buf, xb + ob + sb + 16) != hipSuccess) return FR_HIP_IO;
+  float* dx = reinterpret_cast<float*>(buf);
+  float* dout = reinterpret_cast<float*>(buf + xb);
+  double* dsum = reinterpret_cast<double*>(buf + xb + ob);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(buf + xb + ob + sb);
+  uint32_t status = 0;
+  int rc = FR_HIP_OK;
+  if (hipMemcpy(dx, x, xb, hipMemcpyHostToDevice) != hipSuccess || hipMemset(dst, 0, 4) != hipSuccess) rc = FR_HIP_IO;
+  if (!rc) {
+    hipLaunchKernelGGL(debug_quantize_staged, dim3(1), dim3(kDecodeThreads), 0, E.stream, dx, n, form, dout, dsum, dst);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(E.stream) != hipSuccess ||
+        hipMemcpy(out, dout, ob, hipMemcpyDeviceToHost) != hipSuccess ||
+        (form != 2 && hipMemcpy(sums, dsum, sb, hipMemcpyDeviceToHost) != hipSuccess) ||
+        hipMemcpy(&status, dst, 4, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = FR_HIP_IO;
+  }
+  (void)hipFree(buf);
+  if (!rc && status) rc = FR_HIP_NUMERIC;
+  return rc;
+}
 
 }  // extern "C"

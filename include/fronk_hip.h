@@ -235,6 +235,21 @@ int fr_hip_debug_quantize64(const float *x, unsigned n, float *out);
  * sums s[n/32]); group 32 runs its h quantizer (n = 32; q[32], d[1]; s is not
  * written). */
 int fr_hip_debug_quantize8(const float *x, unsigned n, unsigned group, int8_t *q, float *d, int16_t *s);
+/* fr_q8_activation as the ref-q8 decode kernels apply it, read back from
+ * their LDS: form 0 stages x (n a multiple of 64, at most 4096) as
+ * decode_q8_kernel does, form 1 as decode_rows_q8_kernel does (lane-major);
+ * each value comes back rebuilt from its two staged digits (s*k + u*r) and
+ * sums[n/32] gets the staged exact sum of each 32-value sub-block. Form 2 runs
+ * the kernels' h quantizer on n = 32 values (sums unused). A non-finite x
+ * gives FR_HIP_NUMERIC, as fr_q8_activation's FR_NUMERIC. */
+int fr_hip_debug_quantize_staged(const float *x, unsigned n, unsigned form, float *out, double *sums);
+/* The fp32 partials of the last F32 decode launch on the engine's scratch
+ * (fr_hip_run or fr_hip_launch): items [first, first + count) of its token-
+ * major numbering (a token's (expert, block) units in request order, blocks
+ * ascending; split plans: unit * split + part), each as out[item][4096] in
+ * output order (columns past the hidden size are the kernel's zeros). For
+ * locating a wrong item exactly. */
+int fr_hip_debug_partials(unsigned first, unsigned count, float *out);
 /* Copy `len` re-tiled device bytes of a block, from byte `offset`. */
 int fr_hip_debug_read(unsigned block, uint64_t offset, void *out, uint64_t len);
 

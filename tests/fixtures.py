@@ -133,3 +133,23 @@ def host_units(lay, seed, layer, experts, blocks=20):
             slice_view(u, lay, layer, e)[:] = oracle.synth_slice(lay, seed, b, layer, e)
         units.append(u)
     return units
+
+
+def dense_slice(view, lay, expert):
+    """(Wg, Wu, Wd) float64 of one slice; Wd is [H x 32] in every format."""
+    H = lay.hidden
+    shared = expert == oracle.SHARED
+    gu = lay.shared_gu_type if shared else lay.gu_type
+    dn = lay.shared_down_type if shared else lay.down_type
+    row = oracle.lib().fo_row_bytes(gu, H)
+    proj = lay.shared_proj if shared else lay.proj
+    Wg = np.stack([oracle.dequant(view[n * row:(n + 1) * row], gu, H) for n in range(32)]).astype(np.float64)
+    Wu = np.stack([oracle.dequant(view[proj + n * row:proj + (n + 1) * row], gu, H) for n in range(32)]).astype(np.float64)
+    base = view[2 * proj:]
+    if not shared and lay.down_transposed:
+        drow = oracle.lib().fo_row_bytes(dn, H)
+        Wd = np.stack([oracle.dequant(base[n * drow:(n + 1) * drow], dn, H) for n in range(32)]).astype(np.float64).T
+    else:
+        drow = oracle.lib().fo_row_bytes(dn, 32)
+        Wd = np.stack([oracle.dequant(base[d * drow:(d + 1) * drow], dn, 32) for d in range(H)]).astype(np.float64)
+    return Wg, Wu, Wd

@@ -130,3 +130,50 @@ def test_quantize_bit_exact(eng):
         rc, got = eng.quantize(x)
         assert rc == fa.OK
         assert np.array_equal(got.view(np.uint32), oracle.q8_activation(x)[1].view(np.uint32))
+
+
+def test_ref_q8_decode_kernels_quantizers_bit_exact(eng):
+    """The quantizers the ref-q8 decode kernels run themselves: x staged as two
+    exact digits per value (s*k + u*r) in decode_q8_kernel's layout (form 0)
+    and decode_rows_q8_kernel's lane-major layout (form 1), with the exact sum
+    of each 32-value sub-block, and their h quantizer (form 2), each bit-exact
+    against fr_q8_activation (src/q4.c:37-61) - including a 64-value group
+    whose scale is subnormal - and a non-finite x as FR_NUMERIC. The staged
+    digits are integers, so a value the reference quantizes to -0.0 is staged
+    as k = 0 and comes back +0.0: those are compared as values (equal), every
+    other value bit for bit."""
+    import math
+    rng = np.random.default_rng(41)
+    sub = (rng.standard_normal(4096) * 1e-39).astype(np.float32)   # max/127 below 2^-126: subnormal scales
+    ties = np.zeros(4096, np.float32)
+    ties[:7] = [127, .5, 1.5, 2.5, -.5, -1.5, -2.5]
+    ties[64:66] = [254, 3]
+    ties[128] = np.finfo(np.float32).max
+    ties[192] = 2.0 ** -149
+    ties[256] = 2.0 ** -125
+    mixed = rng.standard_normal(4096).astype(np.float32)
+    mixed[640:704] *= np.float32(1e-38)
+    cases = [rng.standard_normal(4096).astype(np.float32), sub, ties, mixed,
+             (rng.standard_normal(2560) * 1e4).astype(np.float32), np.zeros(128, np.float32)]
+    for i, x in enumerate(cases):
+        rc, want = oracle.q8_activation(x)
+        assert rc == 0
+        exact = [math.fsum(want[32 * s:32 * s + 32].astype(np.float64)) for s in range(x.size // 32)]
+        for form in (0, 1):
+            print(f"staged quantizer case {i} form {form} n={x.size}", flush=True)
+            rc, got, sums = eng.quantize_staged(x, form)
+            assert rc == fa.OK, (i, form, rc)
+            nz = want != 0
+            assert np.array_equal(got[nz].view(np.uint32), want[nz].view(np.uint32)), (i, form)
+            assert np.all(got[~nz] == 0), (i, form)
+            assert np.array_equal(sums, np.array(exact)), (i, form)
+    bad = cases[0].copy()
+    bad[777] = np.nan
+    for form in (0, 1):
+        rc, _, _ = eng.quantize_staged(bad, form)
+        assert rc == fa.NUMERIC, form
+    for h in [(rng.standard_normal(32) * 1e4).astype(np.float32), ties[:32].copy(), sub[:32].copy(),
+              np.zeros(32, np.float32)]:
+        rc, got, _ = eng.quantize_staged(h, 2)
+        assert rc == fa.OK
+        assert np.array_equal(got.view(np.uint32), oracle.q8_activation(h)[1].view(np.uint32))

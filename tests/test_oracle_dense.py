@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 import oracle
-from fixtures import fill_experts, oracle_request, slice_view, softmax_gates, sparse_unit
+from fixtures import dense_slice, fill_experts, oracle_request, slice_view, softmax_gates, sparse_unit
 
 SILU1 = 1.0 / (1.0 + math.exp(-1.0))
 
@@ -81,26 +81,6 @@ def test_silu_closed_forms():
     gates[:, 0] = 0.0
     y = run_ref([u0] + [None] * 19, oracle.FMT_LEGACY, layer, experts[:1], gates[:1], x[:1])
     assert y[0, 0] == np.float32(2 * SILU1)
-
-
-def dense_slice(view, lay, expert):
-    """(Wg, Wu, Wd) float64 of one slice; Wd is [H x 32] in every format."""
-    H = lay.hidden
-    shared = expert == oracle.SHARED
-    gu = lay.shared_gu_type if shared else lay.gu_type
-    dn = lay.shared_down_type if shared else lay.down_type
-    row = oracle.lib().fo_row_bytes(gu, H)
-    proj = lay.shared_proj if shared else lay.proj
-    Wg = np.stack([oracle.dequant(view[n * row:(n + 1) * row], gu, H) for n in range(32)]).astype(np.float64)
-    Wu = np.stack([oracle.dequant(view[proj + n * row:proj + (n + 1) * row], gu, H) for n in range(32)]).astype(np.float64)
-    base = view[2 * proj:]
-    if not shared and lay.down_transposed:
-        drow = oracle.lib().fo_row_bytes(dn, H)
-        Wd = np.stack([oracle.dequant(base[n * drow:(n + 1) * drow], dn, H) for n in range(32)]).astype(np.float64).T
-    else:
-        drow = oracle.lib().fo_row_bytes(dn, 32)
-        Wd = np.stack([oracle.dequant(base[d * drow:(d + 1) * drow], dn, 32) for d in range(H)]).astype(np.float64)
-    return Wg, Wu, Wd
 
 
 def dense_run(units, lay, layer, experts, gates, x):
