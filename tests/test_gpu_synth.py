@@ -380,15 +380,19 @@ def test_ref_q8_decode_error_paths(eng):
             eng.release(b)
 
 
-@pytest.mark.parametrize("nblocks,split,hidden", [(1, 4, 4096), (3, 4, 4096), (5, 4, 4096), (6, 2, 4096),
-                                                 (11, 2, 4096), (12, 1, 4096), (1, 4, 2560), (7, 2, 2560)])
+SPLIT_GRID = [(n, 4 if n <= 5 else 2 if n <= 11 else 1, h) for h in (4096, 2560) for n in range(1, 13)]
+
+
+@pytest.mark.parametrize("nblocks,split,hidden", SPLIT_GRID)
 def test_split_units_for_few_blocks(eng, nblocks, split, hidden):
     """A node that owns at most 5 (11) blocks splits each all-Q4_K unit into
     4 (2) items of fewer row-blocks (decode_split_kernel): a single token
     against the oracle and the layer kernel, bit for bit run to run, and a
     4-token burst whose rows are bit-identical to the tokens run alone (the
-    split depends on the owned blocks only). At hidden 2560 three of the
-    eight wavefronts own no super-block."""
+    split depends on the owned blocks only). Every block count 1..12 at
+    hidden 4096 and 2560 (where three of the eight wavefronts own no
+    super-block): a regression grid over both split kernels and the
+    unsplit decode_kernel."""
     seed = 5150 + nblocks
     lay = oracle.layout(hidden, fa.FMT_Q4KT)
     rng = np.random.default_rng(nblocks)
