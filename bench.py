@@ -543,7 +543,34 @@ def run_leg(fa, lib, reqs, weight_bytes, warmup=512, samples=1024, mode=None):
             "run_tokens_per_s": round(burst * samples / (us.sum() * 1e-6), 1),
             "gbs_at_p50": round(weight_bytes / (p50 * 1e-6) / 1e9, 2),
             "timer": "perf_counter_ns around each fr_hip_run call (ctypes call included), "
-                     "512 warm-ups first (src/bench.c:352-377)"}
+                     "512 warm-ups first (src/bench.c:352-377)",
+            "phases_us": run_phases(fa, lib, call, len(prepared))}
+
+
+def run_phases(fa, lib, call, count, samples=256):
+    """The library's own phase sample of run() (fr_hip_phase_get), medians
+    over `samples` calls: the host phases without events, then the GPU phase
+    (and TOTAL - GPU) over as many calls with events around the launches."""
+    ns = (C.c_double * len(fa.PHASES))()
+    runs = C.c_uint64()
+
+    def sweep(events):
+        fa.check(lib.fr_hip_phase_events(1 if events else 0), "fr_hip_phase_events")
+        rows = []
+        for k in range(samples):
+            call(k % count)
+            fa.check(lib.fr_hip_phase_get(ns, C.byref(runs)), "fr_hip_phase_get")
+            rows.append(list(ns))
+        fa.check(lib.fr_hip_phase_events(0), "fr_hip_phase_events")
+        return np.median(np.array(rows), axis=0) * 1e-3
+
+    host, ev = sweep(False), sweep(True)
+    out = {name: round(float(host[i]), 2) for i, name in enumerate(fa.PHASES) if name in ("plan", "enqueue", "wait",
+                                                                                         "total")}
+    out.update({"gpu_with_events": round(float(ev[3]), 2), "overhead_with_events": round(float(ev[4]), 2),
+                "total_with_events": round(float(ev[5]), 2), "samples": samples,
+                "source": "fr_hip_phase_get medians (host clock; GPU phase from two HIP events, a second pass)"})
+    return out
 
 
 class Launches:

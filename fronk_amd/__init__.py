@@ -19,6 +19,8 @@ MAX_BURST, MAX_HIDDEN, BLOCKS = 8, 4096, 20
 ROUTE_NO_DECODE, ROUTE_NO_BURST, ROUTE_BURST = 2, 4, 8
 # Plan kinds (the kernel a plan runs), plan header word 16.
 KIND_LAYER, KIND_DECODE, KIND_DECODE_ROWS, KIND_DECODE_SPLIT, KIND_DECODE_BURST = 0, 1, 2, 3, 4
+# fr_hip_phase_get's phases, in order.
+PHASES = ("plan", "enqueue", "wait", "gpu", "overhead", "total")
 
 LIB_PATH = _build.HIP_LIB
 
@@ -62,6 +64,8 @@ SIGNATURES = {
     "fr_hip_last_output": (C.c_int, [C.c_void_p, C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_uint)]),
     "fr_hip_launch_static": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "fr_hip_sample_get": (C.c_int, [C.POINTER(Sample)]),
+    "fr_hip_phase_events": (C.c_int, [C.c_int]),
+    "fr_hip_phase_get": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
     "fr_hip_route": (C.c_int, [C.c_uint]),
     "fr_hip_stream_probe": (C.c_int, [C.c_void_p, C.c_uint, C.c_uint, C.c_uint, C.c_void_p, C.c_void_p]),
     "fr_hip_run_batch": (C.c_int, [C.POINTER(Batch), C.POINTER(C.c_float)]),
@@ -231,6 +235,18 @@ class Engine:
         s = Sample()
         lib().fr_hip_sample_get(C.byref(s))
         return s
+
+    def phase_events(self, on):
+        """fr_hip_phase_events: time run()'s launches with HIP events (the
+        GPU phase) from now on, or stop."""
+        check(lib().fr_hip_phase_events(1 if on else 0), "fr_hip_phase_events")
+
+    def phases(self):
+        """fr_hip_phase_get: ({phase: ns} of the last run() call, calls sampled)."""
+        ns = (C.c_double * len(PHASES))()
+        runs = C.c_uint64()
+        check(lib().fr_hip_phase_get(ns, C.byref(runs)), "fr_hip_phase_get")
+        return dict(zip(PHASES, list(ns))), runs.value
 
     def dequant(self, typ, row, n):
         out = np.zeros(n, np.float32)

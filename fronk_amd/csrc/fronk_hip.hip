@@ -29,6 +29,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <chrono>
 #include <cmath>
 #include <vector>
 
@@ -4683,6 +4684,12 @@ struct Engine {
   uint32_t last_parity = 0;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   fr_hip_sample sample = {};
+  // fr_hip_run's phase sample: the last call's phases (ns), the calls
+  // sampled, and events around its launches while phase_events is set.
+  double phase[FR_HIP_PHASES] = {};
+  uint64_t phase_runs = 0;
+  bool phase_events = false;
+  hipEvent_t pev0 = nullptr, pev1 = nullptr;
   // Launch timing (fr_hip_timing): events before, between and after the
   // kernels of each launch, for the first `timed_cap` launches.
   hipEvent_t* tev = nullptr;
@@ -5514,6 +5521,8 @@ static int open_engine(int device) {
   CK(hipHostMalloc(reinterpret_cast<void**>(&E.bstatus_host), sizeof(uint32_t), hipHostMallocDefault));
   CK(hipEventCreate(&E.ev0));
   CK(hipEventCreate(&E.ev1));
+  CK(hipEventCreate(&E.pev0));
+  CK(hipEventCreate(&E.pev1));
   CK(hipDeviceSynchronize());
   g_open = true;
   return FR_HIP_OK;
@@ -5559,6 +5568,8 @@ void release_engine() {
   (void)hipFree(E.hdstat);
   if (E.ev0) (void)hipEventDestroy(E.ev0);
   if (E.ev1) (void)hipEventDestroy(E.ev1);
+  if (E.pev0) (void)hipEventDestroy(E.pev0);
+  if (E.pev1) (void)hipEventDestroy(E.pev1);
   for (unsigned i = 0; i < 3 * E.timed_cap; ++i) (void)hipEventDestroy(E.tev[i]);
   free(E.tev);
   if (E.stream) (void)hipStreamDestroy(E.stream);
@@ -5760,14 +5771,26 @@ int fr_hip_last_output(void* stream, float* y, size_t count, unsigned* status) {
 
 // One run() call's launch; `layer` forces the layer kernel (the plan is
 // built with the decode kernels switched off).
-int run_once(const fr_hip_request* req, float* y, bool layer, unsigned* status_out) {
+double now_ns() {
+  return (double)std::chrono::duration_cast<std::chrono::nanoseconds>(
+             std::chrono::steady_clock::now().time_since_epoch())
+      .count();
+}
+
+// One attempt of fr_hip_run; adds its plan, enqueue, wait and (with
+// phase events) GPU times to ph.
+int run_once(const fr_hip_request* req, float* y, bool layer, unsigned* status_out, double (&ph)[FR_HIP_PHASES]) {
   size_t used = 0;
   unsigned grid = 0;
+  const double t0 = now_ns();
   const bool no_decode = E.no_decode;
   E.no_decode = no_decode || layer;
   int rc = build_plan(req, E.plan_host, E.plan_cap, &used, &grid);
   E.no_decode = no_decode;
   if (rc) return rc;
+  const double t1 = now_ns();
+  const bool events = E.phase_events;
+  if (events) CK(hipEventRecord(E.pev0, E.stream));
   const PlanHeader& H = *reinterpret_cast<const PlanHeader*>(E.plan_host);
   // The plan (with x) is staged into device memory by a copy kernel, then
   // the launch, then one wait. On the decode path decode_reduce writes y and
@@ -5783,6 +5806,8 @@ int run_once(const fr_hip_request* req, float* y, bool layer, unsigned* status_o
                       H.kind == KIND_DECODE_BURST;
   rc = launch(E.plan_dev, H, grid, E.stream, decode);
   if (rc) return rc;
+  if (events) CK(hipEventRecord(E.pev1, E.stream));
+  const double t2 = now_ns();
   const size_t count = (size_t)H.burst * H.hidden;
   unsigned status = 0;
   if (decode) {
@@ -5795,21 +5820,32 @@ int run_once(const fr_hip_request* req, float* y, bool layer, unsigned* status_o
   }
   ++E.sample.runs;
   *status_out = status;
-  if (status) return FR_HIP_OK;
-  memcpy(y, decode ? E.hy_host : reinterpret_cast<const float*>(E.out_host + 4), count * sizeof(float));
+  if (!status) memcpy(y, decode ? E.hy_host : reinterpret_cast<const float*>(E.out_host + 4), count * sizeof(float));
+  const double t3 = now_ns();
+  ph[FR_HIP_PHASE_PLAN] += t1 - t0;
+  ph[FR_HIP_PHASE_ENQUEUE] += t2 - t1;
+  ph[FR_HIP_PHASE_WAIT] += t3 - t2;
+  float ms = 0.f;
+  if (events && hipEventElapsedTime(&ms, E.pev0, E.pev1) == hipSuccess) ph[FR_HIP_PHASE_GPU] += (double)ms * 1e6;
   return FR_HIP_OK;
 }
 
 int fr_hip_run(const fr_hip_request* req, float* y) {
   if (!g_open) return FR_HIP_STATE;
   if (!req || !y) return FR_HIP_INVALID;
+  const double start = now_ns();
   CK(hipSetDevice(E.device));
   unsigned status = 0;
-  int rc = run_once(req, y, false, &status);
+  double ph[FR_HIP_PHASES] = {};
+  int rc = run_once(req, y, false, &status, ph);
   // A ref-q8 decode launch that met a weight the reference rounds in float
   // (and nothing else) is run again on the layer kernel.
-  if (!rc && status == kErrInexact) rc = run_once(req, y, true, &status);
+  if (!rc && status == kErrInexact) rc = run_once(req, y, true, &status, ph);
   if (rc) return rc;
+  ph[FR_HIP_PHASE_TOTAL] = now_ns() - start;
+  ph[FR_HIP_PHASE_OVERHEAD] = ph[FR_HIP_PHASE_TOTAL] - ph[FR_HIP_PHASE_GPU];
+  memcpy(E.phase, ph, sizeof(ph));
+  ++E.phase_runs;
   if (status & kErrTimeout) return FR_HIP_IO;
   if (status) return FR_HIP_NUMERIC;   // y is written only on success: untouched on failure
   return FR_HIP_OK;
@@ -5909,6 +5945,20 @@ int fr_hip_timing_read(double* main_ms, double* total_ms, unsigned* launches) {
 int fr_hip_sample_get(fr_hip_sample* out) {
   if (!out) return FR_HIP_INVALID;
   *out = E.sample;
+  return FR_HIP_OK;
+}
+
+int fr_hip_phase_events(int on) {
+  if (!g_open) return FR_HIP_STATE;
+  E.phase_events = on != 0;
+  return FR_HIP_OK;
+}
+
+int fr_hip_phase_get(double* ns, uint64_t* runs) {
+  if (!g_open) return FR_HIP_STATE;
+  if (!ns) return FR_HIP_INVALID;
+  memcpy(ns, E.phase, sizeof(E.phase));
+  if (runs) *runs = E.phase_runs;
   return FR_HIP_OK;
 }
 

@@ -153,6 +153,29 @@ int fr_hip_launch_static(const void *host_plan, const void *device_plan, float *
 
 int fr_hip_sample_get(fr_hip_sample *out);
 
+/* Phase times of the last successful fr_hip_run (its kernels ran; an
+ * FR_NUMERIC result counts), in ns, after the Metal backend's encode / queue /
+ * gpu / return sample (src/metal.h:9-15, backends/metal.m:572-585) and the
+ * AVX2 backend's probe timers (backends/avx2.c:38-42):
+ *   PLAN     host plan build (routing, gates, x into pinned memory);
+ *   ENQUEUE  the launches (plan staging copy kernel, decode kernel and its
+ *            reduction, or the layer kernel);
+ *   WAIT     from the last launch until y and the status are in host memory
+ *            and y is copied out;
+ *   GPU      device time from before the staging kernel to after the last
+ *            kernel, from two HIP events that are recorded only while
+ *            fr_hip_phase_events(1) is in force (they lengthen the call);
+ *            0 otherwise;
+ *   OVERHEAD TOTAL - GPU;
+ *   TOTAL    the whole call.
+ * A ref-q8 call repeated on the layer kernel sums both attempts. The host
+ * phases are always taken (a few clock reads per call). *runs counts the
+ * calls sampled since open. */
+enum { FR_HIP_PHASE_PLAN, FR_HIP_PHASE_ENQUEUE, FR_HIP_PHASE_WAIT, FR_HIP_PHASE_GPU, FR_HIP_PHASE_OVERHEAD,
+       FR_HIP_PHASE_TOTAL, FR_HIP_PHASES };
+int fr_hip_phase_events(int on);
+int fr_hip_phase_get(double *ns, uint64_t *runs);
+
 /* Kernel selection for comparison tests and measurements (no reference
  * counterpart). By default a request runs on the first kernel that covers
  * it: the decode kernels (decode_kernel / decode_rows_kernel and their
