@@ -26,11 +26,26 @@ stdout: exactly one JSON line. Everything else goes to stderr.
                                         tokens through fr_hip_run_batch
   python bench.py --copy-kernel BYTES   plain device copy, for scaling the
                                         FETCH_SIZE/WRITE_SIZE counters
+  python bench.py --traffic-summary FETCH WRITE COPY_FETCH COPY_WRITE
+                  --copy-kernel BYTES [--workload q4k]
+                                        (no GPU) writes
+                                        profiles/decode_<workload>_traffic.json
+                                        from four rocprofv3 --pmc output
+                                        directories: the workload's FETCH_SIZE
+                                        and WRITE_SIZE runs and the copy
+                                        kernel's; the headline line then
+                                        reports those bytes as roofline.traffic
+                                        while the kernel source is the one
+                                        counted
 """
 import argparse
 import ctypes as C
+import csv
+import glob
+import hashlib
 import json
 import os
+import re
 import sys
 import time
 
@@ -433,13 +448,11 @@ def prefill_leg(fa, lib, eng, steps, warmup):
     achieved = alg / (chunk_ms * 1e-3) / 1e9
     flops = PREFILL_LAYERS * 2.0 * PREFILL_TOKENS * 10 * SLICES * 3 * 32 * HIDDEN   # useful multiply-adds x 2
     tflops = flops / (chunk_ms * 1e-3) / 1e12
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", "prefill_traffic.json")
-    if os.path.exists(tfile):
-        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+    traffic, traffic_note = counted_traffic(os.path.join(ROOT, "profiles", "prefill_traffic.json"))
     return {
         "wall_s": wall, "steps": steps, "warmup": warmup, "weights": float(wts.sum()),
         "chunk_ms": chunk_ms, "achieved": achieved, "tflops": tflops, "traffic": traffic,
+        "traffic_note": traffic_note,
         "main_us": main_ms.value * 1e3 / counted.value, "launch_us": total_ms.value * 1e3 / counted.value,
     }, reqs[0]
 
@@ -487,7 +500,7 @@ def bench_prefill(args):
         "weight_bytes_per_chunk": m["weights"],
         "roofline": {"bound": "hbm", "achieved": round(m["achieved"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(m["achieved"] / HBM_PEAK_GBS, 4), "traffic": m["traffic"],
-                     "traffic_note": "HBM bytes per layer launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                     "traffic_note": "HBM bytes per layer launch: " + m["traffic_note"],
                      "kernel": "prefill_split + prefill_gate_up + prefill_down + prefill_reduce per layer"},
         "mfma": {"achieved": round(m["tflops"], 2), "peak": MFMA_F16_PEAK_TFLOPS,
                  "unit": "TFLOP/s (useful multiply-adds x 2 against the dense f16/bf16 matrix-core peak)",
@@ -520,6 +533,93 @@ def time_run_calls(call, count, warmup=512, samples=1024):
         call(i)
         out[k] = (clock() - t0) * 1e-3
     return out
+
+
+KERNEL_SOURCE = os.path.join(ROOT, "fronk_amd", "csrc", "fronk_hip.hip")
+
+
+def source_sha256():
+    with open(KERNEL_SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
+def counted_traffic(tfile):
+    """HBM bytes per launch from a traffic summary, or (None, why) when the
+    summary is missing or was counted on another kernel source."""
+    if not os.path.exists(tfile):
+        return None, "no counter summary"
+    t = json.load(open(tfile))
+    if t.get("kernel_source_sha256") != source_sha256():
+        return None, "counter summary taken on another kernel source"
+    return t.get("hbm_bytes_per_launch"), (f"FETCH_SIZE + WRITE_SIZE per launch, copy-calibrated, counted on kernel "
+                                           f"source sha256 {t['kernel_source_sha256'][:16]}")
+
+
+def kernel_short(name):
+    m = re.search(r"::([A-Za-z_0-9]+(?:<[^>(]*>)?)\(", name)
+    return m.group(1) if m else name.split("(")[0].strip()
+
+
+def counter_medians(d):
+    """{kernel: ({counter: median value per dispatch}, dispatches)} from a
+    rocprofv3 --pmc output directory (one row per dispatch and counter)."""
+    vals = {}
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        for row in csv.DictReader(open(f)):
+            k = vals.setdefault(kernel_short(row["Kernel_Name"]), {})
+            k.setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+    return {k: ({c: float(np.median(v)) for c, v in cs.items()}, max(len(v) for v in cs.values()))
+            for k, cs in vals.items()}
+
+
+def traffic_summary(args):
+    """profiles/decode_<workload>_traffic.json (prefill_traffic.json for the
+    prefill chunk) from the counter runs: each decode (prefill) kernel's
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch, medians), scaled by what the
+    same counters read for the copy kernel of known size; a launch is one
+    decode call (one layer of a prefill chunk: the chunk's mean)."""
+    fetch_dir, write_dir, copy_fetch, copy_write = args.traffic_summary
+    nbytes = args.copy_kernel
+    if nbytes <= 0:
+        raise SystemExit("--traffic-summary needs --copy-kernel BYTES (the size the copy runs used)")
+    cf = counter_medians(copy_fetch)["__amd_rocclr_copyBuffer"][0]["FETCH_SIZE"]
+    cw = counter_medians(copy_write)["__amd_rocclr_copyBuffer"][0]["WRITE_SIZE"]
+    fs, ws = nbytes / (cf * 1024), nbytes / (cw * 1024)
+    f, w = counter_medians(fetch_dir), counter_medians(write_dir)
+    import fronk_amd as fa
+    prefill = args.workload == "prefill"
+    if prefill:
+        text = (f"one layer launch of a prefill chunk: {PREFILL_TOKENS} tokens x {PREFILL_LAYERS} resident layers, "
+                f"top-10 of 512 uniform, {SLICES} slices, hidden {HIDDEN}, Q4_K (down transposed)")
+        prefix, per_launch = "prefill_", 1
+        slice_bytes = slice_sizes(fa, fa.FMT_Q4KT)[0]
+        routes = prefill_requests(np.random.default_rng(SEED + 5), PREFILL_LAYERS, PREFILL_TOKENS)
+        alg = (sum(len(set(r[1].ravel().tolist())) * SLICES * slice_bytes for r in routes) +
+               PREFILL_LAYERS * 8.0 * PREFILL_TOKENS * HIDDEN) / PREFILL_LAYERS
+    else:
+        spec = WORKLOADS[args.workload]
+        text, prefix, per_launch = spec["text"], "decode_", 1
+        reqs = make_requests(64, spec["burst"], spec["routing"], SEED + 1)
+        alg = np.mean([algorithmic_bytes(fa, getattr(fa, spec["fmt"]), r[1], r[2])[1] for r in reqs])
+    out = {"workload": args.workload, "text": text, "kernel_source_sha256": source_sha256(),
+           "fetch_scale": round(fs, 5), "write_scale": round(ws, 5), "copy_bytes": nbytes}
+    total = 0.0
+    for k in sorted(f):
+        if not k.startswith(prefix) or k not in w:
+            continue
+        fk, wk = f[k][0]["FETCH_SIZE"], w[k][0]["WRITE_SIZE"]
+        rd, wr = fk * 1024 * fs, wk * 1024 * ws
+        out[k] = {"fetch_kib_per_dispatch": round(fk, 1), "write_kib_per_dispatch": round(wk, 1),
+                  "fetch_bytes": int(round(rd)), "write_bytes": int(round(wr)), "dispatches": f[k][1]}
+        total += (rd + wr) * per_launch
+    out["algorithmic_bytes_per_launch"] = int(round(float(alg)))
+    out["hbm_bytes_per_launch"] = int(round(total))
+    path = os.path.join(ROOT, "profiles", "prefill_traffic.json" if prefill else
+                        f"decode_{args.workload}_traffic.json")
+    with open(path, "w") as fh:
+        json.dump(out, fh, indent=1)
+    log(f"wrote {path}: {out['hbm_bytes_per_launch']} HBM bytes per launch, "
+        f"{out['hbm_bytes_per_launch'] / out['algorithmic_bytes_per_launch']:.3f}x the algorithmic bytes")
 
 
 def run_leg(fa, lib, reqs, weight_bytes, warmup=512, samples=1024, mode=None):
@@ -868,6 +968,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' legs")
     ap.add_argument("--copy-kernel", type=int, default=0)
+    ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"))
     ap.add_argument("--blocks", type=int, default=SLICES,
                     help="owned slices of the measured leg (1..20; config 1 is 1); other values skip the other legs")
     ap.add_argument("--mode", default="f32", choices=["f32", "q8", "q8_256"],
@@ -881,6 +982,9 @@ def main():
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the layer share is built and timed on a "
               "single MI355X, and its multi-GPU sharding is a design, not a measured path.", file=sys.stderr)
         sys.exit(2)
+    if args.traffic_summary:
+        traffic_summary(args)
+        return
     if args.copy_kernel:
         copy_kernel(args.copy_kernel)
         return
@@ -949,10 +1053,9 @@ def main():
     run_rec = run_leg(fa, lib, reqs[:1024], float(L.wts[:1024].mean()), mode=mode)
     log(f"run(): p50 {run_rec['p50_us']} us p99 {run_rec['p99_us']} us")
 
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"decode_{key}_traffic.json")
-    if os.path.exists(tfile) and args.blocks == SLICES and args.mode == "f32":   # counted on that workload
-        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+    traffic, traffic_note = None, f"counted only for the default {SLICES}-slice f32 workloads"
+    if args.blocks == SLICES and args.mode == "f32":   # the counted workload
+        traffic, traffic_note = counted_traffic(os.path.join(ROOT, "profiles", f"decode_{key}_traffic.json"))
 
     scalar = None
     if not args.no_cpu:
@@ -1040,7 +1143,7 @@ def main():
         "grid": L.grid,
         "run": run_rec,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      "achievable": {"gbs": ceiling["scattered"]["gbs"],
                                     "frac_of_achievable": round(achieved / ceiling["scattered"]["gbs"], 4),
                                     "probe": ceiling, "bytes_per_call": ceiling_bytes,
