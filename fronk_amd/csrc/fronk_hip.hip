@@ -311,9 +311,14 @@ __device__ __forceinline__ T gld(const void* p) {
   return *(const __attribute__((address_space(1))) T*)(p);
 }
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) {
   const u32x4 v = gld<u32x4>(p);
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld8(const uint8_t* p) {
+  const u32x2 v = gld<u32x2>(p);
+  return make_uint2(v.x, v.y);
 }
 __device__ __forceinline__ uint32_t word(const uint4& v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
@@ -3960,13 +3965,15 @@ struct BatchSlot {                       // one (token, expert) of the chunk
   float gate;
 };
 struct BatchHeader {
-  uint32_t hidden, tokens, nslots, ntiles;
+  uint32_t hidden, tokens, nslots, ntiles;   // ntiles: routed tiles (the shared expert's follow)
   uint32_t nblk, layer, tiles_off, slots_off;
   uint32_t tokslot_off, x_off, total, experts;
-  uint64_t slice_bytes, proj;
+  uint32_t nshared, shtiles, gu, dn;         // tokens with the shared expert, its tiles; routed formats
+  uint64_t slice_bytes, proj, shared_proj;
   uint64_t base[kBlocks];                // owned slices in ascending block order: the layer's base
 };
-static_assert(sizeof(BatchHeader) == 224, "batch header layout");
+static_assert(sizeof(BatchHeader) == 248, "batch header layout");
+constexpr uint32_t kNoSlot = ~0u;        // tokslot entry of a token without the shared expert
 struct BatchScratch {
   float* h;                              // [nslots][nblk * 32] gate * h
   float* part;                           // [nslots][hidden] per-(token, expert) partials
@@ -4351,15 +4358,309 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
   if (bad) flag(S.status, bad);
 }
 
+// ---------------------------------------------- prefill, row-format units
+//
+// The native unit (Q4_K gate/up rows, MXFP4 down [H x 32], src/native.h:9-15)
+// and the shared expert of every format (Q8_0 rows, Q8_0 down [H x 32]),
+// kept in the row layout the row-format decode kernel reads (row: [chunk]
+// [16 B] halves, then the scales; a chunk is 64 columns). Same tiles, x'
+// and h scratch as prefill_gate_up / prefill_down.
+//
+// Gate/up (tile, slice): wavefront w takes row-block w%4 (the gate rows of
+// neurons 8rb..8rb+7, then their up rows) and chunks 2(w/4), 2(w/4)+1 of
+// every super-block; one v_mfma_f32_16x16x32_f16 per 32-column sub-block,
+// lane 16kg + i holding values 8kg..8kg+7 of row i: A exact in f16 (Q4_K:
+// sc*q, scaled_pair; Q8_0: q), B = x' in two f16 parts. Q4_K: the
+// super-block is scaled by d once and the min terms take one fp32 MFMA per
+// four sub-blocks, as in prefill_gate_up; Q8_0: each sub-block's product is
+// scaled by its row's d.
+__device__ __forceinline__ uint32_t int8_pair_f16(uint32_t v, uint32_t sel) {
+  // Bytes of v (signed int8) as two exact f16: 1024 + 128 + q formed in the
+  // bits, less 1152.
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const uint32_t b = __builtin_amdgcn_perm(0u, v ^ 0x80808080u, sel);   // q + 128 in each 16-bit half
+  const f16x2 f = __builtin_bit_cast(f16x2, b | 0x64006400u) - (f16x2){(_Float16)1152.f, (_Float16)1152.f};
+  return __builtin_bit_cast(uint32_t, f);
+}
+
+template <int GU>
+__global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const uint8_t* __restrict__ plan,
+                                                                         BatchScratch S, uint32_t tile0) {
+  constexpr bool kQ4 = GU == TQ4_K;
+  const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
+  // XCD-contiguous runs of the (tile, slice) list, as prefill_gate_up.
+  const unsigned nblk = H.nblk, per = gridDim.x / 8, b = blockIdx.x;
+  const unsigned j = b < 8 * per ? (b % 8) * per + b / 8 : b, brank = j % nblk;
+  const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[tile0 + j / nblk];
+  const BatchSlot* slots = reinterpret_cast<const BatchSlot*>(plan + H.slots_off) + T.slot0;
+  const unsigned hidden = H.hidden, nsb = hidden / 256, nch = hidden / 64;
+  const uint64_t proj = kQ4 ? H.proj : H.shared_proj;
+  const uint8_t* slice = reinterpret_cast<const uint8_t*>(H.base[brank] + (uint64_t)T.expert * H.slice_bytes);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const unsigned rb = (unsigned)wave & 3, p = (unsigned)wave >> 2, kg = (unsigned)lane >> 4,
+                 col = (unsigned)lane & 15, i = col;
+  __shared__ __align__(16) GateUpLds L;
+  // x' staging, as prefill_gate_up: thread -> token tl, 32-byte piece c.
+  const unsigned tl = (unsigned)tid >> 5, c = (unsigned)tid & 31;
+  const bool live = tl < T.ntok;
+  const size_t trow = (size_t)(live ? slots[tl].token : 0) * nsb;
+  const uint16_t* xsrc = S.xh + trow * 512 + 16 * c;
+  struct XStage {
+    uint4 d[2];
+    float s;
+  };
+  const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+  auto load_x = [&](unsigned s, XStage& X) {
+    if (live) {
+      X.d[0] = *reinterpret_cast<const uint4*>(xsrc + 512 * (size_t)s);
+      X.d[1] = *reinterpret_cast<const uint4*>(xsrc + 512 * (size_t)s + 8);
+      if (c < 8) X.s = S.dsum[(trow + s) * 8 + c];
+    }
+  };
+  auto store_x = [&](unsigned buf, const XStage& X) {
+    uint8_t* row = &L.xh[buf][2 * tl + c / 16][32 * (c % 16)];
+    *reinterpret_cast<uint4*>(row) = X.d[0];
+    *reinterpret_cast<uint4*>(row + 16) = X.d[1];
+    if (c < 8) L.xs[buf][tl][c] = X.s;
+  };
+  // The lane's row: gate (i < 8) or up row of neuron 8rb + i%8.
+  const uint8_t* row = slice + (i >> 3) * proj + (size_t)(8 * rb + (i & 7)) * (proj / kNeurons);
+  // Weights of super-block s: the lane's 8-byte pieces of chunks 4s + 2p + cc
+  // (Q4_K: half kg/2 of the chunk, both sub-blocks in its two nibbles; Q8_0:
+  // part 2J + kg/2 of each sub-block J) and its row's scales.
+  struct WStage {
+    uint2 q[2][2];   // [cc][Q4_K: unused 1 | Q8_0: sub-block J]
+    uint4 h;         // Q4_K: the super-block header; Q8_0: .x, .y = the scale pairs of the two chunks
+  };
+  auto load_w = [&](unsigned s) {
+    const unsigned sc = min(s, nsb - 1);
+    WStage W;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      const unsigned ch = 4 * sc + 2 * p + cc;
+      if (kQ4) {
+        W.q[cc][0] = ld8(row + 16 * ch + 16 * nch * (kg >> 1) + 8 * (kg & 1));
+        W.q[cc][1] = W.q[cc][0];
+      } else {
+#pragma unroll
+        for (int J = 0; J < 2; ++J) W.q[cc][J] = ld8(row + 16 * nch * (2 * J + (kg >> 1)) + 16 * ch + 8 * (kg & 1));
+      }
+    }
+    if (kQ4) {
+      W.h = ld16(row + 32 * nch + 16 * sc);
+    } else {
+      const uint2 sp = ld8(row + 64 * nch + 4 * (4 * sc + 2 * p));
+      W.h = make_uint4(sp.x, sp.y, 0u, 0u);
+    }
+    return W;
+  };
+  uint32_t bad = 0;
+  XStage xa = {{z4, z4}, 0.f}, xb = {{z4, z4}, 0.f};
+  load_x(0, xa);
+  WStage wcur = load_w(0), wnxt = load_w(1);
+  store_x(0, xa);
+  if (1 < nsb) load_x(1, xa);
+  __syncthreads();
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  f32x4 cmin = {0.f, 0.f, 0.f, 0.f};
+  for (unsigned s = 0; s < nsb; ++s) {
+    const unsigned buf = s & 1;
+    XStage& cur = (s & 1) ? xb : xa;   // x' of s+1 (stored at the end)
+    XStage& nxt = (s & 1) ? xa : xb;
+    if (s + 2 < nsb) load_x(s + 2, nxt);
+    const WStage W = wcur;
+    wcur = wnxt;
+    wnxt = load_w(s + 2);
+    f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
+    uint32_t scs[2][2] = {{0u, 0u}, {0u, 0u}};
+    if (kQ4) {
+      if (half_bad(W.h.x) || half_bad(W.h.x >> 16)) bad |= kErrScale;
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+        for (int J = 0; J < 2; ++J) {
+          uint32_t mi;
+          q4k_scale_min(W.h.y, W.h.z, W.h.w, 4 * p + 2 * cc + J, scs[cc][J], mi);
+        }
+    }
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int J = 0; J < 2; ++J) {
+        const unsigned sub = 4 * p + 2 * cc + J;   // sub-block of the super-block
+        u32x4 aw;
+        if (kQ4) {
+          const uint32_t w0 = J ? nib_hi(W.q[cc][0].x) : nib_lo(W.q[cc][0].x);
+          const uint32_t w1 = J ? nib_hi(W.q[cc][0].y) : nib_lo(W.q[cc][0].y);
+          aw = u32x4{scaled_pair(w0, 0x0c010c00u, scs[cc][J]), scaled_pair(w0, 0x0c030c02u, scs[cc][J]),
+                     scaled_pair(w1, 0x0c010c00u, scs[cc][J]), scaled_pair(w1, 0x0c030c02u, scs[cc][J])};
+        } else {
+          const uint2 q = W.q[cc][J];
+          aw = u32x4{int8_pair_f16(q.x, 0x0c010c00u), int8_pair_f16(q.x, 0x0c030c02u), int8_pair_f16(q.y, 0x0c010c00u),
+                     int8_pair_f16(q.y, 0x0c030c02u)};
+        }
+        const f16x8 a = __builtin_bit_cast(f16x8, aw);
+        const uint8_t* xb8 = &L.xh[buf][2 * col][2 * (32 * sub + 8 * kg)];
+        const uint4 bh = *reinterpret_cast<const uint4*>(xb8);
+        const uint4 bl = *reinterpret_cast<const uint4*>(xb8 + kXhRow);
+        if (kQ4) {
+          c_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bh), c_hi, 0, 0, 0);
+          c_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bl), c_lo, 0, 0, 0);
+        } else {
+          // The row's Q8_0 scale of this sub-block: scales of chunk 4s+2p+cc,
+          // half J; rows 4kg..4kg+3 of the product come from those lanes.
+          const uint32_t sp = cc ? W.h.y : W.h.x;
+          const uint32_t hb = J ? sp >> 16 : sp & 0xffffu;
+          if (half_bad(hb)) bad |= kErrScale;
+          const float d = half_to_float(hb);
+          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+          const f32x4 ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bh), z, 0, 0, 0);
+          const f32x4 pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bl), z, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = fmaf(__shfl(d, (int)(4 * kg) + r, 64), ph[r] + pl[r], acc[r]);
+        }
+      }
+    if (kQ4) {
+      const float d = half_to_float(W.h.x & 0xffff);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = fmaf(__shfl(d, (int)(4 * kg) + r, 64), c_hi[r] + c_lo[r], acc[r]);
+      // Min terms of sub-blocks 4p..4p+3: A = -dmin * m of (row i, 4p + kg).
+      uint32_t sc, mi;
+      q4k_scale_min(W.h.y, W.h.z, W.h.w, 4 * p + kg, sc, mi);
+      cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-half_to_float(W.h.x >> 16) * (float)mi, L.xs[buf][col][4 * p + kg],
+                                                  cmin, 0, 0, 0);
+    }
+    if (s + 1 < nsb) store_x(buf ^ 1, cur);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    L.main[wave][4 * kg + r][col] = acc[r];
+    L.mins[wave][4 * kg + r][col] = cmin[r];
+  }
+  __syncthreads();
+  {
+    const unsigned trb = (unsigned)tid >> 7, ni = ((unsigned)tid >> 4) & 7, n = (unsigned)tid & 15;
+    if (n < T.ntok) {
+      const float sx = S.dscale[slots[n].token];
+      const float a = ((L.main[trb][ni][n] + L.mins[trb][ni][n]) + (L.main[trb + 4][ni][n] + L.mins[trb + 4][ni][n])) * sx;
+      const float u = ((L.main[trb][8 + ni][n] + L.mins[trb][8 + ni][n]) +
+                       (L.main[trb + 4][8 + ni][n] + L.mins[trb + 4][8 + ni][n])) * sx;
+      uint32_t hb = 0;
+      const float h = slots[n].gate * silu_mul_f32(a, u, hb);
+      bad |= hb;
+      S.h[(size_t)(T.slot0 + n) * (nblk * kNeurons) + kNeurons * brank + 8 * trb + ni] = h;
+    }
+  }
+  if (bad) flag(S.status, bad);
+}
+
+// Down (tile, 1024 outputs) of row-format units: output o's 32 neurons as one
+// record (MXFP4: 16 code bytes at 16o, neuron j in the low nibble of byte j,
+// 16 + j in its high nibble, E8M0 exponent at 16H + o; Q8_0: 16 int8 at 16o,
+// 16 more at 16H + 16o, the fp16 d at 32H + 2o). Wavefront w takes outputs
+// 128w..128w+127 of the workgroup's 1024, in two passes of four 16-output
+// tiles; per slice, v_mfma_f32_16x16x4_f32 over the 32 neurons (A: lane l =
+// output l%16, neuron 4j + l/16 of product j, the code's exact fp32 value;
+// B: h of neuron 4j + l/16, token l%16, from LDS), each slice's product
+// scaled by the outputs' exponents or d before it joins the sum over slices.
+struct DownRowsLds {
+  float h[kBlocks][kNeurons][kTileTokens];   // [slice][neuron][token] gate * h
+};
+template <int DN>
+__global__ __launch_bounds__(kBatchThreads, 4) void prefill_down_rows(const uint8_t* __restrict__ plan, BatchScratch S,
+                                                                      uint32_t tile0) {
+  constexpr bool kMx = DN == TMXFP4;
+  const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
+  const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[tile0 + blockIdx.x];
+  const unsigned hidden = H.hidden, nblk = H.nblk;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __shared__ __align__(16) DownRowsLds L;
+  const unsigned nh = nblk * kNeurons;
+  for (unsigned k = (unsigned)tid; k < nblk * kNeurons * kTileTokens; k += kBatchThreads) {
+    const unsigned n = k & 15, rn = k >> 4;   // rn = 32 * slice + neuron
+    L.h[rn >> 5][rn & 31][n] = n < T.ntok ? S.h[(size_t)(T.slot0 + n) * nh + rn] : 0.f;
+  }
+  __syncthreads();
+  const unsigned o0 = kDownCols * blockIdx.y + 128 * (unsigned)wave;
+  if (o0 >= hidden) return;
+  const unsigned m = (unsigned)lane & 15, kq = (unsigned)lane >> 4;
+  const uint64_t proj = kMx ? H.proj : H.shared_proj;
+  const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * proj;
+  uint32_t bad = 0;
+  for (unsigned ph = 0; ph < 2; ++ph) {
+    const unsigned ob = o0 + 64 * ph;   // the pass's first output
+    f32x4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (unsigned R = 0; R < nblk; ++R) {
+      const uint8_t* d = reinterpret_cast<const uint8_t*>(H.base[R] + eoff);
+      float bv[8];   // B of product j: h of neuron 4j + kq for token m
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) bv[jj] = L.h[R][4 * jj + kq][m];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const unsigned to = ob + 16 * t;   // the tile's first output
+        float av[8];   // A of product j: output to + m, neuron 4j + kq
+        float sc[4];   // scales of the lane's C rows: outputs to + 4kq .. +3
+        if constexpr (kMx) {
+          const uint4 rec = ld16(d + 16 * (size_t)(to + m));
+          const uint32_t e4 = gld<uint32_t>(d + 16 * (size_t)hidden + to + 4 * kq);
+          const uint32_t em = (gld<uint32_t>(d + 16 * (size_t)hidden + to + (m & ~3u)) >> (8 * (m & 3))) & 0xffu;
+          const bool mb = mx_blocks_bad(em, rec, 0u, rec);   // every lane: the screen is a ballot
+          if (kq == 0 && mb) bad |= kErrScale;
+#pragma unroll
+          for (int dw = 0; dw < 4; ++dw) {
+            const auto f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word(rec, dw) >> (8 * kq), 1.0f, 0);
+            av[dw] = f[0];       // neuron 4dw + kq (low nibble of byte 4dw + kq)
+            av[4 + dw] = f[1];   // neuron 16 + 4dw + kq
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[r] = e8m0((e4 >> (8 * r)) & 0xffu);
+        } else {
+          const uint4 q0 = ld16(d + 16 * (size_t)(to + m)), q1 = ld16(d + 16 * (size_t)hidden + 16 * (size_t)(to + m));
+#pragma unroll
+          for (int dw = 0; dw < 4; ++dw) {
+            av[dw] = (float)(int8_t)(word(q0, dw) >> (8 * kq));
+            av[4 + dw] = (float)(int8_t)(word(q1, dw) >> (8 * kq));
+          }
+          const uint2 s4 = ld8(d + 32 * (size_t)hidden + 2 * (size_t)(to + 4 * kq));
+          const uint32_t hs[4] = {s4.x & 0xffffu, s4.x >> 16, s4.y & 0xffffu, s4.y >> 16};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (half_bad(hs[r])) bad |= kErrScale;
+            sc[r] = half_to_float(hs[r]);
+          }
+        }
+        f32x4 pr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) pr = __builtin_amdgcn_mfma_f32_16x16x4f32(av[jj], bv[jj], pr, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc[r], pr[r], acc[t][r]);
+      }
+    }
+    // Lane l holds C rows 4(l/16) + r (outputs ob + 16t + 4kq + r) of token m.
+    if (m < T.ntok) {
+      float* dst = S.part + (size_t)(T.slot0 + m) * hidden + ob + 4 * kq;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        *reinterpret_cast<float4*>(dst + 16 * t) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+    }
+  }
+  if (bad) flag(S.status, bad);
+}
+
 // Token t's outputs 1024 by..+1023: its 10 expert partials in routing order,
-// summed in fp64, narrowed to fp32 with the reference's overflow rule.
+// then the shared expert's if it has one, summed in fp64, narrowed to fp32
+// with the reference's overflow rule.
 __global__ __launch_bounds__(256) void prefill_reduce(const uint8_t* __restrict__ plan, BatchScratch S) {
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
   const unsigned t = blockIdx.x, hidden = H.hidden, c = kDownCols * blockIdx.y + 4 * threadIdx.x;
   if (c >= hidden) return;
-  const uint32_t* ts = reinterpret_cast<const uint32_t*>(plan + H.tokslot_off) + 10 * (size_t)t;
+  const uint32_t* ts = reinterpret_cast<const uint32_t*>(plan + H.tokslot_off) + 11 * (size_t)t;
+  const int ne = ts[10] != kNoSlot ? 11 : 10;
   double a[4] = {0.0, 0.0, 0.0, 0.0};
-  for (int e = 0; e < 10; ++e) {
+  for (int e = 0; e < ne; ++e) {
     const float4 v = *reinterpret_cast<const float4*>(S.part + (size_t)ts[e] * hidden + c);
     a[0] += v.x;
     a[1] += v.y;
@@ -5237,7 +5538,7 @@ int fetch_output(hipStream_t s, size_t count, float* y, unsigned* status_out) {
 // ------------------------------------------------------------ prefill plan
 
 size_t batch_capacity(uint32_t tokens, uint32_t hidden) {
-  const size_t slots = (size_t)tokens * 10;
+  const size_t slots = (size_t)tokens * 11;
   return sizeof(BatchHeader) + slots * (sizeof(BatchTile) + sizeof(BatchSlot) + sizeof(uint32_t)) + 4 * 256 +
          (size_t)tokens * hidden * sizeof(float);
 }
@@ -5245,8 +5546,13 @@ size_t batch_capacity(uint32_t tokens, uint32_t hidden) {
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Tokens grouped by routed expert (ascending id), each expert's tokens in
-// ascending order, cut into tiles of at most 16; tokslot[t][e] is the slot
-// of token t's e-th expert, the order in which its partials are summed.
+// ascending order, cut into tiles of at most 16, then the tokens with the
+// shared expert (slots 10T..) in tiles of their own; tokslot[t][e] is the
+// slot of token t's e-th expert (e = 10: the shared expert, or kNoSlot), the
+// order in which its partials are summed (backends/ref.c:61-97). Every
+// loaded block has one format: Q4_K-T units (routed on prefill_gate_up /
+// prefill_down) or native units (Q4_K rows, MXFP4 down: the row-format
+// prefill kernels); the shared expert is Q8_0 in both.
 int build_batch(const fr_hip_batch* r, uint8_t* out, size_t cap, size_t* used) {
   if (!r || !out || !used || !r->expert || !r->gate || !r->x) return FR_HIP_INVALID;
   if (!r->tokens || r->tokens > (unsigned)kMaxBatchTokens || r->layer >= (unsigned)kLayers || r->mode > MODE_Q8_256)
@@ -5261,15 +5567,18 @@ int build_batch(const fr_hip_batch* r, uint8_t* out, size_t cap, size_t* used) {
     if (!E.block[b]) continue;
     const Layout& l = E.lay[b];
     if (l.hidden != hidden) return FR_HIP_INVALID;
-    if (l.gu != TQ4_KM || l.dn != TQ4_KT) return FR_HIP_UNSUPPORTED;
+    const bool kt = l.gu == TQ4_KM && l.dn == TQ4_KT, nat = l.gu == TQ4_K && l.dn == TMXFP4;
+    if (!(kt || nat) || l.shared_gu != TQ8_0 || l.shared_dn != TQ8_0) return FR_HIP_UNSUPPORTED;
+    if (l0 && (l.gu != l0->gu || l.dn != l0->dn)) return FR_HIP_UNSUPPORTED;
     if (r->layer >= E.layers[b]) return FR_HIP_STATE;
     H->base[H->nblk++] = (uint64_t)(uintptr_t)(E.block[b] + (uint64_t)r->layer * l.layer);
     l0 = &l;
   }
   if (!l0) return FR_HIP_STATE;
   std::vector<uint32_t> count(kRouted, 0), first(kRouted, 0), fill(kRouted, 0);
+  uint32_t nshared = 0;
   for (uint32_t t = 0; t < T; ++t) {
-    if (r->gate[t * 11 + 10] != 0.f) return FR_HIP_UNSUPPORTED;   // shared expert: run() serves it
+    nshared += r->gate[t * 11 + 10] != 0.f ? 1u : 0u;
     for (int e = 0; e < 10; ++e) {
       const uint16_t id = r->expert[t * 10 + e];
       if (id >= kRouted) return FR_HIP_INVALID;
@@ -5285,18 +5594,24 @@ int build_batch(const fr_hip_batch* r, uint8_t* out, size_t cap, size_t* used) {
     ntiles += (count[id] + kTileTokens - 1) / kTileTokens;
     experts += count[id] ? 1u : 0u;
   }
+  const uint32_t shtiles = (nshared + kTileTokens - 1) / kTileTokens;
   H->hidden = hidden;
   H->tokens = T;
-  H->nslots = nslots;
+  H->nslots = nslots + nshared;
   H->ntiles = ntiles;
+  H->nshared = nshared;
+  H->shtiles = shtiles;
+  H->gu = l0->gu;
+  H->dn = l0->dn;
   H->layer = r->layer;
   H->experts = experts;
   H->slice_bytes = l0->slice;
   H->proj = l0->proj;
+  H->shared_proj = l0->shared_proj;
   H->tiles_off = (uint32_t)align256(sizeof(BatchHeader));
-  H->slots_off = (uint32_t)align256(H->tiles_off + (size_t)ntiles * sizeof(BatchTile));
-  H->tokslot_off = (uint32_t)align256(H->slots_off + (size_t)nslots * sizeof(BatchSlot));
-  H->x_off = (uint32_t)align256(H->tokslot_off + (size_t)T * 10 * sizeof(uint32_t));
+  H->slots_off = (uint32_t)align256(H->tiles_off + (size_t)(ntiles + shtiles) * sizeof(BatchTile));
+  H->tokslot_off = (uint32_t)align256(H->slots_off + (size_t)H->nslots * sizeof(BatchSlot));
+  H->x_off = (uint32_t)align256(H->tokslot_off + (size_t)T * 11 * sizeof(uint32_t));
   H->total = H->x_off + T * hidden * (uint32_t)sizeof(float);
   BatchTile* tiles = reinterpret_cast<BatchTile*>(out + H->tiles_off);
   BatchSlot* slots = reinterpret_cast<BatchSlot*>(out + H->slots_off);
@@ -5307,8 +5622,15 @@ int build_batch(const fr_hip_batch* r, uint8_t* out, size_t cap, size_t* used) {
       const uint32_t s = first[id] + fill[id]++;
       slots[s].token = t;
       slots[s].gate = r->gate[t * 11 + e];
-      tokslot[t * 10 + e] = s;
+      tokslot[t * 11 + e] = s;
     }
+  for (uint32_t t = 0, k = 0; t < T; ++t) {
+    tokslot[t * 11 + 10] = kNoSlot;
+    if (r->gate[t * 11 + 10] == 0.f) continue;
+    slots[nslots + k].token = t;
+    slots[nslots + k].gate = r->gate[t * 11 + 10];
+    tokslot[t * 11 + 10] = nslots + k++;
+  }
   uint32_t k = 0;
   for (int id = 0; id < kRouted; ++id)
     for (uint32_t f = 0; f < count[id]; f += kTileTokens) {
@@ -5318,13 +5640,20 @@ int build_batch(const fr_hip_batch* r, uint8_t* out, size_t cap, size_t* used) {
       B.slot0 = first[id] + f;
       B.pad = 0;
     }
+  for (uint32_t f = 0; f < nshared; f += kTileTokens) {
+    BatchTile& B = tiles[k++];
+    B.expert = (uint32_t)kShared;
+    B.ntok = nshared - f < (uint32_t)kTileTokens ? nshared - f : (uint32_t)kTileTokens;
+    B.slot0 = nslots + f;
+    B.pad = 0;
+  }
   memcpy(out + H->x_off, r->x, (size_t)T * hidden * sizeof(float));
   *used = H->total;
   E.sample.unique_experts = experts;
   E.sample.pairs = ntiles * H->nblk;
   E.sample.grid = ntiles;
   E.sample.blocks = H->nblk;
-  E.sample.weight_bytes = (uint64_t)experts * H->nblk * l0->slice;
+  E.sample.weight_bytes = (uint64_t)experts * H->nblk * l0->slice + (nshared ? H->nblk * l0->shared_slice : 0);
   return FR_HIP_OK;
 }
 
@@ -5372,8 +5701,11 @@ int batch_scratch(const BatchHeader& H) {
 
 int batch_launch(const uint8_t* dev_plan, const BatchHeader& H, hipStream_t stream) {
   if (!H.tokens || H.tokens > (unsigned)kMaxBatchTokens || !H.ntiles || !H.nblk || H.nblk > (unsigned)kBlocks ||
-      !H.hidden || H.hidden % 256 || H.hidden > (unsigned)kMaxHidden || H.nslots != 10 * H.tokens)
+      !H.hidden || H.hidden % 256 || H.hidden > (unsigned)kMaxHidden || H.nshared > H.tokens ||
+      H.nslots != 10 * H.tokens + H.nshared || H.shtiles != (H.nshared + kTileTokens - 1) / kTileTokens)
     return FR_HIP_INVALID;
+  const bool kt = H.gu == TQ4_KM && H.dn == TQ4_KT, nat = H.gu == TQ4_K && H.dn == TMXFP4;
+  if (!kt && !nat) return FR_HIP_INVALID;
   int rc = batch_scratch(H);
   if (rc) return rc;
   BatchScratch S;
@@ -5390,8 +5722,20 @@ int batch_launch(const uint8_t* dev_plan, const BatchHeader& H, hipStream_t stre
   if (te) CK(hipEventRecord(te[0], stream));
   const unsigned ncol = (H.hidden + kDownCols - 1) / kDownCols;
   hipLaunchKernelGGL(prefill_split, dim3(H.tokens), dim3(1024), 0, stream, dev_plan, S);
-  hipLaunchKernelGGL(prefill_gate_up, dim3(H.ntiles * H.nblk), dim3(kBatchThreads), 0, stream, dev_plan, S);
-  hipLaunchKernelGGL(prefill_down, dim3(H.ntiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S);
+  if (kt) hipLaunchKernelGGL(prefill_gate_up, dim3(H.ntiles * H.nblk), dim3(kBatchThreads), 0, stream, dev_plan, S);
+  else
+    hipLaunchKernelGGL(prefill_gate_up_rows<TQ4_K>, dim3(H.ntiles * H.nblk), dim3(kBatchThreads), 0, stream, dev_plan,
+                       S, 0u);
+  if (H.shtiles)
+    hipLaunchKernelGGL(prefill_gate_up_rows<TQ8_0>, dim3(H.shtiles * H.nblk), dim3(kBatchThreads), 0, stream,
+                       dev_plan, S, H.ntiles);
+  if (kt) hipLaunchKernelGGL(prefill_down, dim3(H.ntiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S);
+  else
+    hipLaunchKernelGGL(prefill_down_rows<TMXFP4>, dim3(H.ntiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S,
+                       0u);
+  if (H.shtiles)
+    hipLaunchKernelGGL(prefill_down_rows<TQ8_0>, dim3(H.shtiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S,
+                       H.ntiles);
   if (te) CK(hipEventRecord(te[1], stream));
   hipLaunchKernelGGL(prefill_reduce, dim3(H.tokens, ncol), dim3(256), 0, stream, dev_plan, S);
   if (te) CK(hipEventRecord(te[2], stream));

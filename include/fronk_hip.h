@@ -209,14 +209,16 @@ int fr_hip_stream_probe(const void *device_pieces, unsigned count, unsigned thre
  * tokens of one layer, each with its own routing, in one launch sequence that
  * reads each routed expert's weights once for all of its tokens. Row t of y is
  * run() of token t alone (same validation of ids, FR_NUMERIC rule), within
- * the F32 tolerance. Supported: mode F32, every loaded block FR_HIP_FMT_Q4KT,
- * routed experts only (gate[t][10] == 0; otherwise FR_HIP_UNSUPPORTED and the
- * caller uses run()). tokens <= 4096. y receives tokens*hidden floats only on
- * success. */
+ * the F32 tolerance. Supported: mode F32, every loaded block FR_HIP_FMT_Q4KT or
+ * every loaded block FR_HIP_FMT_NATIVE (the reference's own units: Q4_K
+ * gate/up rows, MXFP4 down), the shared expert (gate[t][10] != 0, its Q8_0
+ * slices) on any tokens; other formats or a mix return FR_HIP_UNSUPPORTED and
+ * the caller uses run(). tokens <= 4096. y receives tokens*hidden floats only
+ * on success. */
 typedef struct {
     unsigned layer, tokens, hidden, mode;
     const uint16_t *expert;  /* [tokens][10] distinct routed ids < 512 */
-    const float *gate;       /* [tokens][11], index 10 (shared) must be 0 */
+    const float *gate;       /* [tokens][11], index 10 = shared expert 512 */
     const float *x;          /* [tokens][hidden] */
 } fr_hip_batch;
 int fr_hip_run_batch(const fr_hip_batch *req, float *y);

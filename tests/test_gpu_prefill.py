@@ -172,9 +172,6 @@ def test_prefill_error_paths(eng):
     big = experts.copy()
     big[2, 4] = 512
     assert eng.run_batch(0, big, gates, x)[0] == fa.INVALID
-    shared = gates.copy()
-    shared[5, 10] = 0.5
-    assert eng.run_batch(0, experts, shared, x)[0] == fa.UNSUPPORTED
     assert eng.run_batch(0, experts, gates, x, fa.MODE_F64)[0] == fa.UNSUPPORTED
     assert eng.run_batch(1, experts, gates, x)[0] == fa.STATE
     assert eng.run_batch(0, experts, gates, x[:, :2560])[0] == fa.INVALID
