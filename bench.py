@@ -24,6 +24,8 @@ stdout: exactly one JSON line. Everything else goes to stderr.
                   AVX2 arithmetic (either skips the other legs)
   python bench.py --workload prefill   a step is one 48-layer chunk of 512
                                         tokens through fr_hip_run_batch
+                                        (prefill_native: the reference's own
+                                        units with the shared expert)
   python bench.py --copy-kernel BYTES   plain device copy, for scaling the
                                         FETCH_SIZE/WRITE_SIZE counters
   python bench.py --traffic-summary FETCH WRITE COPY_FETCH COPY_WRITE
@@ -335,32 +337,38 @@ MFMA_F16_PEAK_TFLOPS = 2500.0   # dense f16/bf16 matrix cores (the prefill GEMMs
 PREFILL_TEXT = ("Resident node prefill: 48 layers x 512 experts x 640 intermediate x hidden 4096, all Q4_K "
                 "(down transposed, 108.7 GB in HBM); a chunk of 512 tokens, top-10 of 512 uniform per token per "
                 "layer, through fr_hip_run_batch (f16 and bf16 matrix cores on exactly split operands, fp32 accumulation)")
+PREFILL_NATIVE_TEXT = ("Resident node prefill on the reference's own units: 48 layers x 512 experts x hidden 4096, "
+                       "Q4_K gate/up rows, MXFP4 down, Q8_0 shared expert (106.7 GB in HBM); a chunk of 512 tokens, "
+                       "top-10 of 512 uniform per token per layer and the shared expert at gate 0.5 on every token, "
+                       "through fr_hip_run_batch (f16 matrix cores for gate/up, fp32 matrix cores for the downs)")
 
 
-def prefill_requests(rng, layers, tokens):
+def prefill_requests(rng, layers, tokens, shared=0.0):
     reqs = []
     for layer in range(layers):
         experts = np.argsort(rng.random((tokens, 512)), axis=1)[:, :10].astype(np.uint16)
-        reqs.append((layer, experts, softmax_gates(rng, tokens),
-                     rng.standard_normal((tokens, HIDDEN)).astype(np.float32)))
+        gates = softmax_gates(rng, tokens)
+        gates[:, 10] = shared
+        reqs.append((layer, experts, gates, rng.standard_normal((tokens, HIDDEN)).astype(np.float32)))
     return reqs
 
 
-def prefill_cpu_baseline(fa, y0, req, budget_s):
+def prefill_cpu_baseline(fa, y0, req, budget_s, fmt=None):
     """Bursts of 8 tokens of the chunk's layer 0 (the reference client's cut,
     client/fronk_client.h:41-42) through the oracle's scalar restatement of
     ref (backends/ref.c:57-98), one host thread; bytes are each burst's unique
     experts x 20 slices. The chunk's GPU rows are compared with it."""
     import oracle
     from fixtures import host_units, oracle_request
-    lay = oracle.layout(HIDDEN, fa.FMT_Q4KT)
+    fmt = fa.FMT_Q4KT if fmt is None else fmt
+    lay = oracle.layout(HIDDEN, fmt)
     layer, experts, gates, x = req
     done, seconds, wbytes, worst = 0, 0.0, 0, [0.0, 0.0, 0.0, 0.0]
     for t0 in range(0, experts.shape[0], 8):
         sl = slice(t0, t0 + 8)
         units = host_units(lay, SEED, layer, experts[sl])
         t1 = time.perf_counter()
-        rc, ref = oracle.ref_run(units, fa.FMT_Q4KT, False, oracle_request(layer, experts[sl], gates[sl], x[sl]))
+        rc, ref = oracle.ref_run(units, fmt, False, oracle_request(layer, experts[sl], gates[sl], x[sl]))
         seconds += time.perf_counter() - t1
         if rc != 0:
             raise RuntimeError(f"oracle ref_run failed with {rc}")
@@ -370,6 +378,8 @@ def prefill_cpu_baseline(fa, y0, req, budget_s):
                      max(worst[2], float(np.max(np.abs(y0[t0 + t].astype(np.float64) - ref[t])))),
                      max(worst[3], float(np.max(np.abs(ref[t]))))]
         wbytes += len(set(experts[sl].ravel().tolist())) * SLICES * lay.slice
+        if np.any(gates[sl, 10] != 0):
+            wbytes += SLICES * lay.shared_slice
         done += ref.shape[0]
         del units
         if seconds >= budget_s:
@@ -384,18 +394,21 @@ def prefill_cpu_baseline(fa, y0, req, budget_s):
     }
 
 
-def prefill_leg(fa, lib, eng, steps, warmup):
+def prefill_leg(fa, lib, eng, steps, warmup, fmt=None, shared=0.0):
     """Config 5 on the device: 48 layers x 20 blocks of synthetic Q4_K resident,
     one 512-token chunk per step through fr_hip_batch_launch, timed with
-    events on the launch stream. Returns the measures and the first layer's
-    request (for the CPU leg); the blocks stay resident for the caller."""
+    events on the launch stream (fmt: the unit format, Q4_K-T by default;
+    shared: the shared expert's gate on every token, 0 for none). Returns the
+    measures and the first layer's request (for the CPU leg); the blocks stay
+    resident for the caller."""
     import torch
+    fmt = fa.FMT_Q4KT if fmt is None else fmt
     t0 = time.perf_counter()
     for b in range(SLICES):
-        fa.check(eng.synthetic(b, HIDDEN, fa.FMT_Q4KT, PREFILL_LAYERS, SEED), "fr_hip_synthetic")
+        fa.check(eng.synthetic(b, HIDDEN, fmt, PREFILL_LAYERS, SEED), "fr_hip_synthetic")
     log(f"resident: {SLICES} blocks x {PREFILL_LAYERS} layers generated in {time.perf_counter() - t0:.1f} s")
-    reqs = prefill_requests(np.random.default_rng(SEED + 5), PREFILL_LAYERS, PREFILL_TOKENS)
-    slice_bytes = slice_sizes(fa, fa.FMT_Q4KT)[0]
+    reqs = prefill_requests(np.random.default_rng(SEED + 5), PREFILL_LAYERS, PREFILL_TOKENS, shared)
+    slice_bytes, shared_bytes = slice_sizes(fa, fmt)
     cap = lib.fr_hip_batch_plan_bytes(PREFILL_TOKENS, HIDDEN)
     stride = (cap + 255) // 256 * 256
     host = np.zeros((PREFILL_LAYERS, stride), np.uint8)
@@ -403,7 +416,7 @@ def prefill_leg(fa, lib, eng, steps, warmup):
     for i, (layer, experts, gates, x) in enumerate(reqs):
         plan = eng.batch_plan(layer, experts, gates, x)
         host[i, :plan.size] = plan
-        wts[i] = len(set(experts.ravel().tolist())) * SLICES * slice_bytes
+        wts[i] = len(set(experts.ravel().tolist())) * SLICES * slice_bytes + (SLICES * shared_bytes if shared else 0)
     dev = torch.from_numpy(host).to("cuda")
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
@@ -446,9 +459,12 @@ def prefill_leg(fa, lib, eng, steps, warmup):
 
     alg = wts.sum() + PREFILL_LAYERS * 8.0 * PREFILL_TOKENS * HIDDEN   # weights once per unique expert, x and y
     achieved = alg / (chunk_ms * 1e-3) / 1e9
-    flops = PREFILL_LAYERS * 2.0 * PREFILL_TOKENS * 10 * SLICES * 3 * 32 * HIDDEN   # useful multiply-adds x 2
+    experts_per_token = 11 if shared else 10
+    flops = PREFILL_LAYERS * 2.0 * PREFILL_TOKENS * experts_per_token * SLICES * 3 * 32 * HIDDEN   # multiply-adds x 2
     tflops = flops / (chunk_ms * 1e-3) / 1e12
-    traffic, traffic_note = counted_traffic(os.path.join(ROOT, "profiles", "prefill_traffic.json"))
+    traffic, traffic_note = None, "counted for the Q4_K-T prefill only"
+    if fmt == fa.FMT_Q4KT and not shared:
+        traffic, traffic_note = counted_traffic(os.path.join(ROOT, "profiles", "prefill_traffic.json"))
     return {
         "wall_s": wall, "steps": steps, "warmup": warmup, "weights": float(wts.sum()),
         "chunk_ms": chunk_ms, "achieved": achieved, "tflops": tflops, "traffic": traffic,
@@ -465,13 +481,15 @@ def bench_prefill(args):
     warmup = args.warmup if args.warmup is not None else 1
     lib = fa.lib()
     eng = fa.Engine(0)
-    m, req0 = prefill_leg(fa, lib, eng, steps, warmup)
+    native = args.workload == "prefill_native"
+    fmt, shared = (fa.FMT_NATIVE, 0.5) if native else (fa.FMT_Q4KT, 0.0)
+    m, req0 = prefill_leg(fa, lib, eng, steps, warmup, fmt, shared)
     cpu = None
     if not args.no_cpu:
         layer, experts, gates, x = req0
         rc, y0 = eng.run_batch(layer, experts, gates, x)
         fa.check(rc, "fr_hip_run_batch")
-        cpu = prefill_cpu_baseline(fa, y0, req0, args.cpu_seconds)
+        cpu = prefill_cpu_baseline(fa, y0, req0, args.cpu_seconds, fmt)
     for b in range(SLICES):
         eng.release(b)
     chunk_ms = m["chunk_ms"]
@@ -488,9 +506,9 @@ def bench_prefill(args):
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded device generator; Q4_K d/dmin fp16 U[1e-3,1e-2], x ~ N(0,1))",
-        "config": {"workload": PREFILL_TEXT, "hidden": HIDDEN, "experts": 512, "active_experts": 10,
-                   "slices": SLICES, "tokens": PREFILL_TOKENS, "layers": PREFILL_LAYERS, "format": "Q4KT",
-                   "mode": "f32"},
+        "config": {"workload": PREFILL_NATIVE_TEXT if native else PREFILL_TEXT, "hidden": HIDDEN, "experts": 512,
+                   "active_experts": 10, "shared_gate": shared, "slices": SLICES, "tokens": PREFILL_TOKENS,
+                   "layers": PREFILL_LAYERS, "format": "NATIVE" if native else "Q4KT", "mode": "f32"},
         "hbm_frac": round(m["weights"] * steps / m["wall_s"] / 1e9 / HBM_PEAK_GBS, 4),
         "tokens_per_s_per_layer": round(PREFILL_TOKENS / (chunk_ms * 1e-3 / PREFILL_LAYERS), 1),
         "chunk_ms": round(chunk_ms, 4),
@@ -501,7 +519,10 @@ def bench_prefill(args):
         "roofline": {"bound": "hbm", "achieved": round(m["achieved"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(m["achieved"] / HBM_PEAK_GBS, 4), "traffic": m["traffic"],
                      "traffic_note": "HBM bytes per layer launch: " + m["traffic_note"],
-                     "kernel": "prefill_split + prefill_gate_up + prefill_down + prefill_reduce per layer"},
+                     "kernel": ("prefill_split + prefill_gate_up_rows<Q4_K> + prefill_gate_up_rows<Q8_0> + "
+                                "prefill_down_rows<MXFP4> + prefill_down_rows<Q8_0> + prefill_reduce per layer"
+                                if native else
+                                "prefill_split + prefill_gate_up + prefill_down + prefill_reduce per layer")},
         "mfma": {"achieved": round(m["tflops"], 2), "peak": MFMA_F16_PEAK_TFLOPS,
                  "unit": "TFLOP/s (useful multiply-adds x 2 against the dense f16/bf16 matrix-core peak)",
                  "frac": round(m["tflops"] / MFMA_F16_PEAK_TFLOPS, 4)},
@@ -963,7 +984,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="q4k", choices=sorted(WORKLOADS) + ["prefill", "stream", "run"])
+    ap.add_argument("--workload", default="q4k",
+                    choices=sorted(WORKLOADS) + ["prefill", "prefill_native", "stream", "run"])
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' legs")
@@ -988,7 +1010,7 @@ def main():
     if args.copy_kernel:
         copy_kernel(args.copy_kernel)
         return
-    if args.workload == "prefill":
+    if args.workload in ("prefill", "prefill_native"):
         bench_prefill(args)
         return
     if args.workload == "stream":
@@ -1100,6 +1122,16 @@ def main():
             eng.release(b)
         extra["config5_prefill"] = {
             "workload": PREFILL_TEXT, "chunks": 2, "chunk_ms": round(m["chunk_ms"], 3),
+            "layer_us": round(m["chunk_ms"] * 1e3 / PREFILL_LAYERS, 2),
+            "weight_bytes_per_chunk": m["weights"], "gbs": round(m["achieved"], 1),
+            "frac": round(m["achieved"] / HBM_PEAK_GBS, 4),
+            "tokens_per_s_per_layer": round(PREFILL_TOKENS / (m["chunk_ms"] * 1e-3 / PREFILL_LAYERS), 1),
+            "algorithmic_tflops": round(m["tflops"], 2)}
+        m, _ = prefill_leg(fa, lib, eng, 2, 1, fa.FMT_NATIVE, 0.5)
+        for b in range(SLICES):
+            eng.release(b)
+        extra["config5_prefill_native"] = {
+            "workload": PREFILL_NATIVE_TEXT, "chunks": 2, "chunk_ms": round(m["chunk_ms"], 3),
             "layer_us": round(m["chunk_ms"] * 1e3 / PREFILL_LAYERS, 2),
             "weight_bytes_per_chunk": m["weights"], "gbs": round(m["achieved"], 1),
             "frac": round(m["achieved"] / HBM_PEAK_GBS, 4),

@@ -31,6 +31,7 @@
 
 #include <chrono>
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 #include "fronk_hip.h"
@@ -4457,20 +4458,19 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
   uint32_t bad = 0;
   XStage xa = {{z4, z4}, 0.f}, xb = {{z4, z4}, 0.f};
   load_x(0, xa);
-  WStage wcur = load_w(0), wnxt = load_w(1);
+  WStage wa = load_w(0), wb = load_w(1), wc = load_w(2);
   store_x(0, xa);
   if (1 < nsb) load_x(1, xa);
   __syncthreads();
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   f32x4 cmin = {0.f, 0.f, 0.f, 0.f};
-  for (unsigned s = 0; s < nsb; ++s) {
+  // Super-block s: W holds its weights (reloaded with those of s+3 once
+  // read), cur holds x' of s+1 (stored at the end), s+2 is loaded into nxt;
+  // unrolled by six so that no register set is copied while its loads are
+  // in flight (as prefill_gate_up).
+  auto step = [&](unsigned s, WStage& W, XStage& cur, XStage& nxt) {
     const unsigned buf = s & 1;
-    XStage& cur = (s & 1) ? xb : xa;   // x' of s+1 (stored at the end)
-    XStage& nxt = (s & 1) ? xa : xb;
     if (s + 2 < nsb) load_x(s + 2, nxt);
-    const WStage W = wcur;
-    wcur = wnxt;
-    wnxt = load_w(s + 2);
     f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
     uint32_t scs[2][2] = {{0u, 0u}, {0u, 0u}};
     if (kQ4) {
@@ -4530,8 +4530,17 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
       cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-half_to_float(W.h.x >> 16) * (float)mi, L.xs[buf][col][4 * p + kg],
                                                   cmin, 0, 0, 0);
     }
+    W = load_w(s + 3);
     if (s + 1 < nsb) store_x(buf ^ 1, cur);
     __syncthreads();
+  };
+  for (unsigned s = 0; s < nsb; s += 6) {
+    step(s, wa, xa, xb);
+    if (s + 1 < nsb) step(s + 1, wb, xb, xa);
+    if (s + 2 < nsb) step(s + 2, wc, xa, xb);
+    if (s + 3 < nsb) step(s + 3, wa, xb, xa);
+    if (s + 4 < nsb) step(s + 4, wb, xa, xb);
+    if (s + 5 < nsb) step(s + 5, wc, xb, xa);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -4588,44 +4597,66 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down_rows(const uint
   const uint64_t proj = kMx ? H.proj : H.shared_proj;
   const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * proj;
   uint32_t bad = 0;
+  // A slice's bytes for the pass's four tiles, one slice ahead in two
+  // register sets (the loop is unrolled by two so that neither is copied
+  // while its loads are in flight).
+  struct MxSlice {
+    uint4 rec[4];
+    uint32_t e4[4], em[4];
+  };
+  struct Q8Slice {
+    uint4 q0[4], q1[4];
+    uint2 s4[4];
+  };
+  using SliceBytes = typename std::conditional<kMx, MxSlice, Q8Slice>::type;
   for (unsigned ph = 0; ph < 2; ++ph) {
     const unsigned ob = o0 + 64 * ph;   // the pass's first output
     f32x4 acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (unsigned R = 0; R < nblk; ++R) {
-      const uint8_t* d = reinterpret_cast<const uint8_t*>(H.base[R] + eoff);
+    auto load_slice = [&](unsigned R, SliceBytes& B) {
+      const uint8_t* d = reinterpret_cast<const uint8_t*>(H.base[min(R, nblk - 1)] + eoff);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const unsigned to = ob + 16 * t;   // the tile's first output
+        if constexpr (kMx) {
+          B.rec[t] = ld16(d + 16 * (size_t)(to + m));
+          B.e4[t] = gld<uint32_t>(d + 16 * (size_t)hidden + to + 4 * kq);
+          B.em[t] = gld<uint32_t>(d + 16 * (size_t)hidden + to + (m & ~3u));
+        } else {
+          B.q0[t] = ld16(d + 16 * (size_t)(to + m));
+          B.q1[t] = ld16(d + 16 * (size_t)hidden + 16 * (size_t)(to + m));
+          B.s4[t] = ld8(d + 32 * (size_t)hidden + 2 * (size_t)(to + 4 * kq));
+        }
+      }
+    };
+    auto apply = [&](unsigned R, const SliceBytes& B) {
       float bv[8];   // B of product j: h of neuron 4j + kq for token m
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) bv[jj] = L.h[R][4 * jj + kq][m];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const unsigned to = ob + 16 * t;   // the tile's first output
-        float av[8];   // A of product j: output to + m, neuron 4j + kq
-        float sc[4];   // scales of the lane's C rows: outputs to + 4kq .. +3
+        float av[8];   // A of product j: output ob + 16t + m, neuron 4j + kq
+        float sc[4];   // scales of the lane's C rows: outputs ob + 16t + 4kq .. +3
         if constexpr (kMx) {
-          const uint4 rec = ld16(d + 16 * (size_t)(to + m));
-          const uint32_t e4 = gld<uint32_t>(d + 16 * (size_t)hidden + to + 4 * kq);
-          const uint32_t em = (gld<uint32_t>(d + 16 * (size_t)hidden + to + (m & ~3u)) >> (8 * (m & 3))) & 0xffu;
-          const bool mb = mx_blocks_bad(em, rec, 0u, rec);   // every lane: the screen is a ballot
+          const uint32_t em = (B.em[t] >> (8 * (m & 3))) & 0xffu;
+          const bool mb = mx_blocks_bad(em, B.rec[t], 0u, B.rec[t]);   // every lane: the screen is a ballot
           if (kq == 0 && mb) bad |= kErrScale;
 #pragma unroll
           for (int dw = 0; dw < 4; ++dw) {
-            const auto f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word(rec, dw) >> (8 * kq), 1.0f, 0);
+            const auto f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word(B.rec[t], dw) >> (8 * kq), 1.0f, 0);
             av[dw] = f[0];       // neuron 4dw + kq (low nibble of byte 4dw + kq)
             av[4 + dw] = f[1];   // neuron 16 + 4dw + kq
           }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sc[r] = e8m0((e4 >> (8 * r)) & 0xffu);
+          for (int r = 0; r < 4; ++r) sc[r] = e8m0((B.e4[t] >> (8 * r)) & 0xffu);
         } else {
-          const uint4 q0 = ld16(d + 16 * (size_t)(to + m)), q1 = ld16(d + 16 * (size_t)hidden + 16 * (size_t)(to + m));
 #pragma unroll
           for (int dw = 0; dw < 4; ++dw) {
-            av[dw] = (float)(int8_t)(word(q0, dw) >> (8 * kq));
-            av[4 + dw] = (float)(int8_t)(word(q1, dw) >> (8 * kq));
+            av[dw] = (float)(int8_t)(word(B.q0[t], dw) >> (8 * kq));
+            av[4 + dw] = (float)(int8_t)(word(B.q1[t], dw) >> (8 * kq));
           }
-          const uint2 s4 = ld8(d + 32 * (size_t)hidden + 2 * (size_t)(to + 4 * kq));
-          const uint32_t hs[4] = {s4.x & 0xffffu, s4.x >> 16, s4.y & 0xffffu, s4.y >> 16};
+          const uint32_t hs[4] = {B.s4[t].x & 0xffffu, B.s4[t].x >> 16, B.s4[t].y & 0xffffu, B.s4[t].y >> 16};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             if (half_bad(hs[r])) bad |= kErrScale;
@@ -4637,6 +4668,16 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down_rows(const uint
         for (int jj = 0; jj < 8; ++jj) pr = __builtin_amdgcn_mfma_f32_16x16x4f32(av[jj], bv[jj], pr, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc[r], pr[r], acc[t][r]);
+      }
+    };
+    SliceBytes sa, sb;
+    load_slice(0, sa);
+    for (unsigned R = 0; R < nblk; R += 2) {
+      load_slice(R + 1, sb);
+      apply(R, sa);
+      if (R + 1 < nblk) {
+        load_slice(R + 2, sa);
+        apply(R + 1, sb);
       }
     }
     // Lane l holds C rows 4(l/16) + r (outputs ob + 16t + 4kq + r) of token m.
