@@ -45,8 +45,8 @@ enum { FR_HIP_FMT_LEGACY = 0, FR_HIP_FMT_NATIVE = 1, FR_HIP_FMT_Q4KT = 2,
  *      codes' d and the gate; sums over units in fp64. Native units (Q4_K
  *      gate/up, MXFP4 down, Q8_0 shared expert) and all-Q8_0 units;
  *      requests on legacy Q4_0 blocks run as Q8 (that backend's legacy codes,
- *      avx2.c:83-100, are fr_q8_activation's); other formats, and requests
- *      of more than 1,620 (token, pair) units, return FR_HIP_UNSUPPORTED. */
+ *      avx2.c:83-100, are fr_q8_activation's); other formats return
+ *      FR_HIP_UNSUPPORTED. */
 enum { FR_HIP_MODE_F32 = 0, FR_HIP_MODE_F64 = 1, FR_HIP_MODE_Q8 = 2, FR_HIP_MODE_Q8_256 = 3 };
 
 /* ggml type ids accepted by the debug decoders (src/native.h:8). */
