@@ -4401,6 +4401,13 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
   const unsigned rb = (unsigned)wave & 3, p = (unsigned)wave >> 2, kg = (unsigned)lane >> 4,
                  col = (unsigned)lane & 15, i = col;
   __shared__ __align__(16) GateUpLds L;
+  // Q4_K rows, two super-blocks at a time: [row][half][8 chunks][16 B] (a row
+  // padded to 272 bytes, so that the 16 rows a read spans fall in different
+  // banks) and [row][super-block][16 B] headers; filled from registers loaded
+  // one stage ahead, each row half read as one 128-byte run.
+  constexpr unsigned kRowPad = 272;
+  __shared__ __align__(16) uint8_t WQ[kQ4 ? 64 * kRowPad : 16];
+  __shared__ __align__(16) uint4 WH[kQ4 ? 64 * 2 : 1];
   // x' staging, as prefill_gate_up: thread -> token tl, 32-byte piece c.
   const unsigned tl = (unsigned)tid >> 5, c = (unsigned)tid & 31;
   const bool live = tl < T.ntok;
@@ -4458,17 +4465,14 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
   uint32_t bad = 0;
   XStage xa = {{z4, z4}, 0.f}, xb = {{z4, z4}, 0.f};
   load_x(0, xa);
-  WStage wa = load_w(0), wb = load_w(1), wc = load_w(2);
   store_x(0, xa);
   if (1 < nsb) load_x(1, xa);
   __syncthreads();
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   f32x4 cmin = {0.f, 0.f, 0.f, 0.f};
-  // Super-block s: W holds its weights (reloaded with those of s+3 once
-  // read), cur holds x' of s+1 (stored at the end), s+2 is loaded into nxt;
-  // unrolled by six so that no register set is copied while its loads are
-  // in flight (as prefill_gate_up).
-  auto step = [&](unsigned s, WStage& W, XStage& cur, XStage& nxt) {
+  // Super-block s: W holds its weights, cur holds x' of s+1 (stored at the
+  // end), s+2 is loaded into nxt.
+  auto step = [&](unsigned s, const WStage& W, XStage& cur, XStage& nxt) {
     const unsigned buf = s & 1;
     if (s + 2 < nsb) load_x(s + 2, nxt);
     f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
@@ -4530,17 +4534,86 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
       cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-half_to_float(W.h.x >> 16) * (float)mi, L.xs[buf][col][4 * p + kg],
                                                   cmin, 0, 0, 0);
     }
-    W = load_w(s + 3);
-    if (s + 1 < nsb) store_x(buf ^ 1, cur);
+  };
+  auto finish = [&](unsigned s, const XStage& cur) {
+    if (s + 1 < nsb) store_x((s & 1) ^ 1, cur);
     __syncthreads();
   };
-  for (unsigned s = 0; s < nsb; s += 6) {
-    step(s, wa, xa, xb);
-    if (s + 1 < nsb) step(s + 1, wb, xb, xa);
-    if (s + 2 < nsb) step(s + 2, wc, xa, xb);
-    if (s + 3 < nsb) step(s + 3, wa, xb, xa);
-    if (s + 4 < nsb) step(s + 4, wb, xa, xb);
-    if (s + 5 < nsb) step(s + 5, wc, xb, xa);
+  if constexpr (kQ4) {
+    // Thread -> two 16-byte pieces of quants (piece tid + 512j: row pc/16,
+    // half (pc/8)%2, super-block (pc/4)%2 of the stage, chunk pc%4) and, for
+    // tid < 128, one header (row tid/2, super-block tid%2).
+    const unsigned rowb = (unsigned)(proj / kNeurons), half = 16 * nch;
+    auto grow = [&](unsigned r) {   // row r of the slice: gate (r%16 < 8) or up of neuron 8(r/16) + r%8
+      return slice + ((r & 15) >> 3) * proj + (size_t)(8 * (r >> 4) + (r & 7)) * rowb;
+    };
+    uint4 gq[2], gh = make_uint4(0u, 0u, 0u, 0u);
+    auto load_stage = [&](unsigned s0) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const unsigned pc = (unsigned)tid + 512 * jj, r = pc >> 4, hf = (pc >> 3) & 1;
+        const unsigned sb = min(s0 + ((pc >> 2) & 1), nsb - 1);
+        gq[jj] = ld16(grow(r) + hf * half + 16 * (4 * sb + (pc & 3)));
+      }
+      if (tid < 128) gh = ld16(grow((unsigned)tid >> 1) + 2 * half + 16 * min(s0 + ((unsigned)tid & 1), nsb - 1));
+    };
+    auto store_stage = [&]() {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const unsigned pc = (unsigned)tid + 512 * jj, r = pc >> 4, hf = (pc >> 3) & 1;
+        *reinterpret_cast<uint4*>(&WQ[kRowPad * r + 128 * hf + 16 * (pc & 7)]) = gq[jj];
+      }
+      if (tid < 128) WH[tid] = gh;
+    };
+    // The lane's weights of super-block sbl of the stage, from LDS.
+    const unsigned lrow = 16 * rb + i;
+    auto lds_w = [&](unsigned sbl) {
+      WStage W;
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        W.q[cc][0] = *reinterpret_cast<const uint2*>(
+            &WQ[kRowPad * lrow + 128 * (kg >> 1) + 16 * (4 * sbl + 2 * p + cc) + 8 * (kg & 1)]);
+        W.q[cc][1] = W.q[cc][0];
+      }
+      W.h = WH[2 * lrow + sbl];
+      return W;
+    };
+    load_stage(0);
+    for (unsigned s0 = 0; s0 < nsb; s0 += 2) {
+      store_stage();
+      if (s0 + 2 < nsb) load_stage(s0 + 2);
+      __syncthreads();   // the stage's weights are in LDS
+      {
+        XStage& cur = (s0 & 1) ? xb : xa;
+        XStage& nxt = (s0 & 1) ? xa : xb;
+        step(s0, lds_w(0), cur, nxt);
+        finish(s0, cur);
+      }
+      if (s0 + 1 < nsb) {
+        XStage& cur = ((s0 + 1) & 1) ? xb : xa;
+        XStage& nxt = ((s0 + 1) & 1) ? xa : xb;
+        step(s0 + 1, lds_w(1), cur, nxt);
+        finish(s0 + 1, cur);
+      }
+    }
+  } else {
+    // Rotating register sets, three super-blocks ahead, unrolled by six so
+    // that no set is copied while its loads are in flight (as
+    // prefill_gate_up).
+    WStage wa = load_w(0), wb = load_w(1), wc = load_w(2);
+    auto go = [&](unsigned s, WStage& W, XStage& cur, XStage& nxt) {
+      step(s, W, cur, nxt);
+      W = load_w(s + 3);
+      finish(s, cur);
+    };
+    for (unsigned s = 0; s < nsb; s += 6) {
+      go(s, wa, xa, xb);
+      if (s + 1 < nsb) go(s + 1, wb, xb, xa);
+      if (s + 2 < nsb) go(s + 2, wc, xa, xb);
+      if (s + 3 < nsb) go(s + 3, wa, xb, xa);
+      if (s + 4 < nsb) go(s + 4, wb, xa, xb);
+      if (s + 5 < nsb) go(s + 5, wc, xb, xa);
+    }
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -4569,15 +4642,20 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
 // 16 + j in its high nibble, E8M0 exponent at 16H + o; Q8_0: 16 int8 at 16o,
 // 16 more at 16H + 16o, the fp16 d at 32H + 2o). Wavefront w takes outputs
 // 128w..128w+127 of the workgroup's 1024, in two passes of four 16-output
-// tiles; per slice, v_mfma_f32_16x16x4_f32 over the 32 neurons (A: lane l =
-// output l%16, neuron 4j + l/16 of product j, the code's exact fp32 value;
-// B: h of neuron 4j + l/16, token l%16, from LDS), each slice's product
-// scaled by the outputs' exponents or d before it joins the sum over slices.
+// tiles; per slice, v_mfma_f32_16x16x32_bf16 over the 32 neurons: lane group
+// kq takes neurons 4kq + i and 16 + 4kq + i (i = 0..3), byte i of the
+// record's dword kq; A = the codes exactly in bf16 (MXFP4 by
+// v_cvt_scalef32_pk_bf16_fp4, Q8_0 the int8), B = h of those neurons for the
+// tile's tokens in three bf16 parts that sum to it (three products). Each
+// slice's product is scaled by the outputs' exponents or d before it joins
+// the sum over slices.
 struct DownRowsLds {
   float h[kBlocks][kNeurons][kTileTokens];   // [slice][neuron][token] gate * h
 };
+// The Q8_0 instantiation (the shared expert) holds twice the record bytes per
+// slice and takes two wavefronts per SIMD instead of four.
 template <int DN>
-__global__ __launch_bounds__(kBatchThreads, 4) void prefill_down_rows(const uint8_t* __restrict__ plan, BatchScratch S,
+__global__ __launch_bounds__(kBatchThreads, DN == TMXFP4 ? 4 : 2) void prefill_down_rows(const uint8_t* __restrict__ plan, BatchScratch S,
                                                                       uint32_t tile0) {
   constexpr bool kMx = DN == TMXFP4;
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
@@ -4631,30 +4709,42 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down_rows(const uint
       }
     };
     auto apply = [&](unsigned R, const SliceBytes& B) {
-      float bv[8];   // B of product j: h of neuron 4j + kq for token m
+      // B of the products: lane (kq, token m) holds neurons 4kq + i and
+      // 16 + 4kq + i in k-slots 2i, 2i+1 (i = 0..3), h split into three bf16
+      // parts that sum to it exactly; shared by the pass's four tiles.
+      float hv[8];
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) bv[jj] = L.h[R][4 * jj + kq][m];
+      for (int i = 0; i < 4; ++i) {
+        hv[2 * i] = L.h[R][4 * kq + i][m];
+        hv[2 * i + 1] = L.h[R][16 + 4 * kq + i][m];
+      }
+      bf16x8 b1, b2, b3;
+      split_bf16(hv, b1, b2, b3);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        float av[8];   // A of product j: output ob + 16t + m, neuron 4j + kq
+        // A: output ob + 16t + m, the same k-slots: byte i of record dword kq
+        // (MXFP4: its two codes; Q8_0: the int8 of q0 and of q1), exact in bf16.
+        u32x4 aw;
         float sc[4];   // scales of the lane's C rows: outputs ob + 16t + 4kq .. +3
         if constexpr (kMx) {
           const uint32_t em = (B.em[t] >> (8 * (m & 3))) & 0xffu;
           const bool mb = mx_blocks_bad(em, B.rec[t], 0u, B.rec[t]);   // every lane: the screen is a ballot
           if (kq == 0 && mb) bad |= kErrScale;
-#pragma unroll
-          for (int dw = 0; dw < 4; ++dw) {
-            const auto f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word(B.rec[t], dw) >> (8 * kq), 1.0f, 0);
-            av[dw] = f[0];       // neuron 4dw + kq (low nibble of byte 4dw + kq)
-            av[4 + dw] = f[1];   // neuron 16 + 4dw + kq
-          }
+          const uint32_t w = word(B.rec[t], (int)kq);
+          aw = u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 0)),
+                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 1)),
+                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 2)),
+                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 3))};
 #pragma unroll
           for (int r = 0; r < 4; ++r) sc[r] = e8m0((B.e4[t] >> (8 * r)) & 0xffu);
         } else {
+          const uint32_t w0 = word(B.q0[t], (int)kq), w1 = word(B.q1[t], (int)kq);
 #pragma unroll
-          for (int dw = 0; dw < 4; ++dw) {
-            av[dw] = (float)(int8_t)(word(B.q0[t], dw) >> (8 * kq));
-            av[4 + dw] = (float)(int8_t)(word(B.q1[t], dw) >> (8 * kq));
+          for (int i = 0; i < 4; ++i) {
+            // int8 -> fp32 exactly; the bf16 is its upper half.
+            const uint32_t lo = __float_as_uint((float)(int8_t)(w0 >> (8 * i)));
+            const uint32_t hi = __float_as_uint((float)(int8_t)(w1 >> (8 * i)));
+            aw[i] = (lo >> 16) | (hi & 0xffff0000u);
           }
           const uint32_t hs[4] = {B.s4[t].x & 0xffffu, B.s4[t].x >> 16, B.s4[t].y & 0xffffu, B.s4[t].y >> 16};
 #pragma unroll
@@ -4663,9 +4753,11 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down_rows(const uint
             sc[r] = half_to_float(hs[r]);
           }
         }
-        f32x4 pr = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) pr = __builtin_amdgcn_mfma_f32_16x16x4f32(av[jj], bv[jj], pr, 0, 0, 0);
+        const bf16x8 av = __builtin_bit_cast(bf16x8, aw);
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        f32x4 pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b3, z, 0, 0, 0);
+        pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b2, pr, 0, 0, 0);
+        pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, pr, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc[r], pr[r], acc[t][r]);
       }
