@@ -4637,148 +4637,221 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
   if (bad) flag(S.status, bad);
 }
 
-// Down (tile, 1024 outputs) of row-format units: output o's 32 neurons as one
-// record (MXFP4: 16 code bytes at 16o, neuron j in the low nibble of byte j,
-// 16 + j in its high nibble, E8M0 exponent at 16H + o; Q8_0: 16 int8 at 16o,
-// 16 more at 16H + 16o, the fp16 d at 32H + 2o). Wavefront w takes outputs
-// 128w..128w+127 of the workgroup's 1024, in two passes of four 16-output
-// tiles; per slice, v_mfma_f32_16x16x32_bf16 over the 32 neurons: lane group
-// kq takes neurons 4kq + i and 16 + 4kq + i (i = 0..3), byte i of the
-// record's dword kq; A = the codes exactly in bf16 (MXFP4 by
-// v_cvt_scalef32_pk_bf16_fp4, Q8_0 the int8), B = h of those neurons for the
-// tile's tokens in three bf16 parts that sum to it (three products). Each
-// slice's product is scaled by the outputs' exponents or d before it joins
-// the sum over slices.
-struct DownRowsLds {
-  float h[kBlocks][kNeurons][kTileTokens];   // [slice][neuron][token] gate * h
-};
-// The Q8_0 instantiation (the shared expert) holds twice the record bytes per
-// slice and takes two wavefronts per SIMD instead of four.
+// Down (tile, 128 kT outputs) of row-format units: output o's 32 neurons as
+// one record (MXFP4: 16 code bytes at 16o, neuron j in the low nibble of byte
+// j, 16 + j in its high nibble, E8M0 exponent at 16H + o; Q8_0: 16 int8 at
+// 16o, 16 more at 16H + 16o, the fp16 d at 32H + 2o). Wavefront w takes the
+// kT 16-output tiles from output 16 kT w of the workgroup's; per slice and
+// tile, v_mfma_f32_16x16x32_bf16 over the 32 neurons: lane group kq takes
+// neurons 4kq + i and 16 + 4kq + i (i = 0..3), byte i of the record's dword
+// kq, the one dword of the record that the lane loads. B = h of those neurons
+// for the tile's tokens in three bf16 parts that sum to it exactly (three
+// products), split once per workgroup into LDS.
+// MXFP4: A = code * 2^(e-127) of the lane's output row by
+// v_cvt_scalef32_pk_bf16_fp4, exact (a code has two significant bits, and the
+// product is a normal bf16 for e = 2..254), so the products add straight into
+// the tile's accumulators over the slices. Exponents 253..255 pass the
+// overflow screen of src/native.c:23-27 first. A slice in which some lane
+// holds an exponent below 64 (weights below 2^-63, which no real unit has)
+// is deferred to the end and taken as the exact codes with each row's
+// 2^(e-127) applied after the product, as fp32 scaling, so that no product
+// of the matrix cores comes near the subnormal range.
+// Q8_0: A = the int8 of q0 and q1 exactly; each slice's product is scaled per
+// output row by d before it joins the sum over slices.
+constexpr int kDownRowsTilesMx = 8;   // tiles per wavefront, MXFP4 (routed)
+constexpr uint32_t kMxDirect = 64;    // smallest exponent scaled inside the products
+constexpr int kDownRowsTilesQ8 = 4;   // Q8_0 (the shared expert): twice the workgroups
 template <int DN>
-__global__ __launch_bounds__(kBatchThreads, DN == TMXFP4 ? 4 : 2) void prefill_down_rows(const uint8_t* __restrict__ plan, BatchScratch S,
-                                                                      uint32_t tile0) {
+constexpr unsigned down_rows_cols() {
+  return 128u * (DN == TMXFP4 ? kDownRowsTilesMx : kDownRowsTilesQ8);
+}
+struct DownRowsLds {
+  bf16x8 b[kBlocks][3][64];   // [slice][part][lane 16kq + token m]: k-slots 2i, 2i+1 = neurons 4kq + i, 16 + 4kq + i
+};
+// The Q8_0 instantiation holds twice the record bytes per tile and takes two
+// wavefronts per SIMD instead of four.
+template <int DN>
+__global__ __launch_bounds__(kBatchThreads, DN == TMXFP4 ? 4 : 2) void prefill_down_rows(const uint8_t* __restrict__ plan,
+                                                                                          BatchScratch S,
+                                                                                          uint32_t tile0) {
   constexpr bool kMx = DN == TMXFP4;
+  constexpr int kT = kMx ? kDownRowsTilesMx : kDownRowsTilesQ8;
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
   const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[tile0 + blockIdx.x];
   const unsigned hidden = H.hidden, nblk = H.nblk;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __shared__ __align__(16) DownRowsLds L;
   const unsigned nh = nblk * kNeurons;
-  for (unsigned k = (unsigned)tid; k < nblk * kNeurons * kTileTokens; k += kBatchThreads) {
-    const unsigned n = k & 15, rn = k >> 4;   // rn = 32 * slice + neuron
-    L.h[rn >> 5][rn & 31][n] = n < T.ntok ? S.h[(size_t)(T.slot0 + n) * nh + rn] : 0.f;
+  // Item (slice R, lane 16kq + n): token n's gate * h of neurons 4kq..4kq+3
+  // and 16 + 4kq..+3, interleaved into the lane's k-slots, in three parts.
+  for (unsigned k = (unsigned)tid; k < nblk * 64; k += kBatchThreads) {
+    const unsigned R = k >> 6, ln = k & 63, kq = ln >> 4, n = ln & 15;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), c = a;
+    if (n < T.ntok) {
+      const float* src = S.h + (size_t)(T.slot0 + n) * nh + kNeurons * R + 4 * kq;
+      a = *reinterpret_cast<const float4*>(src);
+      c = *reinterpret_cast<const float4*>(src + 16);
+    }
+    const float hv[8] = {a.x, c.x, a.y, c.y, a.z, c.z, a.w, c.w};
+    bf16x8 b1, b2, b3;
+    split_bf16(hv, b1, b2, b3);
+    L.b[R][0][ln] = b1;
+    L.b[R][1][ln] = b2;
+    L.b[R][2][ln] = b3;
   }
   __syncthreads();
-  const unsigned o0 = kDownCols * blockIdx.y + 128 * (unsigned)wave;
+  const unsigned o0 = down_rows_cols<DN>() * blockIdx.y + 16 * kT * (unsigned)wave;
   if (o0 >= hidden) return;
   const unsigned m = (unsigned)lane & 15, kq = (unsigned)lane >> 4;
   const uint64_t proj = kMx ? H.proj : H.shared_proj;
   const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * proj;
+  const int nrec = (int)((kMx ? 17u : 34u) * hidden);   // the down's bytes
+  const uint32_t vw = 16 * (o0 + m) + 4 * kq;           // dword kq of output o0 + m (tile t: + 256t)
+  const uint32_t ve = 16 * hidden + o0 + (m & ~3u);    // MXFP4: the dword holding its exponent (+ 16t)
+  const uint32_t esh = 8 * (m & 3);                     // ... at this bit
+  const uint32_t vr = 16 * hidden + o0 + 4 * kq;        // MXFP4: exponents of the lane's C rows (+ 16t)
+  const uint32_t vs = 32 * hidden + 2 * (o0 + 4 * kq);  // Q8_0: d of the lane's C rows (+ 32t)
   uint32_t bad = 0;
-  // A slice's bytes for the pass's four tiles, one slice ahead in two
-  // register sets (the loop is unrolled by two so that neither is copied
-  // while its loads are in flight).
+  // A slice's bytes, one slice ahead in two register sets (the loop is
+  // unrolled by two so that neither is copied while its loads are in flight).
   struct MxSlice {
-    uint4 rec[4];
-    uint32_t e4[4], em[4];
+    uint32_t w[kT], e4[kT];
   };
   struct Q8Slice {
-    uint4 q0[4], q1[4];
-    uint2 s4[4];
+    uint32_t q0[kT], q1[kT];
+    u32x2 s[kT];
   };
   using SliceBytes = typename std::conditional<kMx, MxSlice, Q8Slice>::type;
-  for (unsigned ph = 0; ph < 2; ++ph) {
-    const unsigned ob = o0 + 64 * ph;   // the pass's first output
-    f32x4 acc[4];
+  auto load_slice = [&](unsigned R, SliceBytes& B) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(H.base[min(R, nblk - 1)] + eoff), (short)0, nrec, 0x00020000);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto load_slice = [&](unsigned R, SliceBytes& B) {
-      const uint8_t* d = reinterpret_cast<const uint8_t*>(H.base[min(R, nblk - 1)] + eoff);
+    for (int t = 0; t < kT; ++t) {
+      if constexpr (kMx) {
+        B.w[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(vw + 256 * t), 0, 0);
+        B.e4[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(ve + 16 * t), 0, 0);
+      } else {
+        B.q0[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(vw + 256 * t), 0, 0);
+        B.q1[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(16 * hidden + vw + 256 * t), 0, 0);
+        B.s[t] = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(vs + 32 * t), 0, 0);
+      }
+    }
+  };
+  f32x4 acc[kT];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const unsigned to = ob + 16 * t;   // the tile's first output
-        if constexpr (kMx) {
-          B.rec[t] = ld16(d + 16 * (size_t)(to + m));
-          B.e4[t] = gld<uint32_t>(d + 16 * (size_t)hidden + to + 4 * kq);
-          B.em[t] = gld<uint32_t>(d + 16 * (size_t)hidden + to + (m & ~3u));
-        } else {
-          B.q0[t] = ld16(d + 16 * (size_t)(to + m));
-          B.q1[t] = ld16(d + 16 * (size_t)hidden + 16 * (size_t)(to + m));
-          B.s4[t] = ld8(d + 32 * (size_t)hidden + 2 * (size_t)(to + 4 * kq));
+  for (int t = 0; t < kT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  uint32_t deferred = 0;   // MXFP4: slices in which some lane holds e < kMxDirect (bit R)
+  auto apply = [&](unsigned R, const SliceBytes& B) {
+    const bf16x8 b1 = L.b[R][0][lane], b2 = L.b[R][1][lane], b3 = L.b[R][2][lane];
+    if constexpr (kMx) {
+      uint32_t ev[kT];   // the exponent of the lane's output in each tile
+#pragma unroll
+      for (int t = 0; t < kT; ++t) ev[t] = (B.e4[t] >> esh) & 0xffu;
+      uint32_t lo = ev[0], hi = ev[0];
+#pragma unroll
+      for (int t = 1; t < kT; ++t) {
+        lo = min(lo, ev[t]);
+        hi = max(hi, ev[t]);
+      }
+      if (__builtin_expect(__ballot(hi >= 253u) != 0, 0)) {
+#pragma unroll
+        for (int t = 0; t < kT; ++t) {
+          // The record's screen: its four dwords lie in lanes m, m+16, m+32, m+48.
+          const uint32_t w = B.w[t], e = ev[t];
+          uint32_t ge2 = w & 0x44444444u, ge4 = w & (w >> 1) & 0x22222222u;
+          ge2 |= (uint32_t)__shfl_xor((int)ge2, 16);
+          ge2 |= (uint32_t)__shfl_xor((int)ge2, 32);
+          ge4 |= (uint32_t)__shfl_xor((int)ge4, 16);
+          ge4 |= (uint32_t)__shfl_xor((int)ge4, 32);
+          if (kq == 0 && (e == 255u || (e == 254u && ge2 != 0u) || (e == 253u && ge4 != 0u))) bad |= kErrScale;
         }
       }
-    };
-    auto apply = [&](unsigned R, const SliceBytes& B) {
-      // B of the products: lane (kq, token m) holds neurons 4kq + i and
-      // 16 + 4kq + i in k-slots 2i, 2i+1 (i = 0..3), h split into three bf16
-      // parts that sum to it exactly; shared by the pass's four tiles.
-      float hv[8];
+      if (__builtin_expect(__ballot(lo < kMxDirect) != 0, 0)) {
+        deferred |= 1u << R;   // after the loop, on the exact codes
+      } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        hv[2 * i] = L.h[R][4 * kq + i][m];
-        hv[2 * i + 1] = L.h[R][16 + 4 * kq + i][m];
+        for (int t = 0; t < kT; ++t) {
+          // 2^(e-127), e = 64..255 (a block at 253..255 that overflows is flagged above).
+          const float sc = __uint_as_float(ev[t] << 23);
+          const u32x4 aw = {
+              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(B.w[t], sc, 0)),
+              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(B.w[t], sc, 1)),
+              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(B.w[t], sc, 2)),
+              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(B.w[t], sc, 3))};
+          const bf16x8 av = __builtin_bit_cast(bf16x8, aw);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b3, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b2, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, acc[t], 0, 0, 0);
+        }
       }
-      bf16x8 b1, b2, b3;
-      split_bf16(hv, b1, b2, b3);
+    } else {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        // A: output ob + 16t + m, the same k-slots: byte i of record dword kq
-        // (MXFP4: its two codes; Q8_0: the int8 of q0 and of q1), exact in bf16.
+      for (int t = 0; t < kT; ++t) {
         u32x4 aw;
-        float sc[4];   // scales of the lane's C rows: outputs ob + 16t + 4kq .. +3
-        if constexpr (kMx) {
-          const uint32_t em = (B.em[t] >> (8 * (m & 3))) & 0xffu;
-          const bool mb = mx_blocks_bad(em, B.rec[t], 0u, B.rec[t]);   // every lane: the screen is a ballot
-          if (kq == 0 && mb) bad |= kErrScale;
-          const uint32_t w = word(B.rec[t], (int)kq);
-          aw = u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 0)),
-                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 1)),
-                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 2)),
-                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 3))};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sc[r] = e8m0((B.e4[t] >> (8 * r)) & 0xffu);
-        } else {
-          const uint32_t w0 = word(B.q0[t], (int)kq), w1 = word(B.q1[t], (int)kq);
+        for (int i = 0; i < 4; ++i) {
+          // int8 -> fp32 exactly; the bf16 is its upper half.
+          const uint32_t lo = __float_as_uint((float)(int8_t)(B.q0[t] >> (8 * i)));
+          const uint32_t hi = __float_as_uint((float)(int8_t)(B.q1[t] >> (8 * i)));
+          aw[i] = (lo >> 16) | (hi & 0xffff0000u);
+        }
+        const uint32_t hs[4] = {B.s[t].x & 0xffffu, B.s[t].x >> 16, B.s[t].y & 0xffffu, B.s[t].y >> 16};
+        float sc[4];   // d of the lane's C rows: outputs o0 + 16t + 4kq .. +3
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            // int8 -> fp32 exactly; the bf16 is its upper half.
-            const uint32_t lo = __float_as_uint((float)(int8_t)(w0 >> (8 * i)));
-            const uint32_t hi = __float_as_uint((float)(int8_t)(w1 >> (8 * i)));
-            aw[i] = (lo >> 16) | (hi & 0xffff0000u);
-          }
-          const uint32_t hs[4] = {B.s4[t].x & 0xffffu, B.s4[t].x >> 16, B.s4[t].y & 0xffffu, B.s4[t].y >> 16};
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if (half_bad(hs[r])) bad |= kErrScale;
-            sc[r] = half_to_float(hs[r]);
-          }
+        for (int r = 0; r < 4; ++r) {
+          if (half_bad(hs[r])) bad |= kErrScale;
+          sc[r] = half_to_float(hs[r]);
         }
         const bf16x8 av = __builtin_bit_cast(bf16x8, aw);
-        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
         f32x4 pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b3, z, 0, 0, 0);
         pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b2, pr, 0, 0, 0);
         pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, pr, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc[r], pr[r], acc[t][r]);
       }
-    };
-    SliceBytes sa, sb;
-    load_slice(0, sa);
-    for (unsigned R = 0; R < nblk; R += 2) {
-      load_slice(R + 1, sb);
-      apply(R, sa);
-      if (R + 1 < nblk) {
-        load_slice(R + 2, sa);
-        apply(R + 1, sb);
-      }
     }
-    // Lane l holds C rows 4(l/16) + r (outputs ob + 16t + 4kq + r) of token m.
-    if (m < T.ntok) {
-      float* dst = S.part + (size_t)(T.slot0 + m) * hidden + ob + 4 * kq;
+  };
+  SliceBytes sa, sb;
+  load_slice(0, sa);
+  for (unsigned R = 0; R < nblk; R += 2) {
+    load_slice(R + 1, sb);
+    apply(R, sa);
+    if (R + 1 < nblk) {
+      load_slice(R + 2, sa);
+      apply(R + 1, sb);
+    }
+  }
+  // The deferred MXFP4 slices: the exact codes, then each C row's 2^(e-127)
+  // (lane 16kq + m reads the exponents of outputs o0 + 16t + 4kq .. +3).
+  // Added after the other slices: a float sum in another order.
+  for (uint32_t dm = deferred; dm; dm &= dm - 1) {
+    const unsigned R = (unsigned)__builtin_ctz(dm);
+    const bf16x8 b1 = L.b[R][0][lane], b2 = L.b[R][1][lane], b3 = L.b[R][2][lane];
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(H.base[R] + eoff), (short)0, nrec, 0x00020000);
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        *reinterpret_cast<float4*>(dst + 16 * t) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+    for (int t = 0; t < kT; ++t) {
+      const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(vw + 256 * t), 0, 0);
+      const uint32_t er = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(vr + 16 * t), 0, 0);
+      const u32x4 aw = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 0)),
+                        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 1)),
+                        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 2)),
+                        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 3))};
+      const bf16x8 av = __builtin_bit_cast(bf16x8, aw);
+      f32x4 pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b3, z, 0, 0, 0);
+      pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b2, pr, 0, 0, 0);
+      pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, pr, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(e8m0((er >> (8 * r)) & 0xffu), pr[r], acc[t][r]);
     }
+  }
+  // Lane l holds C rows 4(l/16) + r (outputs o0 + 16t + 4kq + r) of token m.
+  if (m < T.ntok) {
+    float* dst = S.part + (size_t)(T.slot0 + m) * hidden + o0 + 4 * kq;
+#pragma unroll
+    for (int t = 0; t < kT; ++t)
+      *reinterpret_cast<float4*>(dst + 16 * t) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
   }
   if (bad) flag(S.status, bad);
 }
@@ -5862,13 +5935,15 @@ int batch_launch(const uint8_t* dev_plan, const BatchHeader& H, hipStream_t stre
   if (H.shtiles)
     hipLaunchKernelGGL(prefill_gate_up_rows<TQ8_0>, dim3(H.shtiles * H.nblk), dim3(kBatchThreads), 0, stream,
                        dev_plan, S, H.ntiles);
+  const unsigned ncol_mx = (H.hidden + down_rows_cols<TMXFP4>() - 1) / down_rows_cols<TMXFP4>();
+  const unsigned ncol_q8 = (H.hidden + down_rows_cols<TQ8_0>() - 1) / down_rows_cols<TQ8_0>();
   if (kt) hipLaunchKernelGGL(prefill_down, dim3(H.ntiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S);
   else
-    hipLaunchKernelGGL(prefill_down_rows<TMXFP4>, dim3(H.ntiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S,
-                       0u);
+    hipLaunchKernelGGL(prefill_down_rows<TMXFP4>, dim3(H.ntiles, ncol_mx), dim3(kBatchThreads), 0, stream, dev_plan,
+                       S, 0u);
   if (H.shtiles)
-    hipLaunchKernelGGL(prefill_down_rows<TQ8_0>, dim3(H.shtiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S,
-                       H.ntiles);
+    hipLaunchKernelGGL(prefill_down_rows<TQ8_0>, dim3(H.shtiles, ncol_q8), dim3(kBatchThreads), 0, stream, dev_plan,
+                       S, H.ntiles);
   if (te) CK(hipEventRecord(te[1], stream));
   hipLaunchKernelGGL(prefill_reduce, dim3(H.tokens, ncol), dim3(256), 0, stream, dev_plan, S);
   if (te) CK(hipEventRecord(te[2], stream));

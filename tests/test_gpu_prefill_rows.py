@@ -189,3 +189,107 @@ def test_prefill_rows_error_paths(eng):
     assert eng.synthetic(2, hidden, fa.FMT_Q4KT, 1, SEED) == fa.OK
     assert eng.run_batch(0, experts, gates, x)[0] == fa.UNSUPPORTED
     eng.release(2)
+
+
+def set_codes(view, off, e, mag_max, at=None):
+    """Block at `off` (E8M0 byte, then 16 code bytes): exponent e, every code's
+    magnitude index (code & 7) at most mag_max; with `at`, the low nibble of
+    code byte `at` exactly mag_max."""
+    view[off] = e
+    codes = view[off + 1:off + 17]
+    lo, hi = codes & 15, codes >> 4
+    lo = (lo & 8) | np.minimum(lo & 7, mag_max)
+    hi = (hi & 8) | np.minimum(hi & 7, mag_max)
+    if at is not None:
+        lo[at] = mag_max
+    view[off + 1:off + 17] = lo | (hi << 4)
+
+
+def test_prefill_rows_mx_exponent_edges(eng):
+    """MXFP4 down exponents at both ends of the E8M0 range in one routed
+    expert's slices (src/native.c:23-27), against the oracle, on tokens 0..7
+    that route to that expert alone, so that its products are all of their
+    y: every output row at exponent 0, 1, 2 or 63 (the kernel's exact slices
+    for weights below 2^-63; 0 and 1 put code values below bf16's smallest
+    normal), then at 64 or 65 (the lowest scaled inside the products); then
+    rows at 253 with codes below 4 and at 254 with codes below 2 (finite
+    weights); then 253 with a code of 4 and 254 with a code of 2, each placed
+    in a later dword of the record, give FR_NUMERIC with y untouched."""
+    hidden, blocks = 2560, (0, 1)
+    lay = oracle.layout(hidden, fa.FMT_NATIVE)
+    load(eng, hidden, blocks, fa.FMT_NATIVE)
+    rng = np.random.default_rng(91)
+    pool = rng.choice(512, 30, replace=False)
+    experts, gates, x = chunk(rng, 24, hidden, pool, shared_every=2)
+    e0 = int(experts[3, 1])
+    for t in range(8):
+        experts[t] = [e0] + [int(e) for e in experts[t] if e != e0][:9]
+        gates[t] = 0.0
+        gates[t, 0] = 0.7
+    used = sorted(set(int(e) for e in experts.ravel()) | {oracle.SHARED})
+    units = [None] * 20
+    for b in blocks:
+        u = sparse_unit(lay)
+        for e in used:
+            slice_view(u, lay, 0, e)[:] = oracle.synth_slice(lay, SEED, b, 0, e)
+        units[b] = u
+    views = [slice_view(units[b], lay, 0, e0) for b in blocks]
+    goods = [v.copy() for v in views]
+    down = 2 * lay.proj
+
+    def refresh():
+        for b in blocks:
+            assert eng.refresh(b, units[b], 0, e0) == fa.OK
+
+    def against_oracle(what, small):
+        y = run_ok(eng, 0, experts, gates, x)
+        rows = []
+        for t0 in range(0, x.shape[0], 8):
+            sl = slice(t0, t0 + 8)
+            rc, ref = oracle.ref_run(units, fa.FMT_NATIVE, False, oracle_request(0, experts[sl], gates[sl], x[sl]))
+            assert rc == 0
+            rows.append(ref[:8])
+        ref = np.concatenate(rows)
+        assert np.abs(ref[:8]).max() < small   # tokens 0..7: the edited rows alone
+        check_close(ref[:8], y[:8], fa.MODE_F32, (what, "tokens 0..7"))
+        check_close(ref, y, fa.MODE_F32, what)
+        check_close(run_bursts(eng, 0, experts, gates, x), y, fa.MODE_F32, (what, "vs run"))
+
+    try:
+        for exps, small in (((0, 1, 2, 63), 1e-10), ((64, 65), 1e-9)):
+            for v in views:
+                for row in range(hidden):
+                    set_codes(v, down + 17 * row, exps[row % len(exps)], 7)
+            refresh()
+            against_oracle(f"exponents {exps}", small)
+        for v, g in zip(views, goods):
+            v[:] = g
+        for v in views:
+            for row, e, mag in ((200, 253, 5), (300, 254, 3), (301, 253, 5)):
+                set_codes(v, down + 17 * row, e, mag)
+        refresh()
+        print("prefill rows MXFP4 exponents 253, 254 finite", flush=True)
+        rc, y = eng.run_batch(0, experts, gates, x)
+        rows = []
+        for t0 in range(0, x.shape[0], 8):
+            sl = slice(t0, t0 + 8)
+            rc_ref, ref = oracle.ref_run(units, fa.FMT_NATIVE, False,
+                                         oracle_request(0, experts[sl], gates[sl], x[sl]))
+            rows.append((rc_ref, ref[:8]))
+        if all(r == 0 for r, _ in rows):
+            assert rc == fa.OK, rc
+            check_close(np.concatenate([r for _, r in rows]), y, fa.MODE_F32, "exponents 253, 254")
+        else:
+            assert rc == fa.NUMERIC and not y.any(), rc
+        for e, mag, at in ((253, 6, 9), (254, 4, 14)):
+            for v, g in zip(views, goods):
+                v[:] = g
+            set_codes(views[1], down + 17 * 40, e, mag, at)
+            refresh()
+            print(f"prefill rows MXFP4 overflow e={e} code {mag} at byte {at}", flush=True)
+            rc, yb = eng.run_batch(0, experts, gates, x)
+            assert rc == fa.NUMERIC and not yb.any(), (e, mag, at, rc)
+    finally:
+        for v, g in zip(views, goods):
+            v[:] = g
+        refresh()
