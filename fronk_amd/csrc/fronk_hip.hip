@@ -4210,14 +4210,6 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-struct DownLds {
-  float h[kBlocks][4][kTileTokens][8];   // [slice][round q][token][neuron 8q + i of the slice]
-  // [wave][slice parity][18 q + 8 g + i]: (d*sc, dmin*m) of neuron 8q + i for
-  // the pass's sub-block g; the stride of 18 puts the four rounds of a read
-  // in different banks and keeps 16-byte reads aligned.
-  float2 tab[kDecodeWaves][2][4 * 18];
-};
-
 // v as three bf16 values whose sum is v exactly (8 + 8 + 8 significant bits,
 // each residual exact in fp32).
 __device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& b1, bf16x8& b2, bf16x8& b3) {
@@ -4233,16 +4225,45 @@ __device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& b1, bf16
 }
 
 // Workgroup (tile, 1024 outputs): wavefront w takes the 128 outputs
-// 256 sb + 128 hb .. +127 (sb = 4 blockIdx.y + w/2, hb = w%2), in two passes
-// of 64. On v_mfma_f32_16x16x32_bf16 the contraction runs over the 32
-// neurons of a slice (lane group kq: neurons 8kq..8kq+7) with:
-//   A[output][neuron] = 16 + q, exact in bf16 (bits 0x4180 | q << 3), built
-//     from the Q4_K-T unit that holds the lane's output (4 outputs x 8
-//     neurons per 16-byte unit);
-//   B[neuron][token]  = h * d * sc of the output's sub-block, split into
-//     three bf16 parts that sum to it exactly (three MFMAs);
-// so C = sum (16 + q) h d sc, and the fp32 correction sum h (16 d sc + dmin m)
-// per (sub-block, token) leaves sum (d sc q - dmin m) h.
+// 256 sb + 128 hb .. +127 (sb = 4 blockIdx.y + w/2, hb = w%2), eight 16-output
+// tiles, over all owned slices. With the Q4_K-T down's weight
+// w = d sc q - dmin m (src/native.c:14-22; per neuron n a super-block over
+// the outputs, sub-block g of 32 outputs), a slice adds
+//   sum_n d_n sc_ng q_on h'_n  -  sum_n dmin_n m_ng h'_n
+// to output o of sub-block g, with h' = h * 2^-e_t (per token t of the tile,
+// e_t puts the largest |h'| in [2^12, 2^13)). The first sum runs on
+// v_mfma_f32_16x16x32_f16 over the 32 neurons (lane group kq: neurons
+// 8kq..8kq+7):
+//   A[o][n] = sc_ng * q_on in the bits of an f16 subnormal (sc q < 1024, so
+//     A = sc q 2^-24 exactly), one packed 16-bit multiply per two neurons;
+//   B[n][t] = d_n h'_nt in two f16 parts (22 significant bits), formed once
+//     per slice for the wavefront's eight tiles;
+// and the products add straight into the tiles' accumulators over the
+// slices. The second sum is fp32 FMAs per (sub-block, token). A 16-byte unit
+// holds 4 outputs x 8 neurons; each lane of a quad loads one of the four
+// units its quad's four tiles need, and the quad shares them by DPP. A slice
+// in which a neuron's |d| is 4 or more (d h' could leave f16's range; no real
+// unit has such a d) is deferred to the end and taken with B scaled down by
+// a power of two.
+constexpr float kDownDirect = 4.f;
+struct DownLds {
+  float h[kBlocks][4][kTileTokens][8];   // [slice][round q][token][neuron 8q + i]: gate * h * 2^-e_t
+  int e[kTileTokens];                    // e_t
+  // [wave][slice parity][sub-block of the pass][neuron]
+  uint16_t sc[kDecodeWaves][2][2][kNeurons];   // 6-bit scale
+  float mm[kDecodeWaves][2][2][kNeurons];      // dmin * m
+  float d[kDecodeWaves][2][kNeurons];          // d
+};
+
+// v as two f16 values hi = f16(v), lo = f16(v - hi) (v - hi is exact in fp32).
+__device__ __forceinline__ void split_f16(const float (&v)[8], f16x8& hi, f16x8& lo) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    hi[j] = (_Float16)v[j];
+    lo[j] = (_Float16)(v[j] - (float)hi[j]);
+  }
+}
+
 __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* __restrict__ plan, BatchScratch S) {
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
   const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[blockIdx.x];
@@ -4250,109 +4271,187 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __shared__ __align__(16) DownLds L;
   const unsigned nh = nblk * kNeurons;
-  for (unsigned k = (unsigned)tid; k < nblk * 4 * kTileTokens * 8; k += kBatchThreads) {
-    const unsigned i = k & 7, n = (k >> 3) & 15, rq = k >> 7;   // rq = 4 * slice + round
-    L.h[rq >> 2][rq & 3][n][i] = n < T.ntok ? S.h[(size_t)(T.slot0 + n) * nh + 8 * rq + i] : 0.f;
+  {
+    // Thread (token n, j) takes neuron j of each slice of the token's
+    // gate * h; the 32 threads of a token (one half wavefront) agree on e_t.
+    const unsigned n = (unsigned)tid >> 5, j = (unsigned)tid & 31;
+    float v[kBlocks];
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < kBlocks; ++i) {
+      v[i] = i < (int)nblk && n < T.ntok ? S.h[(size_t)(T.slot0 + n) * nh + kNeurons * i + j] : 0.f;
+      mx = fmaxf(mx, fabsf(v[i]));
+    }
+#pragma unroll
+    for (int o = 16; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    int E = 0;
+    if (mx > 0.f) (void)frexpf(mx, &E);   // mx < 2^E
+    const int e = E - 13;
+#pragma unroll
+    for (int i = 0; i < kBlocks; ++i)
+      if (i < (int)nblk) L.h[i][j >> 3][n][j & 7] = ldexpf(v[i], -e);
+    if (j == 0) L.e[n] = e;
   }
   __syncthreads();
   const unsigned sb = 4 * blockIdx.y + ((unsigned)wave >> 1), hb = (unsigned)wave & 1;
   if (sb >= nsb) return;
-  const unsigned m = (unsigned)lane & 15, kq = (unsigned)lane >> 4, n = m, c4 = m & 3;
-  const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * H.proj + 4608 * (uint64_t)sb;
-  // Header decoding: lane l forms the scales of neuron l%32 for the pass's
-  // sub-block l/32.
+  const unsigned m = (unsigned)lane & 15, kq = (unsigned)lane >> 4, qa = m >> 2, qq = m & 3;
   const unsigned hn = (unsigned)lane & 31, hgg = (unsigned)lane >> 5;
-  const uint32_t hoff = 4096 + 16 * hn;
+  const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * H.proj + 4608 * (uint64_t)sb;
+  const uint32_t shift = 4 * qq, mask = 0x000F000Fu << shift;   // the lane's output column in a unit
+  const uint32_t vh = 4096 + 16 * hn;                            // every lane: the header of neuron l%32
   uint32_t bad = 0;
   for (unsigned ph = 0; ph < 2; ++ph) {
-    // Unit of M-tile t (outputs 128hb + 64ph + 16t .. +15): lane m's output
-    // lies in unit 32hb + 16ph + 4t + m/4 of round kq, at column m%4.
-    const uint32_t ubase = 1024 * kq + 16 * (32 * hb + 16 * ph + (m >> 2));
+    // Pass ph: tiles 4ph + q (outputs 128hb + 64ph + 16q .. +15 of the
+    // super-block), sub-blocks g = 4hb + 2ph + gi. Lane (kq, qa, qq) loads
+    // unit 32hb + 16ph + 4qq + qa of round kq: tile q of its quad reads the
+    // unit of quad lane q.
+    const uint32_t vu = 1024 * kq + 16 * (32 * hb + 16 * ph + 4 * qq + qa);
     struct DnBytes {
-      uint4 u[4], h;
+      u32x4 u, h;
     };
-    auto load = [&](unsigned R) {
-      const uint8_t* d = reinterpret_cast<const uint8_t*>(H.base[min(R, nblk - 1)] + eoff);
-      DnBytes B;
+    auto load = [&](unsigned R, DnBytes& B) {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          reinterpret_cast<void*>(H.base[min(R, nblk - 1)] + eoff), (short)0, 4608, 0x00020000);
+      B.u = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vu, 0, 0);
+      B.h = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vh, 0, 0);
+    };
+    // The slice's header table (parity par): lane l decodes neuron l%32 for
+    // the pass's sub-block l/32. Returns whether the neuron's d takes the
+    // direct path.
+    auto table = [&](const u32x4& hd, unsigned par) {
+      if (half_bad(hd[0]) || half_bad(hd[0] >> 16)) bad |= kErrScale;
+      const float dn = half_to_float(hd[0] & 0xffff), dmn = half_to_float(hd[0] >> 16);
+      uint32_t sc, mi;
+      q4k_scale_min(hd[1], hd[2], hd[3], 4 * hb + 2 * ph + hgg, sc, mi);
+      L.sc[wave][par][hgg][hn] = (uint16_t)sc;
+      L.mm[wave][par][hgg][hn] = dmn * (float)mi;
+      if (hgg == 0) L.d[wave][par][hn] = dn;
+      __builtin_amdgcn_wave_barrier();
+      return fabsf(dn) < kDownDirect;
+    };
+    // gate * h' of the lane's token m, neurons 8kq..8kq+7 of slice R, and
+    // B = d h' (times 2^-k) in two f16 parts.
+    auto b_parts = [&](unsigned R, unsigned par, int k, float (&hv)[8], f16x8& bh, f16x8& bl) {
+      const float4 a = *reinterpret_cast<const float4*>(&L.h[R][kq][m][0]);
+      const float4 b = *reinterpret_cast<const float4*>(&L.h[R][kq][m][4]);
+      const float4 d0 = *reinterpret_cast<const float4*>(&L.d[wave][par][8 * kq]);
+      const float4 d1 = *reinterpret_cast<const float4*>(&L.d[wave][par][8 * kq + 4]);
+      hv[0] = a.x, hv[1] = a.y, hv[2] = a.z, hv[3] = a.w, hv[4] = b.x, hv[5] = b.y, hv[6] = b.z, hv[7] = b.w;
+      const float dv[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      float v[8];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) B.u[t] = ld16(d + ubase + 64 * t);
-      B.h = ld16(d + hoff);
-      return B;
+      for (int j = 0; j < 8; ++j) v[j] = k ? ldexpf(hv[j] * dv[j], -k) : hv[j] * dv[j];
+      split_f16(v, bh, bl);
+    };
+    // A of tile MQ: the unit of quad lane MQ, the lane's column, times the
+    // sub-block's scales (u16 pairs of neurons 8kq + 2w, 8kq + 2w + 1).
+    auto a_tile = [&](const u32x4& U, unsigned par, auto mq) {
+      constexpr int MQ = decltype(mq)::value;
+      const uint4 s4 = *reinterpret_cast<const uint4*>(&L.sc[wave][par][MQ / 2][8 * kq]);
+      const u32x4 aw = {mul_u16x2(quad_nibbles<MQ>(U[0], mask, shift), s4.x),
+                        mul_u16x2(quad_nibbles<MQ>(U[1], mask, shift), s4.y),
+                        mul_u16x2(quad_nibbles<MQ>(U[2], mask, shift), s4.z),
+                        mul_u16x2(quad_nibbles<MQ>(U[3], mask, shift), s4.w)};
+      return __builtin_bit_cast(f16x8, aw);
     };
     f32x4 acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float corr[2] = {0.f, 0.f};
-    DnBytes nxt = load(0);
-    for (unsigned R = 0; R < nblk; ++R) {
-      const DnBytes cur = nxt;
-      nxt = load(R + 1);
-      float2* tab = &L.tab[wave][R & 1][0];
-      {
-        float D, M;
-        bool ok;
-        hdr_dm(cur.h, 4 * hb + 2 * ph + hgg, D, M, ok);
-        if (!ok) bad |= kErrScale;
-        tab[18 * (hn >> 3) + 8 * hgg + (hn & 7)] = make_float2(D, M);
+    float corr[2] = {0.f, 0.f};   // [sub-block of the pass] the min terms of token m, this lane's neurons
+    uint32_t deferred = 0;        // slices with a neuron's |d| >= 4 (bit R)
+    auto min_terms = [&](unsigned par, const float (&hv)[8]) {
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi) {
+        const float4 m0 = *reinterpret_cast<const float4*>(&L.mm[wave][par][gi][8 * kq]);
+        const float4 m1 = *reinterpret_cast<const float4*>(&L.mm[wave][par][gi][8 * kq + 4]);
+        const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) corr[gi] = fmaf(mv[j], hv[j], corr[gi]);
       }
-      __builtin_amdgcn_wave_barrier();
-      const float4 hv0 = *reinterpret_cast<const float4*>(&L.h[R][kq][n][0]);
-      const float4 hv1 = *reinterpret_cast<const float4*>(&L.h[R][kq][n][4]);
-      const float hv[8] = {hv0.x, hv0.y, hv0.z, hv0.w, hv1.x, hv1.y, hv1.z, hv1.w};
-#pragma unroll
-      for (int gg = 0; gg < 2; ++gg) {
-        const float4* tp = reinterpret_cast<const float4*>(&tab[18 * kq + 8 * gg]);
-        float D[8], M[8];
-#pragma unroll
-        for (int j2 = 0; j2 < 4; ++j2) {
-          const float4 dm = tp[j2];
-          D[2 * j2] = dm.x;
-          M[2 * j2] = dm.y;
-          D[2 * j2 + 1] = dm.z;
-          M[2 * j2 + 1] = dm.w;
-        }
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          v[j] = hv[j] * D[j];
-          corr[gg] = fmaf(hv[j], fmaf(16.f, D[j], M[j]), corr[gg]);
-        }
-        bf16x8 b1, b2, b3;
-        split_bf16(v, b1, b2, b3);
-        bf16x8 a[2];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          // Dword w of the unit: neurons 8kq+2w (low half) and 8kq+2w+1 (high
-          // half), nibble c4 of each half -> bf16 16 + q in each half.
-          u32x4 aw;
-#pragma unroll
-          for (int w = 0; w < 4; ++w)
-            aw[w] = 0x41804180u | (((word(cur.u[2 * gg + tt], w) >> (4 * c4)) & 0x000F000Fu) << 3);
-          a[tt] = __builtin_bit_cast(bf16x8, aw);
-        }
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) acc[2 * gg + tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tt], b3, acc[2 * gg + tt], 0, 0, 0);
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) acc[2 * gg + tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tt], b2, acc[2 * gg + tt], 0, 0, 0);
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) acc[2 * gg + tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tt], b1, acc[2 * gg + tt], 0, 0, 0);
+    };
+    auto apply = [&](unsigned R, const DnBytes& B) {
+      const unsigned par = R & 1;
+      const bool direct = table(B.h, par);
+      float hv[8];
+      f16x8 bh, bl;
+      b_parts(R, par, 0, hv, bh, bl);
+      min_terms(par, hv);
+      if (__builtin_expect(__ballot(!direct) != 0, 0)) {
+        deferred |= 1u << R;
+        return;
+      }
+      const f16x8 a0 = a_tile(B.u, par, std::integral_constant<int, 0>{});
+      const f16x8 a1 = a_tile(B.u, par, std::integral_constant<int, 1>{});
+      const f16x8 a2 = a_tile(B.u, par, std::integral_constant<int, 2>{});
+      const f16x8 a3 = a_tile(B.u, par, std::integral_constant<int, 3>{});
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bl, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl, acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bl, acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a3, bl, acc[3], 0, 0, 0);
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bh, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bh, acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bh, acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a3, bh, acc[3], 0, 0, 0);
+    };
+    DnBytes sa, sbb;
+    load(0, sa);
+    for (unsigned R = 0; R < nblk; R += 2) {
+      load(R + 1, sbb);
+      apply(R, sa);
+      if (R + 1 < nblk) {
+        load(R + 2, sa);
+        apply(R + 1, sbb);
       }
     }
-    // The correction of token n over all 32 neurons: sum the four rounds.
+    // Deferred slices: B = d h' 2^-k with 2^k >= max |d| / 4 over the slice's
+    // neurons, each product times 2^k before it joins the sum.
+    for (uint32_t dm = deferred; dm; dm &= dm - 1) {
+      const unsigned R = (unsigned)__builtin_ctz(dm);
+      DnBytes B;
+      load(R, B);
+      (void)table(B.h, 0);
+      float dmax = fabsf(L.d[wave][0][hn]);
+      dmax = isfinite(dmax) ? dmax : 0.f;   // a non-finite d is flagged by the table
 #pragma unroll
-    for (int gg = 0; gg < 2; ++gg) {
-      corr[gg] += __shfl_xor(corr[gg], 16, 64);
-      corr[gg] += __shfl_xor(corr[gg], 32, 64);
+      for (int o = 16; o; o >>= 1) dmax = fmaxf(dmax, __shfl_xor(dmax, o));
+      int E = 0;
+      (void)frexpf(dmax, &E);   // dmax < 2^E
+      const int k = max(E - 2, 0);
+      float hv[8];
+      f16x8 bh, bl;
+      b_parts(R, 0, k, hv, bh, bl);
+      const f16x8 a[4] = {a_tile(B.u, 0, std::integral_constant<int, 0>{}),
+                          a_tile(B.u, 0, std::integral_constant<int, 1>{}),
+                          a_tile(B.u, 0, std::integral_constant<int, 2>{}),
+                          a_tile(B.u, 0, std::integral_constant<int, 3>{})};
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4 pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], bl, z, 0, 0, 0);
+        pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], bh, pr, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[q][r] += ldexpf(pr[r], k);
+      }
+      __builtin_amdgcn_wave_barrier();   // the table is read before the next deferred slice writes it
     }
-    // Lane l holds rows 4(l/16) + r (outputs 128hb + 64ph + 16t + 4(l/16) + r)
-    // of token l%16.
-    if (n < T.ntok) {
-      float* dst = S.part + (size_t)(T.slot0 + n) * hidden + 256 * sb + 128 * hb + 64 * ph + 4 * kq;
+    // The min terms of token m over all 32 neurons: sum the four lane groups.
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float c = corr[t >> 1];
-        *reinterpret_cast<float4*>(dst + 16 * t) =
-            make_float4(acc[t][0] - c, acc[t][1] - c, acc[t][2] - c, acc[t][3] - c);
+    for (int gi = 0; gi < 2; ++gi) {
+      corr[gi] += __shfl_xor(corr[gi], 16, 64);
+      corr[gi] += __shfl_xor(corr[gi], 32, 64);
+    }
+    // Lane l holds C rows 4(l/16) + r (outputs 128hb + 64ph + 16q + 4(l/16) + r
+    // of the super-block) of token l%16: y = (2^24 C - min terms) * 2^e_t.
+    if (m < T.ntok) {
+      const int et = L.e[m];
+      float* dst = S.part + (size_t)(T.slot0 + m) * hidden + 256 * sb + 128 * hb + 64 * ph + 4 * kq;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float c = corr[q >> 1];
+        *reinterpret_cast<float4*>(dst + 16 * q) =
+            make_float4(ldexpf(ldexpf(acc[q][0], 24) - c, et), ldexpf(ldexpf(acc[q][1], 24) - c, et),
+                        ldexpf(ldexpf(acc[q][2], 24) - c, et), ldexpf(ldexpf(acc[q][3], 24) - c, et));
       }
     }
   }

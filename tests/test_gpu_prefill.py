@@ -184,3 +184,36 @@ def test_prefill_error_paths(eng):
     assert eng.synthetic(2, hidden, fa.FMT_Q8, 1, SEED) == fa.OK
     assert eng.run_batch(0, experts, gates, x)[0] == fa.UNSUPPORTED
     eng.release(2)
+
+
+def test_prefill_large_down_scales(eng):
+    """Down super-blocks whose d is 4 or more in magnitude (4, -5, 6, 100, and
+    65504, the largest fp16) in one expert's slice: the down kernel takes those
+    slices on its scaled path; rows against the oracle and against run()."""
+    hidden, blocks = 4096, (0, 1)
+    lay = oracle.layout(hidden, fa.FMT_Q4KT)
+    load(eng, hidden, blocks)
+    rng = np.random.default_rng(4444)
+    pool = rng.choice(512, 30, replace=False)
+    experts, gates, x = chunk(rng, 24, hidden, pool)
+    e0 = int(experts[2, 3])
+    units = host_units(lay, blocks, 0, experts)
+    view = slice_view(units[1], lay, 0, e0)
+    good = view.copy()
+    for neuron, sb, d in ((5, 3, 0x4400), (17, 9, 0xC500), (0, 0, 0x4600), (31, 15, 0x5640), (12, 6, 0x7BFF)):
+        off = 2 * lay.proj + neuron * lay.down_row + 144 * sb
+        view[off:off + 2] = np.array([d], np.uint16).view(np.uint8)
+    try:
+        assert eng.refresh(1, units[1], 0, e0) == fa.OK
+        y = run_ok(eng, 0, experts, gates, x)
+        rows = []
+        for t0 in range(0, x.shape[0], 8):
+            sl = slice(t0, t0 + 8)
+            rc, ref = oracle.ref_run(units, fa.FMT_Q4KT, False, oracle_request(0, experts[sl], gates[sl], x[sl]))
+            assert rc == 0
+            rows.append(ref[:8])
+        check_close(np.concatenate(rows), y, fa.MODE_F32, "prefill large down scales")
+        check_close(run_bursts(eng, 0, experts, gates, x), y, fa.MODE_F32, "prefill large down scales vs run")
+    finally:
+        view[:] = good
+        assert eng.refresh(1, units[1], 0, e0) == fa.OK
