@@ -1983,14 +1983,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const uint
 //
 // Columns: token t in column 2t (hi part of its operand) and 2t+1 (lo part).
 // Gate/up, per super-block and row-block: A = sc*q, the 6-bit sub-block scale
-// times the nibble (< 1024), written straight into the bits of an f16
-// subnormal by one packed 16-bit multiply, so that A = sc*q*2^-24 exactly;
+// times the nibble (< 1024), exactly in f16 (a packed 16-bit multiply-add
+// forms the bits of 1024 + sc*q, less 1024 in f16);
 // lane 16kg + i holds row i, sub-block 4p + kg, as the TQ4_KM tiles lie, so
 // one v_mfma_f32_16x16x32_f16 spans 8 positions of 4 sub-blocks and 8 of them
 // the super-block. B = x' of the column's token, x' = x*2^-e with |x'| < 2^15
 // over the token's values in the super-block, as hi = f16(x'), lo = f16(x' -
 // hi) (22 significant bits). The super-block's sums are scaled once by
-// d*2^(24+e); the min terms -dmin*m*sum(x) take v_mfma_f32_16x16x4f32 per
+// d*2^e; the min terms -dmin*m*sum(x) take v_mfma_f32_16x16x4f32 per
 // four sub-blocks on the fp32 sub-block sums of x. x is staged once per
 // workgroup: each wavefront turns its own two super-blocks of every token
 // into B operands that stay in registers for all of its pairs.
@@ -2015,7 +2015,7 @@ struct BurstLds {
   uint4 hdr[kDecodeWaves][2][64];               // [wave][super-block][row-block*16 + row]: gate/up headers
   float dg[kDecodeWaves][2][64];                // d of each gate/up header
   uint4 dsc[kDecodeWaves][2][8][4];             // [wave][super-block][sub-block][kg]: down sc of neurons 8kg.. as u16
-  uint4 dmn[kDecodeWaves][2][8][4];             // the down mins, same layout
+  uint4 dmn[kDecodeWaves][2][8][4];             // the down mins, same layout, as f16
   float dd[kDecodeWaves][2][kNeurons];          // [wave][super-block][neuron] down d
   float dm[kDecodeWaves][2][kNeurons];          // down dmin
   float out[kDecodeWaves][kMaxBurst][260];      // [wave][token][output]: one super-block's down outputs (unscaled)
@@ -2076,18 +2076,27 @@ __device__ __forceinline__ void load_burst_down(const PairBuf& B, unsigned lb0, 
   D.h = bld(B, voff_h, base + 4096);
 }
 
-__device__ __forceinline__ uint32_t mul_u16x2(uint32_t a, uint32_t b) {
-  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
+// Two nibble values (u16 halves of p, each below 16) times the 6-bit scale
+// (sc2 = sc | sc << 16) as two f16 in one dword: the packed 16-bit
+// multiply-add forms the f16 bits of 1024 + sc*q (exact: sc*q < 1024), and
+// subtracting 1024 in f16 leaves sc*q exactly. (The bits of sc*q alone would
+// be the f16 subnormal sc*q*2^-24, but the matrix cores round products of
+// subnormal f16 operands more coarsely: about 4e-6 of the dot's magnitude
+// against 2e-7 for normal operands, measured.)
+__device__ __forceinline__ uint32_t scaled_u16(uint32_t p, uint32_t sc2) {
+  const u16x2 m = __builtin_bit_cast(u16x2, p) * __builtin_bit_cast(u16x2, sc2) + (u16x2){0x6400, 0x6400};
+  const f16x2 f = __builtin_bit_cast(f16x2, m) - (f16x2){(_Float16)1024.f, (_Float16)1024.f};
+  return __builtin_bit_cast(uint32_t, f);
 }
 // Word w of a gate/up lane chunk (positions 8v..8v+3 in the low nibbles,
 // 8v+4..8v+7 in the high ones) times the scale pair s2 = sc | sc << 16, as 8
-// f16 subnormals sc*q*2^-24 in position order.
+// f16 values sc*q in position order.
 __device__ __forceinline__ f16x8 burst_a(uint32_t w, uint32_t s2) {
   const uint32_t lo = nib_lo(w), hi = nib_hi(w);
-  const u32x4 a = {mul_u16x2(__builtin_amdgcn_perm(0u, lo, 0x0c010c00u), s2),
-                   mul_u16x2(__builtin_amdgcn_perm(0u, lo, 0x0c030c02u), s2),
-                   mul_u16x2(__builtin_amdgcn_perm(0u, hi, 0x0c010c00u), s2),
-                   mul_u16x2(__builtin_amdgcn_perm(0u, hi, 0x0c030c02u), s2)};
+  const u32x4 a = {scaled_u16(__builtin_amdgcn_perm(0u, lo, 0x0c010c00u), s2),
+                   scaled_u16(__builtin_amdgcn_perm(0u, lo, 0x0c030c02u), s2),
+                   scaled_u16(__builtin_amdgcn_perm(0u, hi, 0x0c010c00u), s2),
+                   scaled_u16(__builtin_amdgcn_perm(0u, hi, 0x0c030c02u), s2)};
   return __builtin_bit_cast(f16x8, a);
 }
 // v split into the f16 part of the lane's column: hi = f16(v), lo = f16(v - hi).
@@ -2109,10 +2118,10 @@ __device__ __forceinline__ uint32_t quad_nibbles(uint32_t v, uint32_t mask, uint
 template <int MQ>
 __device__ __forceinline__ f32x4 burst_tile(const uint4& U, uint32_t mask, uint32_t shift, const uint4& scp,
                                             const f16x8& bd, const f32x4& cmin) {
-  const u32x4 a = {mul_u16x2(quad_nibbles<MQ>(U.x, mask, shift), scp.x),
-                   mul_u16x2(quad_nibbles<MQ>(U.y, mask, shift), scp.y),
-                   mul_u16x2(quad_nibbles<MQ>(U.z, mask, shift), scp.z),
-                   mul_u16x2(quad_nibbles<MQ>(U.w, mask, shift), scp.w)};
+  const u32x4 a = {scaled_u16(quad_nibbles<MQ>(U.x, mask, shift), scp.x),
+                   scaled_u16(quad_nibbles<MQ>(U.y, mask, shift), scp.y),
+                   scaled_u16(quad_nibbles<MQ>(U.z, mask, shift), scp.z),
+                   scaled_u16(quad_nibbles<MQ>(U.w, mask, shift), scp.w)};
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), bd, cmin, 0, 0, 0);
 }
 // Max over the 32 lanes of each half wavefront (quad butterflies, two row
@@ -2186,7 +2195,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_burst_kernel(const uint
 
   f16x8 bx[2][2][4];   // [super-block][part p][word v]: positions 8v..8v+7 of sub-block 4p + kg
   float xsm[2][2];     // sum of x over sub-block 4p + kg (hi columns of the burst's tokens; 0 otherwise)
-  int xe[2];           // 24 + e of the column's token in the super-block
+  int xe[2];           // e of the column's token in the super-block
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     xe[s] = 0;
@@ -2260,7 +2269,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_burst_kernel(const uint
           xsm[s][pp] = mine && !lo_part ? sm : xsm[s][pp];
         }
         const int e = X.e[row >> 1][sb];
-        xe[s] = mine ? 24 + e : xe[s];
+        xe[s] = mine ? e : xe[s];
       }
     }
     __syncthreads();   // the staging area becomes the pair loop's
@@ -2378,7 +2387,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_burst_kernel(const uint
 #pragma unroll
       for (int g = 0; g < 8; ++g) {
         ts[32 * g + n] = (uint16_t)((g < 4 ? sc_lo : sc_hi) >> (8 * (g & 3)) & 0xffu);
-        tm[32 * g + n] = (uint16_t)((g < 4 ? mi_lo : mi_hi) >> (8 * (g & 3)) & 0xffu);
+        const float mf = (float)((g < 4 ? mi_lo : mi_hi) >> (8 * (g & 3)) & 0xffu);
+        tm[32 * g + n] = __builtin_bit_cast(uint16_t, (_Float16)mf);   // m as an f16 operand
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -2419,7 +2429,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_burst_kernel(const uint
           bd[j] = f16_part(ldexpf(cd[j], -e), lo_part);
           bm[j] = f16_part(ldexpf(cm[j], -e), lo_part);
         }
-        const int ye = 24 + e;
+        const int ye = e;
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int G = 0; G < 4; ++G) {
@@ -4044,25 +4054,21 @@ __global__ __launch_bounds__(1024) void prefill_split(const uint8_t* __restrict_
   }
 }
 
-constexpr int kXhRow = 528;              // LDS bytes per (token, part) row: 512 + 16 of padding
+// LDS bytes per (part, token) row: 512 + 16 of padding, so that the rows of
+// 8 consecutive tokens start 16 bytes apart modulo 128 and a 16-byte read
+// across them touches every bank once.
+constexpr int kXhRow = 528;
 
 struct GateUpLds {
-  uint8_t xh[2][kTileTokens * 2][kXhRow];    // [buffer][token * 2 + part][256 f16]: one super-block of x'
+  uint8_t xh[2][2][kTileTokens][kXhRow];     // [buffer][part][token][256 f16]: one super-block of x'
   float xs[2][kTileTokens][8];               // sub-block sums of x'
   float main[kDecodeWaves][16][kTileTokens]; // [wave][row][token] scale-weighted dot part
   float mins[kDecodeWaves][16][kTileTokens]; // [wave][row][token] min part
 };
 
-// Two nibble values (bytes b and b+1 of v, each below 16) times the 6-bit
-// scale sc as two f16 in one dword: the packed 16-bit multiply-add forms the
-// f16 bits of 1024 + sc*q (exact: sc*q < 1024), and subtracting 1024 in f16
-// leaves sc*q exactly.
-__device__ __forceinline__ uint32_t scaled_pair(uint32_t v, uint32_t sel, uint32_t sc) {
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  const u16x2 p = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, v, sel));
-  const u16x2 m = p * (u16x2){(unsigned short)sc, (unsigned short)sc} + (u16x2){0x6400, 0x6400};
-  const f16x2 f = __builtin_bit_cast(f16x2, m) - (f16x2){(_Float16)1024.f, (_Float16)1024.f};
-  return __builtin_bit_cast(uint32_t, f);
+// The same for two nibble values taken as bytes b and b+1 of v.
+__device__ __forceinline__ uint32_t scaled_pair(uint32_t v, uint32_t sel, uint32_t sc2) {
+  return scaled_u16(__builtin_amdgcn_perm(0u, v, sel), sc2);
 }
 
 // Workgroup (tile, slice): wavefront w takes row-block w%4 (gate rows of
@@ -4114,7 +4120,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     }
   };
   auto store_x = [&](unsigned buf, const XStage& X) {
-    uint8_t* row = &L.xh[buf][2 * tl + c / 16][32 * (c % 16)];
+    uint8_t* row = &L.xh[buf][c / 16][tl][32 * (c % 16)];
     *reinterpret_cast<uint4*>(row) = X.d[0];
     *reinterpret_cast<uint4*>(row + 16) = X.d[1];
     if (c < 8) L.xs[buf][tl][c] = X.s;
@@ -4145,14 +4151,15 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     if (s + 2 < nsb) load_x(s + 2, nxt);
     uint32_t sc, mi;
     q4k_scale_min(hc.y, hc.z, hc.w, 4 * p + kg, sc, mi);
+    sc *= 0x10001u;
     if (half_bad(hc.x) || half_bad(hc.x >> 16)) bad |= kErrScale;
     const float d = half_to_float(hc.x & 0xffff);
     float drow[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) drow[r] = __shfl(d, (int)(4 * kg) + r, 64);
     // B row of token col, part h: x' of sub-block 4p + kg at LDS
-    // xh[buf][2 col + h][2 (32 (4p + kg) + 8v)].
-    const uint8_t* xb8 = &L.xh[buf][2 * col][64 * (4 * p + kg)];
+    // xh[buf][h][col][2 (32 (4p + kg) + 8v)].
+    const uint8_t* xb8 = &L.xh[buf][0][col][64 * (4 * p + kg)];
     f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -4162,7 +4169,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
                         scaled_pair(hi, 0x0c010c00u, sc), scaled_pair(hi, 0x0c030c02u, sc)};
       const f16x8 a = __builtin_bit_cast(f16x8, aw);
       const uint4 bh = *reinterpret_cast<const uint4*>(xb8 + 16 * v);
-      const uint4 bl = *reinterpret_cast<const uint4*>(xb8 + kXhRow + 16 * v);
+      const uint4 bl = *reinterpret_cast<const uint4*>(xb8 + kTileTokens * kXhRow + 16 * v);
       c_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bh), c_hi, 0, 0, 0);
       c_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bl), c_lo, 0, 0, 0);
     }
@@ -4234,8 +4241,8 @@ __device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& b1, bf16
 // e_t puts the largest |h'| in [2^12, 2^13)). The first sum runs on
 // v_mfma_f32_16x16x32_f16 over the 32 neurons (lane group kq: neurons
 // 8kq..8kq+7):
-//   A[o][n] = sc_ng * q_on in the bits of an f16 subnormal (sc q < 1024, so
-//     A = sc q 2^-24 exactly), one packed 16-bit multiply per two neurons;
+//   A[o][n] = sc_ng * q_on exactly in f16 (sc q < 1024), a packed 16-bit
+//     multiply-add and an f16 subtraction per two neurons;
 //   B[n][t] = d_n h'_nt in two f16 parts (22 significant bits), formed once
 //     per slice for the wavefront's eight tiles;
 // and the products add straight into the tiles' accumulators over the
@@ -4349,10 +4356,10 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
     auto a_tile = [&](const u32x4& U, unsigned par, auto mq) {
       constexpr int MQ = decltype(mq)::value;
       const uint4 s4 = *reinterpret_cast<const uint4*>(&L.sc[wave][par][MQ / 2][8 * kq]);
-      const u32x4 aw = {mul_u16x2(quad_nibbles<MQ>(U[0], mask, shift), s4.x),
-                        mul_u16x2(quad_nibbles<MQ>(U[1], mask, shift), s4.y),
-                        mul_u16x2(quad_nibbles<MQ>(U[2], mask, shift), s4.z),
-                        mul_u16x2(quad_nibbles<MQ>(U[3], mask, shift), s4.w)};
+      const u32x4 aw = {scaled_u16(quad_nibbles<MQ>(U[0], mask, shift), s4.x),
+                        scaled_u16(quad_nibbles<MQ>(U[1], mask, shift), s4.y),
+                        scaled_u16(quad_nibbles<MQ>(U[2], mask, shift), s4.z),
+                        scaled_u16(quad_nibbles<MQ>(U[3], mask, shift), s4.w)};
       return __builtin_bit_cast(f16x8, aw);
     };
     f32x4 acc[4];
@@ -4442,7 +4449,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
       corr[gi] += __shfl_xor(corr[gi], 32, 64);
     }
     // Lane l holds C rows 4(l/16) + r (outputs 128hb + 64ph + 16q + 4(l/16) + r
-    // of the super-block) of token l%16: y = (2^24 C - min terms) * 2^e_t.
+    // of the super-block) of token l%16: y = (C - min terms) * 2^e_t.
     if (m < T.ntok) {
       const int et = L.e[m];
       float* dst = S.part + (size_t)(T.slot0 + m) * hidden + 256 * sb + 128 * hb + 64 * ph + 4 * kq;
@@ -4450,8 +4457,8 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
       for (int q = 0; q < 4; ++q) {
         const float c = corr[q >> 1];
         *reinterpret_cast<float4*>(dst + 16 * q) =
-            make_float4(ldexpf(ldexpf(acc[q][0], 24) - c, et), ldexpf(ldexpf(acc[q][1], 24) - c, et),
-                        ldexpf(ldexpf(acc[q][2], 24) - c, et), ldexpf(ldexpf(acc[q][3], 24) - c, et));
+            make_float4(ldexpf(acc[q][0] - c, et), ldexpf(acc[q][1] - c, et), ldexpf(acc[q][2] - c, et),
+                        ldexpf(acc[q][3] - c, et));
       }
     }
   }
@@ -4525,7 +4532,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
     }
   };
   auto store_x = [&](unsigned buf, const XStage& X) {
-    uint8_t* row = &L.xh[buf][2 * tl + c / 16][32 * (c % 16)];
+    uint8_t* row = &L.xh[buf][c / 16][tl][32 * (c % 16)];
     *reinterpret_cast<uint4*>(row) = X.d[0];
     *reinterpret_cast<uint4*>(row + 16) = X.d[1];
     if (c < 8) L.xs[buf][tl][c] = X.s;
@@ -4584,6 +4591,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
         for (int J = 0; J < 2; ++J) {
           uint32_t mi;
           q4k_scale_min(W.h.y, W.h.z, W.h.w, 4 * p + 2 * cc + J, scs[cc][J], mi);
+          scs[cc][J] *= 0x10001u;
         }
     }
 #pragma unroll
@@ -4603,9 +4611,9 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
                      int8_pair_f16(q.y, 0x0c030c02u)};
         }
         const f16x8 a = __builtin_bit_cast(f16x8, aw);
-        const uint8_t* xb8 = &L.xh[buf][2 * col][2 * (32 * sub + 8 * kg)];
+        const uint8_t* xb8 = &L.xh[buf][0][col][2 * (32 * sub + 8 * kg)];
         const uint4 bh = *reinterpret_cast<const uint4*>(xb8);
-        const uint4 bl = *reinterpret_cast<const uint4*>(xb8 + kXhRow);
+        const uint4 bl = *reinterpret_cast<const uint4*>(xb8 + kTileTokens * kXhRow);
         if (kQ4) {
           c_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bh), c_hi, 0, 0, 0);
           c_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bl), c_lo, 0, 0, 0);
