@@ -336,11 +336,13 @@ PREFILL_TOKENS = 512
 MFMA_F16_PEAK_TFLOPS = 2500.0   # dense f16/bf16 matrix cores (the prefill GEMMs' instructions)
 PREFILL_TEXT = ("Resident node prefill: 48 layers x 512 experts x 640 intermediate x hidden 4096, all Q4_K "
                 "(down transposed, 108.7 GB in HBM); a chunk of 512 tokens, top-10 of 512 uniform per token per "
-                "layer, through fr_hip_run_batch (f16 and bf16 matrix cores on exactly split operands, fp32 accumulation)")
+                "layer, through fr_hip_run_batch (f16 matrix cores on exact operands and exactly split x and h, fp32 "
+                "accumulation)")
 PREFILL_NATIVE_TEXT = ("Resident node prefill on the reference's own units: 48 layers x 512 experts x hidden 4096, "
                        "Q4_K gate/up rows, MXFP4 down, Q8_0 shared expert (106.7 GB in HBM); a chunk of 512 tokens, "
                        "top-10 of 512 uniform per token per layer and the shared expert at gate 0.5 on every token, "
-                       "through fr_hip_run_batch (f16 matrix cores for gate/up, fp32 matrix cores for the downs)")
+                       "through fr_hip_run_batch (f16 matrix cores for gate/up, bf16 matrix cores for the downs, on exact "
+                       "operands and exactly split x and h)")
 
 
 def prefill_requests(rng, layers, tokens, shared=0.0):
