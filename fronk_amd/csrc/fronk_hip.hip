@@ -3940,29 +3940,31 @@ __global__ void synth_kernel(uint8_t* __restrict__ dst, SliceShape routed, Slice
 
 // ------------------------------------------------------------ prefill path
 // A prefill chunk: T tokens of one layer (T up to kMaxBatchTokens), each with
-// its own top-10 routing, all owned slices Q4_K with the transposed down, F32.
-// The reference serves it as run() calls of at most 8 tokens
-// (client/fronk_client.h:41-42, src/backend.h:21); the result of token t is
-// that of run() on token t alone (backends/ref.c:57-98). Here the tokens are
-// grouped by routed expert, so that each expert's weights are read once for
-// all of its tokens and the work is a contraction:
+// its own top-10 routing, F32; every owned slice Q4_K with the transposed
+// down, or every one a native unit (row-format kernels further below), and
+// the shared expert on the tokens whose gate asks for it. The reference
+// serves it as run() calls of at most 8 tokens (client/fronk_client.h:41-42,
+// src/backend.h:21); the result of token t is that of run() on token t alone
+// (backends/ref.c:57-98). Here the tokens are grouped by routed expert, so
+// that each expert's weights are read once for all of its tokens and the
+// work is a contraction:
 //   prefill_split    (token): x as two f16 parts of x * 2^-e, once;
 //   prefill_gate_up  (tile, slice): a, u of up to 16 tokens over one slice's
 //                    32 neurons on f16 matrix cores (operands exact), then
 //                    gate*SiLU(a)*u;
 //   prefill_down     (tile, 1024 outputs): the expert's down matrix over all
-//                    owned slices applied to the tile's h on bf16 matrix
-//                    cores (operands exact), one fp32 partial per
-//                    (token, expert);
+//                    owned slices applied to the tile's h on f16 matrix
+//                    cores (A = sc*q exact, B = d*h in two exact parts), one
+//                    fp32 partial per (token, expert);
 //   prefill_reduce   (token, 1024 outputs): the token's 10 expert partials
-//                    summed in its routing order in fp64, then narrowed with
-//                    the reference's rule (backends/ref.c:37-40, 95).
-// For the down, v_mfma_f32_16x16x4_f32 (A: lane l holds A[l%16][l/16]; B:
-// B[l/16][l%16]; C: lane l holds C[4(l/16)+r][l%16]) takes one fp32 value per
-// lane and operand, so each lane dequantizes exactly the weight it
-// contributes, and the Q4_K-T down, stored along the outputs, needs no
-// transposition. Its scales vary along both the neurons (the contraction) and
-// the outputs, which rules out folding them into integer operands.
+//                    (then the shared expert's) summed in its routing order
+//                    in fp64, then narrowed with the reference's rule
+//                    (backends/ref.c:37-40, 95).
+// Matrix-core layouts used below (16x16 tiles, 64 lanes): v_mfma_f32_16x16x32
+// (f16/bf16): A lane l holds row l%16, k = 8(l/16)..+7; B lane l holds
+// column l%16, the same k; C lane l holds rows 4(l/16)..+3 of column l%16.
+// v_mfma_f32_16x16x4_f32 (the min terms): A lane l holds A[l%16][l/16], B
+// lane l B[l/16][l%16].
 constexpr int kTileTokens = 16;          // tokens of one expert tile (the MFMA N)
 constexpr int kBatchThreads = 512;
 constexpr int kMaxBatchTokens = 4096;
@@ -4814,15 +4816,16 @@ __global__ __launch_bounds__(kBatchThreads, DN == TMXFP4 ? 4 : 2) void prefill_d
   const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * proj;
   const int nrec = (int)((kMx ? 17u : 34u) * hidden);   // the down's bytes
   const uint32_t vw = 16 * (o0 + m) + 4 * kq;           // dword kq of output o0 + m (tile t: + 256t)
-  const uint32_t ve = 16 * hidden + o0 + (m & ~3u);    // MXFP4: the dword holding its exponent (+ 16t)
-  const uint32_t esh = 8 * (m & 3);                     // ... at this bit
+  const uint32_t ve = 16 * hidden + o0 + 4 * (lane & 31);   // MXFP4: dword l%32 of the wavefront's 128 exponents
   const uint32_t vr = 16 * hidden + o0 + 4 * kq;        // MXFP4: exponents of the lane's C rows (+ 16t)
   const uint32_t vs = 32 * hidden + 2 * (o0 + 4 * kq);  // Q8_0: d of the lane's C rows (+ 32t)
   uint32_t bad = 0;
-  // A slice's bytes, one slice ahead in two register sets (the loop is
-  // unrolled by two so that neither is copied while its loads are in flight).
+  // A slice's bytes, two slices ahead in three register sets (the loop is
+  // unrolled by three so that no set is copied while its loads are in
+  // flight). MXFP4: one dword of exponents per lane; lane 4t + m/4 holds
+  // those of tile t's outputs 16t + 4(m/4) .. +3.
   struct MxSlice {
-    uint32_t w[kT], e4[kT];
+    uint32_t w[kT], e32;
   };
   struct Q8Slice {
     uint32_t q0[kT], q1[kT];
@@ -4836,13 +4839,13 @@ __global__ __launch_bounds__(kBatchThreads, DN == TMXFP4 ? 4 : 2) void prefill_d
     for (int t = 0; t < kT; ++t) {
       if constexpr (kMx) {
         B.w[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(vw + 256 * t), 0, 0);
-        B.e4[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(ve + 16 * t), 0, 0);
       } else {
         B.q0[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(vw + 256 * t), 0, 0);
         B.q1[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(16 * hidden + vw + 256 * t), 0, 0);
         B.s[t] = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(vs + 32 * t), 0, 0);
       }
     }
+    if constexpr (kMx) B.e32 = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)ve, 0, 0);
   };
   f32x4 acc[kT];
 #pragma unroll
@@ -4854,7 +4857,8 @@ __global__ __launch_bounds__(kBatchThreads, DN == TMXFP4 ? 4 : 2) void prefill_d
     if constexpr (kMx) {
       uint32_t ev[kT];   // the exponent of the lane's output in each tile
 #pragma unroll
-      for (int t = 0; t < kT; ++t) ev[t] = (B.e4[t] >> esh) & 0xffu;
+      for (int t = 0; t < kT; ++t)
+        ev[t] = ((uint32_t)__shfl((int)B.e32, (int)(4 * t + (m >> 2))) >> (8 * (m & 3))) & 0xffu;
       uint32_t lo = ev[0], hi = ev[0];
 #pragma unroll
       for (int t = 1; t < kT; ++t) {
@@ -4919,14 +4923,19 @@ __global__ __launch_bounds__(kBatchThreads, DN == TMXFP4 ? 4 : 2) void prefill_d
       }
     }
   };
-  SliceBytes sa, sb;
+  SliceBytes sa, sb, sc;
   load_slice(0, sa);
-  for (unsigned R = 0; R < nblk; R += 2) {
-    load_slice(R + 1, sb);
+  load_slice(1, sb);
+  for (unsigned R = 0; R < nblk; R += 3) {
+    load_slice(R + 2, sc);
     apply(R, sa);
     if (R + 1 < nblk) {
-      load_slice(R + 2, sa);
+      load_slice(R + 3, sa);
       apply(R + 1, sb);
+    }
+    if (R + 2 < nblk) {
+      load_slice(R + 4, sb);
+      apply(R + 2, sc);
     }
   }
   // The deferred MXFP4 slices: the exact codes, then each C row's 2^(e-127)
