@@ -130,6 +130,15 @@ struct Scratch {
   // per decode_reduce workgroup in mapped host memory (yout is then mapped
   // host memory too, and dstat a device word of the engine).
   uint32_t* hstat;
+  // Decode launches: the plan header's fields and token table, copied from
+  // the host plan (launch_decode). Kernel arguments are the first memory a
+  // workgroup reads, so its pair descriptor and x are requested one
+  // dependent load earlier than through the device plan's header, and
+  // decode_reduce's partials two.
+  struct {
+    uint32_t hidden, burst, npairs, tpw, pairs_off, groups_off, x_off, pad;
+    DecodeToken tok[kMaxBurst];
+  } A;
 };
 
 // ------------------------------------------------------------ scalars
@@ -1728,20 +1737,18 @@ __device__ __forceinline__ uint32_t* decode_status(const Scratch& S) {
 }
 
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* __restrict__ plan, Scratch S) {
-  const PlanHeader* PH = reinterpret_cast<const PlanHeader*>(plan);
   uint32_t* status = decode_status(S);
-  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + plan_field(PH, offsetof(PlanHeader, pairs_off)));
-  const unsigned hidden = plan_field(PH, offsetof(PlanHeader, hidden)), nsb = hidden / 256, nsub = hidden / 32;
-  const unsigned np = plan_field(PH, offsetof(PlanHeader, npairs)), tpw = plan_field(PH, offsetof(PlanHeader, tpw));
-  const unsigned burst = plan_field(PH, offsetof(PlanHeader, burst));
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(plan + S.A.pairs_off);
+  const unsigned hidden = S.A.hidden, nsb = hidden / 256, nsub = hidden / 32;
+  const unsigned np = S.A.npairs, tpw = S.A.tpw;
+  const unsigned burst = S.A.burst;
   // Token-major partial index of each unit of the work list (after the token table).
-  const uint32_t* upart = reinterpret_cast<const uint32_t*>(plan + plan_field(PH, offsetof(PlanHeader, groups_off)) +
-                                                          burst * sizeof(DecodeToken));
+  const uint32_t* upart = reinterpret_cast<const uint32_t*>(plan + S.A.groups_off + burst * sizeof(DecodeToken));
   // The wavefront index through readfirstlane: the compiler then knows it is
   // uniform, so offsets built from it stay in scalar registers.
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __shared__ __align__(16) DecodeLds L;
-  const float* xg = reinterpret_cast<const float*>(plan + plan_field(PH, offsetof(PlanHeader, x_off)));
+  const float* xg = reinterpret_cast<const float*>(plan + S.A.x_off);
   const unsigned xs0 = 32 * ((unsigned)tid >> 2) + 8 * ((unsigned)tid & 3);   // this thread's 8 values of a token
   const bool xin = ((unsigned)tid >> 2) < nsub;
   const unsigned sb0 = 2 * (unsigned)wave, sb1 = sb0 + 1;
@@ -1759,9 +1766,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const uint8_t* _
   // bytes and staged into the other slot after this unit.
   unsigned p = blockIdx.x * tpw;   // this workgroup's chunk: units [p, min(p + tpw, np))
   const unsigned pend = min(p + tpw, np);
-  PairBuf B = pair_buf(pairs + p);
+  // A single-token plan's x is token 0's: requested before the descriptor.
   float4 xv[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
-  if (xin) {
+  if (burst == 1 && xin) {
+    xv[0] = *reinterpret_cast<const float4*>(xg + xs0);
+    xv[1] = *reinterpret_cast<const float4*>(xg + xs0 + 4);
+  }
+  PairBuf B = pair_buf(pairs + p);
+  if (burst != 1 && xin) {
     const float* xt = xg + (size_t)B.token * hidden + xs0;
     xv[0] = *reinterpret_cast<const float4*>(xt);
     xv[1] = *reinterpret_cast<const float4*>(xt + 4);
@@ -3002,10 +3014,11 @@ __device__ __forceinline__ double xor_d(double v, int m) {
 // kDouble: the unit partials are doubles (decode_q8_kernel's).
 template <bool kDouble>
 __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* __restrict__ plan, Scratch S) {
-  const PlanHeader H = *reinterpret_cast<const PlanHeader*>(plan);
-  const DecodeToken tk = reinterpret_cast<const DecodeToken*>(plan + H.groups_off)[blockIdx.y];
+  (void)plan;
+  const DecodeToken tk = S.A.tok[blockIdx.y];
+  const unsigned hidden = S.A.hidden;
   uint32_t* status = S.ystat ? S.ystat : S.out + (size_t)S.parity * S.out_words;
-  float* yout = (S.ystat || S.hstat ? S.yout : reinterpret_cast<float*>(status + 4)) + (size_t)blockIdx.y * H.hidden;
+  float* yout = (S.ystat || S.hstat ? S.yout : reinterpret_cast<float*>(status + 4)) + (size_t)blockIdx.y * hidden;
   if (S.ystat && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
     const uint32_t e = *S.dstat;   // written by decode_kernel (kernel boundary)
     if (e) flag(status, e);
@@ -3067,7 +3080,7 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce(const uint8_t* _
     if (tid < kReducePositions) {
       const double t = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
       const unsigned col = decode_column(kReducePositions * blockIdx.x + tid);
-      if (col < H.hidden) {
+      if (col < hidden) {
         float f = 0.f;
         if (!isfinite(t) || fabs(t) > (double)FLT_MAX) over = true;
         else f = (float)t;
@@ -5689,12 +5702,31 @@ int build_plan(const fr_hip_request* r, uint8_t* out, size_t cap, size_t* used, 
   return FR_HIP_OK;
 }
 
+// A decode plan's token table lies within the plan (launch_decode copies it
+// from the host plan into the kernel arguments).
+bool decode_table_ok(const PlanHeader& H) {
+  return H.groups_off >= sizeof(PlanHeader) && (uint64_t)H.groups_off + H.burst * sizeof(DecodeToken) <= H.total;
+}
+
 // decode_kernel or the decode_rows_kernel instantiation of the plan's unit
 // formats, then decode_reduce, on `stream`; `mid`, if set, is recorded
 // between them. Returns false if an event could not be recorded.
-bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, const Scratch& S, hipStream_t stream,
+bool launch_decode(const uint8_t* dev_plan, const PlanHeader& H, unsigned grid, const Scratch& S0, hipStream_t stream,
                    hipEvent_t mid) {
   const dim3 g(grid), b(kDecodeThreads);
+  // The header's fields and the token table (at groups_off of the host plan
+  // H heads; every caller checks that it lies within the plan).
+  Scratch S = S0;
+  S.A.hidden = H.hidden;
+  S.A.burst = H.burst;
+  S.A.npairs = H.npairs;
+  S.A.tpw = H.tpw;
+  S.A.pairs_off = H.pairs_off;
+  S.A.groups_off = H.groups_off;
+  S.A.x_off = H.x_off;
+  S.A.pad = 0;
+  memset(S.A.tok, 0, sizeof(S.A.tok));
+  memcpy(S.A.tok, reinterpret_cast<const uint8_t*>(&H) + H.groups_off, H.burst * sizeof(DecodeToken));
   // decode_q8_kernel or decode_rows_q8_kernel: double partials.
   const bool q8 = H.mode == MODE_Q8 || H.mode == MODE_Q8_256;
   if (H.kind == KIND_DECODE_BURST) hipLaunchKernelGGL(decode_burst_kernel, g, b, 0, stream, dev_plan, S);
@@ -6396,7 +6428,7 @@ int fr_hip_launch(const void* host_plan, const void* device_plan, void* stream) 
   if (H.kind == KIND_LAYER ? !H.ntA || !H.ntB || H.grid != H.ntA + H.ntB
                            : (H.kind != KIND_DECODE && H.kind != KIND_DECODE_ROWS && H.kind != KIND_DECODE_SPLIT &&
                               H.kind != KIND_DECODE_BURST) ||
-                                 !H.grid)
+                                 !H.grid || !decode_table_ok(H))
     return FR_HIP_INVALID;
   return launch(static_cast<const uint8_t*>(device_plan), H, H.grid,
                 stream ? static_cast<hipStream_t>(stream) : E.stream);
@@ -6414,7 +6446,8 @@ int fr_hip_launch_static(const void* host_plan, const void* device_plan, float* 
   if (H.kind == KIND_DECODE_SPLIT && H.pad != 2 && H.pad != 4) return FR_HIP_INVALID;
   const unsigned items = H.kind == KIND_DECODE_SPLIT ? H.npairs * H.pad : H.npairs;
   if (H.burst != 1 || items > kStaticUnits || !H.hidden || H.hidden > (unsigned)kMaxHidden) return FR_HIP_UNSUPPORTED;
-  if (!H.grid || H.grid > (unsigned)kDecodeGridMax || H.grid > items || H.ngroups != H.burst) return FR_HIP_INVALID;
+  if (!H.grid || H.grid > (unsigned)kDecodeGridMax || H.grid > items || H.ngroups != H.burst || !decode_table_ok(H))
+    return FR_HIP_INVALID;
   if (H.kind == KIND_DECODE_ROWS && (H.pad & ~kComboShared) > COMBO_Q4_0) return FR_HIP_INVALID;
   if (!E.static_scratch) return FR_HIP_STATE;
   CK(hipSetDevice(E.device));
