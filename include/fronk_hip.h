@@ -123,8 +123,11 @@ int fr_hip_run(const fr_hip_request *req, float *y);
 /* Resident-input path for timing: build the plan (and x) into host memory,
  * copy it to device memory the caller owns, then enqueue launches on
  * `stream` (a hipStream_t; NULL = the library stream). The host copy gives
- * the launch shape; the device copy is what the kernel reads. `cap` must be
- * at least fr_hip_plan_bytes(burst, hidden). */
+ * the launch shape and, for the decode kernels, the header fields and token
+ * table they take as launch arguments; the device copy is what the kernels
+ * read otherwise (descriptors, x), so the two must hold the same plan, also
+ * when a launch is captured in a graph and replayed. `cap` must be at least
+ * fr_hip_plan_bytes(burst, hidden). */
 size_t fr_hip_plan_bytes(unsigned burst, unsigned hidden);
 int fr_hip_plan(const fr_hip_request *req, void *plan, size_t cap, size_t *used, unsigned *grid);
 int fr_hip_launch(const void *host_plan, const void *device_plan, void *stream);
