@@ -2100,15 +2100,29 @@ __device__ __forceinline__ uint32_t scaled_u16(uint32_t p, uint32_t sc2) {
   const f16x2 f = __builtin_bit_cast(f16x2, m) - (f16x2){(_Float16)1024.f, (_Float16)1024.f};
   return __builtin_bit_cast(uint32_t, f);
 }
+// Bytes 2H, 2H+1 of v (each below 16) times sch (two f16 copies of a 6-bit
+// scale) as two exact normal f16 values sc*q, in two instructions: a byte
+// below 16 read as FP8 E4M3 is q * 2^-9 exactly, v_cvt_scalef32_pk_f16_fp8
+// scales it by 2^9 (the instruction takes only the exponent of its scale
+// operand, so the scale must be a power of two) and q * sc <= 945 is an
+// integer, exact in f16.
+template <bool H>
+__device__ __forceinline__ uint32_t nib_pair_sc(uint32_t v, f16x2 sch) {
+  const f16x2 q = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v, 512.f, H);
+  return __builtin_bit_cast(uint32_t, q * sch);
+}
+__device__ __forceinline__ f16x2 f16_pair(uint32_t sc) {
+  const _Float16 h = (_Float16)(float)sc;
+  return (f16x2){h, h};
+}
 // Word w of a gate/up lane chunk (positions 8v..8v+3 in the low nibbles,
-// 8v+4..8v+7 in the high ones) times the scale pair s2 = sc | sc << 16, as 8
-// f16 values sc*q in position order.
-__device__ __forceinline__ f16x8 burst_a(uint32_t w, uint32_t s2) {
+// 8v+4..8v+7 in the high ones) times the scale sc, as 8 f16 values sc*q in
+// position order.
+__device__ __forceinline__ f16x8 burst_a(uint32_t w, uint32_t sc) {
   const uint32_t lo = nib_lo(w), hi = nib_hi(w);
-  const u32x4 a = {scaled_u16(__builtin_amdgcn_perm(0u, lo, 0x0c010c00u), s2),
-                   scaled_u16(__builtin_amdgcn_perm(0u, lo, 0x0c030c02u), s2),
-                   scaled_u16(__builtin_amdgcn_perm(0u, hi, 0x0c010c00u), s2),
-                   scaled_u16(__builtin_amdgcn_perm(0u, hi, 0x0c030c02u), s2)};
+  const f16x2 sch = f16_pair(sc);
+  const u32x4 a = {nib_pair_sc<false>(lo, sch), nib_pair_sc<true>(lo, sch), nib_pair_sc<false>(hi, sch),
+                   nib_pair_sc<true>(hi, sch)};
   return __builtin_bit_cast(f16x8, a);
 }
 // v split into the f16 part of the lane's column: hi = f16(v), lo = f16(v - hi).
@@ -2341,11 +2355,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_burst_kernel(const uint
         f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(burst_a(word(C.q[s][0], v), sc0 * 0x10001u), bx[s][0][v], c, 0,
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(burst_a(word(C.q[s][0], v), sc0), bx[s][0][v], c, 0,
                                                      0, 0);
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(burst_a(word(C.q[s][1], v), sc1 * 0x10001u), bx[s][1][v], c, 0,
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(burst_a(word(C.q[s][1], v), sc1), bx[s][1][v], c, 0,
                                                      0, 0);
         cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-dmn * (float)mi0, xsm[s][0], cmin, 0, 0, 0);
         cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-dmn * (float)mi1, xsm[s][1], cmin, 0, 0, 0);
@@ -4166,7 +4180,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     if (s + 2 < nsb) load_x(s + 2, nxt);
     uint32_t sc, mi;
     q4k_scale_min(hc.y, hc.z, hc.w, 4 * p + kg, sc, mi);
-    sc *= 0x10001u;
+    const f16x2 sch = f16_pair(sc);
     if (half_bad(hc.x) || half_bad(hc.x >> 16)) bad |= kErrScale;
     const float d = half_to_float(hc.x & 0xffff);
     float drow[4];
@@ -4180,8 +4194,8 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     for (int v = 0; v < 4; ++v) {
       // Word v: low nibbles = positions 8v..8v+3, high nibbles 8v+4..8v+7.
       const uint32_t w = word(qc, v), lo = nib_lo(w), hi = nib_hi(w);
-      const u32x4 aw = {scaled_pair(lo, 0x0c010c00u, sc), scaled_pair(lo, 0x0c030c02u, sc),
-                        scaled_pair(hi, 0x0c010c00u, sc), scaled_pair(hi, 0x0c030c02u, sc)};
+      const u32x4 aw = {nib_pair_sc<false>(lo, sch), nib_pair_sc<true>(lo, sch), nib_pair_sc<false>(hi, sch),
+                        nib_pair_sc<true>(hi, sch)};
       const f16x8 a = __builtin_bit_cast(f16x8, aw);
       const uint4 bh = *reinterpret_cast<const uint4*>(xb8 + 16 * v);
       const uint4 bl = *reinterpret_cast<const uint4*>(xb8 + kTileTokens * kXhRow + 16 * v);
@@ -4597,16 +4611,16 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
     const unsigned buf = s & 1;
     if (s + 2 < nsb) load_x(s + 2, nxt);
     f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
-    uint32_t scs[2][2] = {{0u, 0u}, {0u, 0u}};
+    f16x2 scs[2][2] = {};
     if (kQ4) {
       if (half_bad(W.h.x) || half_bad(W.h.x >> 16)) bad |= kErrScale;
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
         for (int J = 0; J < 2; ++J) {
-          uint32_t mi;
-          q4k_scale_min(W.h.y, W.h.z, W.h.w, 4 * p + 2 * cc + J, scs[cc][J], mi);
-          scs[cc][J] *= 0x10001u;
+          uint32_t sc, mi;
+          q4k_scale_min(W.h.y, W.h.z, W.h.w, 4 * p + 2 * cc + J, sc, mi);
+          scs[cc][J] = f16_pair(sc);
         }
     }
 #pragma unroll
@@ -4618,8 +4632,8 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
         if (kQ4) {
           const uint32_t w0 = J ? nib_hi(W.q[cc][0].x) : nib_lo(W.q[cc][0].x);
           const uint32_t w1 = J ? nib_hi(W.q[cc][0].y) : nib_lo(W.q[cc][0].y);
-          aw = u32x4{scaled_pair(w0, 0x0c010c00u, scs[cc][J]), scaled_pair(w0, 0x0c030c02u, scs[cc][J]),
-                     scaled_pair(w1, 0x0c010c00u, scs[cc][J]), scaled_pair(w1, 0x0c030c02u, scs[cc][J])};
+          aw = u32x4{nib_pair_sc<false>(w0, scs[cc][J]), nib_pair_sc<true>(w0, scs[cc][J]),
+                     nib_pair_sc<false>(w1, scs[cc][J]), nib_pair_sc<true>(w1, scs[cc][J])};
         } else {
           const uint2 q = W.q[cc][J];
           aw = u32x4{int8_pair_f16(q.x, 0x0c010c00u), int8_pair_f16(q.x, 0x0c030c02u), int8_pair_f16(q.y, 0x0c010c00u),
