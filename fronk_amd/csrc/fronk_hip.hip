@@ -4103,10 +4103,12 @@ __device__ __forceinline__ uint32_t scaled_pair(uint32_t v, uint32_t sel, uint32
 // Workgroup (tile, slice): wavefront w takes row-block w%4 (gate rows of
 // neurons 8rb..8rb+7, then their up rows) and part w/4 (sub-blocks 0-3 or 4-7
 // of every super-block) of the TQ4_KM tiles; lane 16kg + i holds sub-block
-// 4p + kg of row i, which makes it the A operand of v_mfma_f32_16x16x32_f16
-// (row i, k = 8kg..8kg+7) for 8 positions at a time: A = sc*q, exact in f16,
-// so that each MFMA sums over 4 sub-blocks at once and the super-block is
-// scaled by d only once. B = x' in two f16 parts (two MFMAs). The min terms,
+// 4p + kg of row i, which makes it the B operand of v_mfma_f32_16x16x32_f16
+// (column i, k = 8kg..8kg+7) for 8 positions at a time: B = sc*q, exact in
+// f16, so that each MFMA sums over 4 sub-blocks at once and the super-block
+// is scaled by d only once. A = x' in two f16 parts (two MFMAs), tokens as
+// rows, so that the four results of a lane are one weight row's, scaled by
+// that row's d from the lane's own header. The min terms,
 // sum_sub dmin * m_sub * sum(x'_sub), take one fp32 MFMA per super-block; the
 // token's 2^e multiplies a and u at the end. x' moves through LDS one
 // super-block at a time, double-buffered.
@@ -4182,11 +4184,8 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     q4k_scale_min(hc.y, hc.z, hc.w, 4 * p + kg, sc, mi);
     const f16x2 sch = f16_pair(sc);
     if (half_bad(hc.x) || half_bad(hc.x >> 16)) bad |= kErrScale;
-    const float d = half_to_float(hc.x & 0xffff);
-    float drow[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) drow[r] = __shfl(d, (int)(4 * kg) + r, 64);
-    // B row of token col, part h: x' of sub-block 4p + kg at LDS
+    const float d = half_to_float(hc.x & 0xffff);   // of row col, the lane's rows of the product
+    // x' of token col, part h, sub-block 4p + kg at LDS
     // xh[buf][h][col][2 (32 (4p + kg) + 8v)].
     const uint8_t* xb8 = &L.xh[buf][0][col][64 * (4 * p + kg)];
     f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
@@ -4199,14 +4198,14 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
       const f16x8 a = __builtin_bit_cast(f16x8, aw);
       const uint4 bh = *reinterpret_cast<const uint4*>(xb8 + 16 * v);
       const uint4 bl = *reinterpret_cast<const uint4*>(xb8 + kTileTokens * kXhRow + 16 * v);
-      c_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bh), c_hi, 0, 0, 0);
-      c_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bl), c_lo, 0, 0, 0);
+      c_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bh), a, c_hi, 0, 0, 0);
+      c_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bl), a, c_lo, 0, 0, 0);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = fmaf(drow[r], c_hi[r] + c_lo[r], acc[r]);
-    // Min terms: A = -dmin * m of the lane's (row, sub-block), B = the
-    // sub-block sum of token col.
-    cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-half_to_float(hc.x >> 16) * (float)mi, L.xs[buf][col][4 * p + kg],
+    for (int r = 0; r < 4; ++r) acc[r] = fmaf(d, c_hi[r] + c_lo[r], acc[r]);
+    // Min terms: A = the sub-block sum of token col, B = -dmin * m of the
+    // lane's (sub-block, row).
+    cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(L.xs[buf][col][4 * p + kg], -half_to_float(hc.x >> 16) * (float)mi,
                                                 cmin, 0, 0, 0);
     W = load_w(s + 3);
     if (s + 1 < nsb) store_x(buf ^ 1, cur);
@@ -4220,10 +4219,13 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     if (s + 4 < nsb) step(s + 4, wb, xa, xb);
     if (s + 5 < nsb) step(s + 5, wc, xb, xa);
   }
+  // The products are [token][row] (x' is the A operand, so that a lane's
+  // four results share its row's d): lane (kg, col) holds tokens
+  // 4kg..4kg+3 of row col.
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    L.main[wave][4 * kg + r][col] = acc[r];
-    L.mins[wave][4 * kg + r][col] = cmin[r];
+    L.main[wave][col][4 * kg + r] = acc[r];
+    L.mins[wave][col][4 * kg + r] = cmin[r];
   }
   __syncthreads();
   // Thread -> (row-block, neuron i, token n): a = gate row i, u = up row 8+i,
@@ -4505,11 +4507,11 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
 // Gate/up (tile, slice): wavefront w takes row-block w%4 (the gate rows of
 // neurons 8rb..8rb+7, then their up rows) and chunks 2(w/4), 2(w/4)+1 of
 // every super-block; one v_mfma_f32_16x16x32_f16 per 32-column sub-block,
-// lane 16kg + i holding values 8kg..8kg+7 of row i: A exact in f16 (Q4_K:
-// sc*q, scaled_pair; Q8_0: q), B = x' in two f16 parts. Q4_K: the
-// super-block is scaled by d once and the min terms take one fp32 MFMA per
-// four sub-blocks, as in prefill_gate_up; Q8_0: each sub-block's product is
-// scaled by its row's d.
+// lane 16kg + i holding values 8kg..8kg+7 of row i: B exact in f16 (Q4_K:
+// sc*q, nib_pair_sc; Q8_0: q), A = x' in two f16 parts (tokens as rows, so
+// that a lane's results are its own row's). Q4_K: the super-block is scaled
+// by d once and the min terms take one fp32 MFMA per four sub-blocks, as in
+// prefill_gate_up; Q8_0: each sub-block's product is scaled by its row's d.
 __device__ __forceinline__ uint32_t int8_pair_f16(uint32_t v, uint32_t sel) {
   // Bytes of v (signed int8) as two exact f16: 1024 + 128 + q formed in the
   // bits, less 1152.
@@ -4644,30 +4646,30 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
         const uint4 bh = *reinterpret_cast<const uint4*>(xb8);
         const uint4 bl = *reinterpret_cast<const uint4*>(xb8 + kTileTokens * kXhRow);
         if (kQ4) {
-          c_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bh), c_hi, 0, 0, 0);
-          c_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bl), c_lo, 0, 0, 0);
+          c_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bh), a, c_hi, 0, 0, 0);
+          c_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bl), a, c_lo, 0, 0, 0);
         } else {
-          // The row's Q8_0 scale of this sub-block: scales of chunk 4s+2p+cc,
-          // half J; rows 4kg..4kg+3 of the product come from those lanes.
+          // The row's Q8_0 scale of this sub-block (scales of chunk 4s+2p+cc,
+          // half J): the lane's results are all of its own row.
           const uint32_t sp = cc ? W.h.y : W.h.x;
           const uint32_t hb = J ? sp >> 16 : sp & 0xffffu;
           if (half_bad(hb)) bad |= kErrScale;
           const float d = half_to_float(hb);
           const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-          const f32x4 ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bh), z, 0, 0, 0);
-          const f32x4 pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bl), z, 0, 0, 0);
+          const f32x4 ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bh), a, z, 0, 0, 0);
+          const f32x4 pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bl), a, z, 0, 0, 0);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] = fmaf(__shfl(d, (int)(4 * kg) + r, 64), ph[r] + pl[r], acc[r]);
+          for (int r = 0; r < 4; ++r) acc[r] = fmaf(d, ph[r] + pl[r], acc[r]);
         }
       }
     if (kQ4) {
       const float d = half_to_float(W.h.x & 0xffff);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = fmaf(__shfl(d, (int)(4 * kg) + r, 64), c_hi[r] + c_lo[r], acc[r]);
-      // Min terms of sub-blocks 4p..4p+3: A = -dmin * m of (row i, 4p + kg).
+      for (int r = 0; r < 4; ++r) acc[r] = fmaf(d, c_hi[r] + c_lo[r], acc[r]);
+      // Min terms of sub-blocks 4p..4p+3: B = -dmin * m of (4p + kg, row i).
       uint32_t sc, mi;
       q4k_scale_min(W.h.y, W.h.z, W.h.w, 4 * p + kg, sc, mi);
-      cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(-half_to_float(W.h.x >> 16) * (float)mi, L.xs[buf][col][4 * p + kg],
+      cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(L.xs[buf][col][4 * p + kg], -half_to_float(W.h.x >> 16) * (float)mi,
                                                   cmin, 0, 0, 0);
     }
   };
@@ -4751,10 +4753,11 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
       if (s + 5 < nsb) go(s + 5, wc, xb, xa);
     }
   }
+  // Lane (kg, col) holds tokens 4kg..4kg+3 of row col.
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    L.main[wave][4 * kg + r][col] = acc[r];
-    L.mins[wave][4 * kg + r][col] = cmin[r];
+    L.main[wave][col][4 * kg + r] = acc[r];
+    L.mins[wave][col][4 * kg + r] = cmin[r];
   }
   __syncthreads();
   {
