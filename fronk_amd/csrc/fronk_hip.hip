@@ -2132,11 +2132,13 @@ __device__ __forceinline__ _Float16 f16_part(float v, bool lo) {
 }
 // Lane mq's dword v of its quad, masked to the two nibbles at bit `shift`
 // and 16 + shift (the mask goes with the DPP read, so the move folds into
-// the AND), then shifted down: one output's two neurons as a u16 pair.
+// the AND as its source modifier: the callers keep the mask opaque so that
+// the compiler does not shift first), then shifted down: one output's two
+// neurons as a u16 pair.
 template <int MQ>
 __device__ __forceinline__ uint32_t quad_nibbles(uint32_t v, uint32_t mask, uint32_t shift) {
   constexpr int ctrl = MQ | MQ << 2 | MQ << 4 | MQ << 6;
-  return ((uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xf, 0xf, false) & mask) >> shift;
+  return ((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xf, 0xf, true) & mask) >> shift;
 }
 // One down tile (outputs 16m..16m+15 of a super-block) for every column: A
 // = sc*q of the lane's output (position q of the quad's unit) and neurons
@@ -2424,7 +2426,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_burst_kernel(const uint
       const float4 ha = *reinterpret_cast<const float4*>(&L.h[tok][8 * kg]);
       const float4 hb4 = *reinterpret_cast<const float4*>(&L.h[tok][8 * kg + 4]);
       const float hv[8] = {ha.x, ha.y, ha.z, ha.w, hb4.x, hb4.y, hb4.z, hb4.w};
-      const uint32_t shift = 4 * qq, mask = 0x000F000Fu << shift;
+      const uint32_t shift = 4 * qq;
+      uint32_t mask = 0x000F000Fu << shift;
+      asm volatile("" : "+v"(mask));   // kept as (x & mask) >> shift: the AND takes the DPP read
       float* outw = &L.out[wave][tok][4 * kg];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
@@ -4336,7 +4340,12 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
   const unsigned m = (unsigned)lane & 15, kq = (unsigned)lane >> 4, qa = m >> 2, qq = m & 3;
   const unsigned hn = (unsigned)lane & 31, hgg = (unsigned)lane >> 5;
   const uint64_t eoff = (uint64_t)T.expert * H.slice_bytes + 2 * H.proj + 4608 * (uint64_t)sb;
-  const uint32_t shift = 4 * qq, mask = 0x000F000Fu << shift;   // the lane's output column in a unit
+  const uint32_t shift = 4 * qq;   // the lane's output column in a unit
+  uint32_t mask = 0x000F000Fu << shift;
+  // Opaque to the compiler, so that (x & mask) >> shift is not rewritten as
+  // (x >> shift) & 0xF000F: the AND then takes quad_nibbles' DPP read as its
+  // source modifier.
+  asm volatile("" : "+v"(mask));
   const uint32_t vh = 4096 + 16 * hn;                            // every lane: the header of neuron l%32
   uint32_t bad = 0;
   for (unsigned ph = 0; ph < 2; ++ph) {
