@@ -147,6 +147,12 @@ __device__ __forceinline__ float half_to_float(uint32_t bits) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
 }
 __device__ __forceinline__ bool half_bad(uint32_t bits) { return (bits & 0x7c00u) == 0x7c00u; }
+// half_bad of both halves of w, as bits to OR together over a loop: bit 15
+// (31) of the result is set iff the low (high) half has the all-ones
+// exponent (e + 0x400 reaches 0x8000 only for e = 0x7c00, and the low
+// half's sum never carries into the high half).
+constexpr uint32_t kHalfBadBits = 0x80008000u;
+__device__ __forceinline__ uint32_t half_bad_bits(uint32_t w) { return (w & 0x7c007c00u) + 0x04000400u; }
 
 // 2^(e-127) for an E8M0 exponent 0..254; e = 0 is the subnormal 2^-127.
 __device__ __forceinline__ float e8m0(uint32_t e) {
@@ -4162,7 +4168,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
   };
   const uint8_t* wq = slice + 1024 + 2048 * rb + 1024 * p + 16 * (unsigned)lane;   // + 9216 s
   const uint8_t* wh = slice + 256 * rb + 16 * col;
-  uint32_t bad = 0;
+  uint32_t bad = 0, hflag = 0;   // hflag: half_bad_bits of the scale words read
   struct WStage {
     uint4 q, h;
   };
@@ -4187,11 +4193,14 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
     uint32_t sc, mi;
     q4k_scale_min(hc.y, hc.z, hc.w, 4 * p + kg, sc, mi);
     const f16x2 sch = f16_pair(sc);
-    if (half_bad(hc.x) || half_bad(hc.x >> 16)) bad |= kErrScale;
+    hflag |= half_bad_bits(hc.x);
     const float d = half_to_float(hc.x & 0xffff);   // of row col, the lane's rows of the product
     // x' of token col, part h, sub-block 4p + kg at LDS
     // xh[buf][h][col][2 (32 (4p + kg) + 8v)].
     const uint8_t* xb8 = &L.xh[buf][0][col][64 * (4 * p + kg)];
+    // The parts accumulate in tiles of their own: a lo product added to the
+    // hi sum in the matrix core loses low bits that a neuron's dot, whose
+    // main and min terms can nearly cancel, needs.
     f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -4247,6 +4256,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up(const uint8_
       S.h[(size_t)(T.slot0 + n) * (nblk * kNeurons) + kNeurons * brank + 8 * trb + i] = h;
     }
   }
+  if (hflag & kHalfBadBits) bad |= kErrScale;
   if (bad) flag(S.status, bad);
 }
 
@@ -4347,7 +4357,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
   // source modifier.
   asm volatile("" : "+v"(mask));
   const uint32_t vh = 4096 + 16 * hn;                            // every lane: the header of neuron l%32
-  uint32_t bad = 0;
+  uint32_t bad = 0, hflag = 0;   // hflag: half_bad_bits of the scale words read
   for (unsigned ph = 0; ph < 2; ++ph) {
     // Pass ph: tiles 4ph + q (outputs 128hb + 64ph + 16q .. +15 of the
     // super-block), sub-blocks g = 4hb + 2ph + gi. Lane (kq, qa, qq) loads
@@ -4367,7 +4377,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
     // the pass's sub-block l/32. Returns whether the neuron's d takes the
     // direct path.
     auto table = [&](const u32x4& hd, unsigned par) {
-      if (half_bad(hd[0]) || half_bad(hd[0] >> 16)) bad |= kErrScale;
+      hflag |= half_bad_bits(hd[0]);
       const float dn = half_to_float(hd[0] & 0xffff), dmn = half_to_float(hd[0] >> 16);
       uint32_t sc, mi;
       q4k_scale_min(hd[1], hd[2], hd[3], 4 * hb + 2 * ph + hgg, sc, mi);
@@ -4502,6 +4512,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
       }
     }
   }
+  if (hflag & kHalfBadBits) bad |= kErrScale;
   if (bad) flag(S.status, bad);
 }
 
@@ -4608,7 +4619,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
     }
     return W;
   };
-  uint32_t bad = 0;
+  uint32_t bad = 0, hflag = 0;   // hflag: half_bad_bits of the scale words read
   XStage xa = {{z4, z4}, 0.f}, xb = {{z4, z4}, 0.f};
   load_x(0, xa);
   store_x(0, xa);
@@ -4624,7 +4635,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
     f32x4 c_hi = {0.f, 0.f, 0.f, 0.f}, c_lo = {0.f, 0.f, 0.f, 0.f};
     f16x2 scs[2][2] = {};
     if (kQ4) {
-      if (half_bad(W.h.x) || half_bad(W.h.x >> 16)) bad |= kErrScale;
+      hflag |= half_bad_bits(W.h.x);
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
@@ -4662,7 +4673,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
           // half J): the lane's results are all of its own row.
           const uint32_t sp = cc ? W.h.y : W.h.x;
           const uint32_t hb = J ? sp >> 16 : sp & 0xffffu;
-          if (half_bad(hb)) bad |= kErrScale;
+          if (J == 0) hflag |= half_bad_bits(sp);   // both halves: this sub-block's scale and the next one's
           const float d = half_to_float(hb);
           const f32x4 z = {0.f, 0.f, 0.f, 0.f};
           const f32x4 ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bh), a, z, 0, 0, 0);
@@ -4782,6 +4793,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_gate_up_rows(const u
       S.h[(size_t)(T.slot0 + n) * (nblk * kNeurons) + kNeurons * brank + 8 * trb + ni] = h;
     }
   }
+  if (hflag & kHalfBadBits) bad |= kErrScale;
   if (bad) flag(S.status, bad);
 }
 
