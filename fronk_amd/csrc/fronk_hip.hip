@@ -563,24 +563,27 @@ __device__ __forceinline__ float lane_dot_f32(const LaneRaw& r, const float* sc,
   if (type == TQ4_K) {
     // Byte i of the 32-byte chunk: column i (low nibble), 32+i (high). Eight
     // independent chains (one per byte position and nibble) so that the
-    // FMAs of a wave do not wait on each other.
+    // FMAs of a wave do not wait on each other. Nibbles two per conversion
+    // as q * 2^-9 (nib_pair); the sums are those of q times 2^-9 exactly.
     float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t v = word(r.q[i >> 2], i & 3);
       const uint32_t lo = nib_lo(v), hi = nib_hi(v);
       const float4 xa = x[i], xb = x[8 + i];
-      a[0] = fmaf(ub(lo, 0), xa.x, a[0]);
-      a[1] = fmaf(ub(lo, 1), xa.y, a[1]);
-      a[2] = fmaf(ub(lo, 2), xa.z, a[2]);
-      a[3] = fmaf(ub(lo, 3), xa.w, a[3]);
-      b[0] = fmaf(ub(hi, 0), xb.x, b[0]);
-      b[1] = fmaf(ub(hi, 1), xb.y, b[1]);
-      b[2] = fmaf(ub(hi, 2), xb.z, b[2]);
-      b[3] = fmaf(ub(hi, 3), xb.w, b[3]);
+      const float2 l01 = nib_pair<false>(lo), l23 = nib_pair<true>(lo);
+      const float2 h01 = nib_pair<false>(hi), h23 = nib_pair<true>(hi);
+      a[0] = fmaf(l01.x, xa.x, a[0]);
+      a[1] = fmaf(l01.y, xa.y, a[1]);
+      a[2] = fmaf(l23.x, xa.z, a[2]);
+      a[3] = fmaf(l23.y, xa.w, a[3]);
+      b[0] = fmaf(h01.x, xb.x, b[0]);
+      b[1] = fmaf(h01.y, xb.y, b[1]);
+      b[2] = fmaf(h23.x, xb.z, b[2]);
+      b[3] = fmaf(h23.y, xb.w, b[3]);
     }
-    s0 = (a[0] + a[1]) + (a[2] + a[3]);
-    s1 = (b[0] + b[1]) + (b[2] + b[3]);
+    s0 = ((a[0] + a[1]) + (a[2] + a[3])) * kFp8Nibble;
+    s1 = ((b[0] + b[1]) + (b[2] + b[3])) * kFp8Nibble;
     return (sc[0] * s0 - mn[0] * X0) + (sc[1] * s1 - mn[1] * X1);
   }
   if (type == TQ4_0) {
@@ -593,15 +596,18 @@ __device__ __forceinline__ float lane_dot_f32(const LaneRaw& r, const float* sc,
         const uint32_t v = word(r.q[p], i);
         const uint32_t lo = nib_lo(v), hi = nib_hi(v);
         const float4 a = x[8 * p + i], b = x[8 * p + 4 + i];
-        s = fmaf(ub(lo, 0), a.x, s);
-        s = fmaf(ub(lo, 1), a.y, s);
-        s = fmaf(ub(lo, 2), a.z, s);
-        s = fmaf(ub(lo, 3), a.w, s);
-        s = fmaf(ub(hi, 0), b.x, s);
-        s = fmaf(ub(hi, 1), b.y, s);
-        s = fmaf(ub(hi, 2), b.z, s);
-        s = fmaf(ub(hi, 3), b.w, s);
+        const float2 l01 = nib_pair<false>(lo), l23 = nib_pair<true>(lo);
+        const float2 h01 = nib_pair<false>(hi), h23 = nib_pair<true>(hi);
+        s = fmaf(l01.x, a.x, s);
+        s = fmaf(l01.y, a.y, s);
+        s = fmaf(l23.x, a.z, s);
+        s = fmaf(l23.y, a.w, s);
+        s = fmaf(h01.x, b.x, s);
+        s = fmaf(h01.y, b.y, s);
+        s = fmaf(h23.x, b.z, s);
+        s = fmaf(h23.y, b.w, s);
       }
+      s *= kFp8Nibble;   // the sum of q * x (nib_pair's 2^-9 undone exactly)
       if (p) s1 = s; else s0 = s;
     }
     return sc[0] * (s0 - 8.f * X0) + sc[1] * (s1 - 8.f * X1);
