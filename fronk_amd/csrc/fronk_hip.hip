@@ -2007,8 +2007,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const uint
 //
 // Columns: token t in column 2t (hi part of its operand) and 2t+1 (lo part).
 // Gate/up, per super-block and row-block: A = sc*q, the 6-bit sub-block scale
-// times the nibble (< 1024), exactly in f16 (a packed 16-bit multiply-add
-// forms the bits of 1024 + sc*q, less 1024 in f16);
+// times the nibble (< 1024), exactly in f16 (nib_pair_sc: the nibble bytes
+// as FP8 E4M3 scaled by 2^9, then a packed f16 multiply by sc);
 // lane 16kg + i holds row i, sub-block 4p + kg, as the TQ4_KM tiles lie, so
 // one v_mfma_f32_16x16x32_f16 spans 8 positions of 4 sub-blocks and 8 of them
 // the super-block. B = x' of the column's token, x' = x*2^-e with |x'| < 2^15
@@ -4111,10 +4111,6 @@ struct GateUpLds {
   float mins[kDecodeWaves][16][kTileTokens]; // [wave][row][token] min part
 };
 
-// The same for two nibble values taken as bytes b and b+1 of v.
-__device__ __forceinline__ uint32_t scaled_pair(uint32_t v, uint32_t sel, uint32_t sc2) {
-  return scaled_u16(__builtin_amdgcn_perm(0u, v, sel), sc2);
-}
 
 // Workgroup (tile, slice): wavefront w takes row-block w%4 (gate rows of
 // neurons 8rb..8rb+7, then their up rows) and part w/4 (sub-blocks 0-3 or 4-7
