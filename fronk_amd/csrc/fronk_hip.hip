@@ -4278,9 +4278,11 @@ __device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& b1, bf16
   }
 }
 
-// Workgroup (tile, 1024 outputs): wavefront w takes the 128 outputs
-// 256 sb + 128 hb .. +127 (sb = 4 blockIdx.y + w/2, hb = w%2), eight 16-output
-// tiles, over all owned slices. With the Q4_K-T down's weight
+// Workgroup (tile, 512 outputs), four wavefronts: wavefront w takes the 128
+// outputs 256 sb + 128 hb .. +127 (sb = 2 blockIdx.y + w/2, hb = w%2), eight
+// 16-output tiles in one pass over all owned slices (B, the slice's header
+// table and the min terms formed once per slice for all eight; three
+// workgroups per CU, so that the eight accumulators fit without spills). With the Q4_K-T down's weight
 // w = d sc q - dmin m (src/native.c:14-22; per neuron n a super-block over
 // the outputs, sub-block g of 32 outputs), a slice adds
 //   sum_n d_n sc_ng q_on h'_n  -  sum_n dmin_n m_ng h'_n
@@ -4289,7 +4291,7 @@ __device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& b1, bf16
 // v_mfma_f32_16x16x32_f16 over the 32 neurons (lane group kq: neurons
 // 8kq..8kq+7):
 //   A[o][n] = sc_ng * q_on exactly in f16 (sc q < 1024), a packed 16-bit
-//     multiply-add and an f16 subtraction per two neurons;
+//     multiply-add and an f16 subtraction per two neurons (scaled_u16);
 //   B[n][t] = d_n h'_nt in two f16 parts (22 significant bits), formed once
 //     per slice for the wavefront's eight tiles;
 // and the products add straight into the tiles' accumulators over the
@@ -4300,13 +4302,17 @@ __device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& b1, bf16
 // unit has such a d) is deferred to the end and taken with B scaled down by
 // a power of two.
 constexpr float kDownDirect = 4.f;
+// prefill_down's workgroups: 4 wavefronts over 512 outputs (two super-blocks),
+// three workgroups per CU (168 registers per lane: the eight tiles' accumulators
+// and two slices of bytes in flight).
+constexpr int kDownThreads = 256, kDownWaves = kDownThreads / 64, kDownWgCols = 512;
 struct DownLds {
   float h[kBlocks][4][kTileTokens][8];   // [slice][round q][token][neuron 8q + i]: gate * h * 2^-e_t
   int e[kTileTokens];                    // e_t
-  // [wave][slice parity][sub-block of the pass][neuron]
-  uint16_t sc[kDecodeWaves][2][2][kNeurons];   // 6-bit scale
-  float mm[kDecodeWaves][2][2][kNeurons];      // dmin * m
-  float d[kDecodeWaves][2][kNeurons];          // d
+  // [wave][slice parity][sub-block 4hb + j of the wavefront][neuron]
+  uint16_t sc[kDownWaves][2][4][kNeurons];   // 6-bit scale
+  float mm[kDownWaves][2][4][kNeurons];      // dmin * m
+  float d[kDownWaves][2][kNeurons];          // d
 };
 
 // v as two f16 values hi = f16(v), lo = f16(v - hi) (v - hi is exact in fp32).
@@ -4318,17 +4324,18 @@ __device__ __forceinline__ void split_f16(const float (&v)[8], f16x8& hi, f16x8&
   }
 }
 
-__global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* __restrict__ plan, BatchScratch S) {
+__global__ __launch_bounds__(kDownThreads, 3) void prefill_down(const uint8_t* __restrict__ plan, BatchScratch S) {
   const BatchHeader& H = *reinterpret_cast<const BatchHeader*>(plan);
   const BatchTile T = reinterpret_cast<const BatchTile*>(plan + H.tiles_off)[blockIdx.x];
   const unsigned hidden = H.hidden, nsb = hidden / 256, nblk = H.nblk;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __shared__ __align__(16) DownLds L;
   const unsigned nh = nblk * kNeurons;
-  {
+#pragma unroll 1
+  for (unsigned th = 0; th < kTileTokens / (kDownThreads / 32); ++th) {
     // Thread (token n, j) takes neuron j of each slice of the token's
     // gate * h; the 32 threads of a token (one half wavefront) agree on e_t.
-    const unsigned n = (unsigned)tid >> 5, j = (unsigned)tid & 31;
+    const unsigned n = (unsigned)tid / 32 + th * (kDownThreads / 32), j = (unsigned)tid & 31;
     float v[kBlocks];
     float mx = 0.f;
 #pragma unroll
@@ -4347,7 +4354,7 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
     if (j == 0) L.e[n] = e;
   }
   __syncthreads();
-  const unsigned sb = 4 * blockIdx.y + ((unsigned)wave >> 1), hb = (unsigned)wave & 1;
+  const unsigned sb = 2 * blockIdx.y + ((unsigned)wave >> 1), hb = (unsigned)wave & 1;
   if (sb >= nsb) return;
   const unsigned m = (unsigned)lane & 15, kq = (unsigned)lane >> 4, qa = m >> 2, qq = m & 3;
   const unsigned hn = (unsigned)lane & 31, hgg = (unsigned)lane >> 5;
@@ -4360,31 +4367,36 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
   asm volatile("" : "+v"(mask));
   const uint32_t vh = 4096 + 16 * hn;                            // every lane: the header of neuron l%32
   uint32_t bad = 0, hflag = 0;   // hflag: half_bad_bits of the scale words read
-  for (unsigned ph = 0; ph < 2; ++ph) {
-    // Pass ph: tiles 4ph + q (outputs 128hb + 64ph + 16q .. +15 of the
-    // super-block), sub-blocks g = 4hb + 2ph + gi. Lane (kq, qa, qq) loads
+  {
+    // One pass over the slices for all eight tiles: tile t = 4ph + q (outputs
+    // 128hb + 64ph + 16q .. +15 of the super-block) takes sub-block
+    // g = 4hb + j, j = 2ph + q/2. Lane (kq, qa, qq) loads, for each half ph,
     // unit 32hb + 16ph + 4qq + qa of round kq: tile q of its quad reads the
-    // unit of quad lane q.
-    const uint32_t vu = 1024 * kq + 16 * (32 * hb + 16 * ph + 4 * qq + qa);
+    // unit of quad lane q. B = d h' is formed once per slice for all eight.
+    const uint32_t vu = 1024 * kq + 16 * (32 * hb + 4 * qq + qa);
     struct DnBytes {
-      u32x4 u, h;
+      u32x4 u[2], h;
     };
     auto load = [&](unsigned R, DnBytes& B) {
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           reinterpret_cast<void*>(H.base[min(R, nblk - 1)] + eoff), (short)0, 4608, 0x00020000);
-      B.u = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vu, 0, 0);
+      B.u[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vu, 0, 0);
+      B.u[1] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(vu + 256), 0, 0);
       B.h = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vh, 0, 0);
     };
     // The slice's header table (parity par): lane l decodes neuron l%32 for
-    // the pass's sub-block l/32. Returns whether the neuron's d takes the
-    // direct path.
+    // sub-blocks j = l/32 and 2 + l/32. Returns whether the neuron's d takes
+    // the direct path.
     auto table = [&](const u32x4& hd, unsigned par) {
       hflag |= half_bad_bits(hd[0]);
       const float dn = half_to_float(hd[0] & 0xffff), dmn = half_to_float(hd[0] >> 16);
-      uint32_t sc, mi;
-      q4k_scale_min(hd[1], hd[2], hd[3], 4 * hb + 2 * ph + hgg, sc, mi);
-      L.sc[wave][par][hgg][hn] = (uint16_t)sc;
-      L.mm[wave][par][hgg][hn] = dmn * (float)mi;
+      uint32_t sc0, mi0, sc1, mi1;
+      q4k_scale_min(hd[1], hd[2], hd[3], 4 * hb + hgg, sc0, mi0);
+      q4k_scale_min(hd[1], hd[2], hd[3], 4 * hb + 2 + hgg, sc1, mi1);
+      L.sc[wave][par][hgg][hn] = (uint16_t)sc0;
+      L.sc[wave][par][2 + hgg][hn] = (uint16_t)sc1;
+      L.mm[wave][par][hgg][hn] = dmn * (float)mi0;
+      L.mm[wave][par][2 + hgg][hn] = dmn * (float)mi1;
       if (hgg == 0) L.d[wave][par][hn] = dn;
       __builtin_amdgcn_wave_barrier();
       return fabsf(dn) < kDownDirect;
@@ -4403,31 +4415,51 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
       for (int j = 0; j < 8; ++j) v[j] = k ? ldexpf(hv[j] * dv[j], -k) : hv[j] * dv[j];
       split_f16(v, bh, bl);
     };
-    // A of tile MQ: the unit of quad lane MQ, the lane's column, times the
-    // sub-block's scales (u16 pairs of neurons 8kq + 2w, 8kq + 2w + 1).
-    auto a_tile = [&](const u32x4& U, unsigned par, auto mq) {
-      constexpr int MQ = decltype(mq)::value;
-      const uint4 s4 = *reinterpret_cast<const uint4*>(&L.sc[wave][par][MQ / 2][8 * kq]);
+    // A of tile 4PH + MQ: the unit of quad lane MQ in half PH, the lane's
+    // column, times sub-block 2PH + MQ/2's scales (u16 pairs of neurons
+    // 8kq + 2w, 8kq + 2w + 1).
+    auto a_tile = [&](const DnBytes& B, unsigned par, auto ph, auto mq) {
+      constexpr int PH = decltype(ph)::value, MQ = decltype(mq)::value;
+      const uint4 s4 = *reinterpret_cast<const uint4*>(&L.sc[wave][par][2 * PH + MQ / 2][8 * kq]);
+      const u32x4& U = B.u[PH];
       const u32x4 aw = {scaled_u16(quad_nibbles<MQ>(U[0], mask, shift), s4.x),
                         scaled_u16(quad_nibbles<MQ>(U[1], mask, shift), s4.y),
                         scaled_u16(quad_nibbles<MQ>(U[2], mask, shift), s4.z),
                         scaled_u16(quad_nibbles<MQ>(U[3], mask, shift), s4.w)};
       return __builtin_bit_cast(f16x8, aw);
     };
-    f32x4 acc[4];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    f32x4 acc[8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float corr[2] = {0.f, 0.f};   // [sub-block of the pass] the min terms of token m, this lane's neurons
-    uint32_t deferred = 0;        // slices with a neuron's |d| >= 4 (bit R)
+    for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float corr[4] = {0.f, 0.f, 0.f, 0.f};   // [sub-block j] the min terms of token m, this lane's neurons
+    uint32_t deferred = 0;                  // slices with a neuron's |d| >= 4 (bit R)
     auto min_terms = [&](unsigned par, const float (&hv)[8]) {
 #pragma unroll
-      for (int gi = 0; gi < 2; ++gi) {
-        const float4 m0 = *reinterpret_cast<const float4*>(&L.mm[wave][par][gi][8 * kq]);
-        const float4 m1 = *reinterpret_cast<const float4*>(&L.mm[wave][par][gi][8 * kq + 4]);
+      for (int j = 0; j < 4; ++j) {
+        const float4 m0 = *reinterpret_cast<const float4*>(&L.mm[wave][par][j][8 * kq]);
+        const float4 m1 = *reinterpret_cast<const float4*>(&L.mm[wave][par][j][8 * kq + 4]);
         const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) corr[gi] = fmaf(mv[j], hv[j], corr[gi]);
+        for (int i = 0; i < 8; ++i) corr[j] = fmaf(mv[i], hv[i], corr[j]);
       }
+    };
+    // Tiles 4PH..4PH+3 of one slice: A of each, times B (lo, then hi).
+    auto half_tiles = [&](const DnBytes& B, unsigned par, auto ph, const f16x8& bh, const f16x8& bl) {
+      constexpr int PH = decltype(ph)::value;
+      auto tile = [&](auto mq) {
+        constexpr int T = 4 * PH + decltype(mq)::value;
+        const f16x8 a = a_tile(B, par, ph, mq);
+        acc[T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc[T], 0, 0, 0);
+        acc[T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc[T], 0, 0, 0);
+      };
+      tile(I0{});
+      tile(I1{});
+      tile(I2{});
+      tile(I3{});
     };
     auto apply = [&](unsigned R, const DnBytes& B) {
       const unsigned par = R & 1;
@@ -4440,18 +4472,8 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
         deferred |= 1u << R;
         return;
       }
-      const f16x8 a0 = a_tile(B.u, par, std::integral_constant<int, 0>{});
-      const f16x8 a1 = a_tile(B.u, par, std::integral_constant<int, 1>{});
-      const f16x8 a2 = a_tile(B.u, par, std::integral_constant<int, 2>{});
-      const f16x8 a3 = a_tile(B.u, par, std::integral_constant<int, 3>{});
-      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bl, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl, acc[1], 0, 0, 0);
-      acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bl, acc[2], 0, 0, 0);
-      acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a3, bl, acc[3], 0, 0, 0);
-      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bh, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bh, acc[1], 0, 0, 0);
-      acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bh, acc[2], 0, 0, 0);
-      acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a3, bh, acc[3], 0, 0, 0);
+      half_tiles(B, par, I0{}, bh, bl);
+      half_tiles(B, par, I1{}, bh, bl);
     };
     DnBytes sa, sbb;
     load(0, sa);
@@ -4480,37 +4502,41 @@ __global__ __launch_bounds__(kBatchThreads, 4) void prefill_down(const uint8_t* 
       float hv[8];
       f16x8 bh, bl;
       b_parts(R, 0, k, hv, bh, bl);
-      const f16x8 a[4] = {a_tile(B.u, 0, std::integral_constant<int, 0>{}),
-                          a_tile(B.u, 0, std::integral_constant<int, 1>{}),
-                          a_tile(B.u, 0, std::integral_constant<int, 2>{}),
-                          a_tile(B.u, 0, std::integral_constant<int, 3>{})};
-      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      // One tile at a time (its A operand alone live).
+      auto scaled = [&](int t, const f16x8& a) {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        f32x4 pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, z, 0, 0, 0);
+        pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, pr, 0, 0, 0);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        f32x4 pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], bl, z, 0, 0, 0);
-        pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], bh, pr, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[q][r] += ldexpf(pr[r], k);
-      }
+        for (int r = 0; r < 4; ++r) acc[t][r] += ldexpf(pr[r], k);
+      };
+      scaled(0, a_tile(B, 0, I0{}, I0{}));
+      scaled(1, a_tile(B, 0, I0{}, I1{}));
+      scaled(2, a_tile(B, 0, I0{}, I2{}));
+      scaled(3, a_tile(B, 0, I0{}, I3{}));
+      scaled(4, a_tile(B, 0, I1{}, I0{}));
+      scaled(5, a_tile(B, 0, I1{}, I1{}));
+      scaled(6, a_tile(B, 0, I1{}, I2{}));
+      scaled(7, a_tile(B, 0, I1{}, I3{}));
       __builtin_amdgcn_wave_barrier();   // the table is read before the next deferred slice writes it
     }
     // The min terms of token m over all 32 neurons: sum the four lane groups.
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      corr[gi] += __shfl_xor(corr[gi], 16, 64);
-      corr[gi] += __shfl_xor(corr[gi], 32, 64);
+    for (int j = 0; j < 4; ++j) {
+      corr[j] += __shfl_xor(corr[j], 16, 64);
+      corr[j] += __shfl_xor(corr[j], 32, 64);
     }
-    // Lane l holds C rows 4(l/16) + r (outputs 128hb + 64ph + 16q + 4(l/16) + r
-    // of the super-block) of token l%16: y = (C - min terms) * 2^e_t.
+    // Lane l holds C rows 4(l/16) + r (outputs 128hb + 16t + 4(l/16) + r of
+    // the super-block) of token l%16: y = (C - min terms) * 2^e_t.
     if (m < T.ntok) {
       const int et = L.e[m];
-      float* dst = S.part + (size_t)(T.slot0 + m) * hidden + 256 * sb + 128 * hb + 64 * ph + 4 * kq;
+      float* dst = S.part + (size_t)(T.slot0 + m) * hidden + 256 * sb + 128 * hb + 4 * kq;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float c = corr[q >> 1];
-        *reinterpret_cast<float4*>(dst + 16 * q) =
-            make_float4(ldexpf(acc[q][0] - c, et), ldexpf(acc[q][1] - c, et), ldexpf(acc[q][2] - c, et),
-                        ldexpf(acc[q][3] - c, et));
+      for (int t = 0; t < 8; ++t) {
+        const float c = corr[t >> 1];
+        *reinterpret_cast<float4*>(dst + 16 * t) =
+            make_float4(ldexpf(acc[t][0] - c, et), ldexpf(acc[t][1] - c, et), ldexpf(acc[t][2] - c, et),
+                        ldexpf(acc[t][3] - c, et));
       }
     }
   }
@@ -6125,7 +6151,9 @@ int batch_launch(const uint8_t* dev_plan, const BatchHeader& H, hipStream_t stre
                        dev_plan, S, H.ntiles);
   const unsigned ncol_mx = (H.hidden + down_rows_cols<TMXFP4>() - 1) / down_rows_cols<TMXFP4>();
   const unsigned ncol_q8 = (H.hidden + down_rows_cols<TQ8_0>() - 1) / down_rows_cols<TQ8_0>();
-  if (kt) hipLaunchKernelGGL(prefill_down, dim3(H.ntiles, ncol), dim3(kBatchThreads), 0, stream, dev_plan, S);
+  if (kt)
+    hipLaunchKernelGGL(prefill_down, dim3(H.ntiles, (H.hidden + kDownWgCols - 1) / kDownWgCols), dim3(kDownThreads), 0,
+                       stream, dev_plan, S);
   else
     hipLaunchKernelGGL(prefill_down_rows<TMXFP4>, dim3(H.ntiles, ncol_mx), dim3(kBatchThreads), 0, stream, dev_plan,
                        S, 0u);
