@@ -3995,7 +3995,7 @@ __global__ void synth_kernel(uint8_t* __restrict__ dst, SliceShape routed, Slice
 //   prefill_gate_up  (tile, slice): a, u of up to 16 tokens over one slice's
 //                    32 neurons on f16 matrix cores (operands exact), then
 //                    gate*SiLU(a)*u;
-//   prefill_down     (tile, 1024 outputs): the expert's down matrix over all
+//   prefill_down     (tile, 512 outputs): the expert's down matrix over all
 //                    owned slices applied to the tile's h on f16 matrix
 //                    cores (A = sc*q exact, B = d*h in two exact parts), one
 //                    fp32 partial per (token, expert);
