@@ -94,10 +94,12 @@ def run_bursts(eng, layer, experts, gates, x):
 @pytest.mark.parametrize("hidden,tokens,blocks", [
     (4096, 40, tuple(range(20))),
     (2560, 24, (0, 7, 19)),
+    (2304, 24, (0, 5, 19)),
 ])
 def test_prefill_rows_match_oracle(eng, hidden, tokens, blocks):
     """Hot experts span several tiles, cold ones hold one token; at hidden 2560
-    the last down workgroup has idle wavefronts, and only 3 slices are owned."""
+    and 2304 only 3 slices are owned, and at 2304 (9 super-blocks) the last
+    down workgroup (512 outputs) has idle wavefronts."""
     lay = oracle.layout(hidden, fa.FMT_Q4KT)
     load(eng, hidden, blocks)
     rng = np.random.default_rng(hidden + tokens)
